@@ -1,0 +1,254 @@
+/*
+ * tmnn_hip.h -- C-ABI of the MI355X (gfx950) neural-field hot path.
+ *
+ * This library replaces the reference's Metal layers (L5 kernel generation,
+ * L6 device runtime) under tiny-metal-nn's ITrainerRuntime / FieldEvaluator /
+ * RuntimeAuthority boundary. Plain C types only: every array argument is a
+ * caller-owned pointer with an explicit element count. Host-pointer entry
+ * points copy inputs in and results out before they return (the reference's
+ * synchronous step contract); the *_device entry points take device pointers
+ * and only enqueue on the trainer's stream.
+ *
+ * Reference citations are relative to the reference checkout. Every entry
+ * point returns TMNN_OK (0) or a negative status; tmnn_last_error() returns
+ * the thread-local message of the last failure on the calling thread.
+ */
+#ifndef TMNN_HIP_H
+#define TMNN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------- */
+#define TMNN_OK 0
+#define TMNN_ERR_INVALID_ARGUMENT (-1) /* std::invalid_argument in the reference */
+#define TMNN_ERR_RUNTIME (-2)          /* std::runtime_error in the reference */
+#define TMNN_ERR_GPU (-3)              /* a HIP call failed */
+#define TMNN_ERR_UNSUPPORTED (-4)      /* geometry outside this build's kernels */
+
+/* ---- enums ------------------------------------------------------------ */
+/* Loss kinds: extension::LossKind (include/tiny-metal-nn/extension/
+ * kernel_compile_spec.h) plus RelativeL2, which the reference lacks
+ * (factory_json_detail.h:368-377). */
+#define TMNN_LOSS_L2 0
+#define TMNN_LOSS_L1 1
+#define TMNN_LOSS_HUBER 2
+#define TMNN_LOSS_COSINE 3
+#define TMNN_LOSS_RELATIVE_L2 4
+
+/* MLP arithmetic. FP32: fp32 MFMA (v_mfma_f32_16x16x4_f32), the reference's
+ * fp32 math. FP16: fp16 MFMA operands, fp32 accumulation and fp32 master
+ * parameters. Inference always runs FP32 (default_trainer.cpp:356-379). */
+#define TMNN_PRECISION_FP32 0
+#define TMNN_PRECISION_FP16 1
+
+/* Hash-table Adam: LAZY updates only entries visited by the step's batch
+ * (the reference default, adam_kernel_msl.h:120-164); DENSE updates every
+ * entry (the reference's unified kernel, adam_kernel_msl.h:37-109). */
+#define TMNN_HASH_ADAM_LAZY 0
+#define TMNN_HASH_ADAM_DENSE 1
+
+/* ---- descriptors ------------------------------------------------------ */
+
+/* Model descriptor: HashGridEncoding::Config (hash_grid.h:19-26),
+ * FullyFusedMLP::Config (fully_fused_mlp.h:18-23), TrainerConfig
+ * (trainer.h:34-61) and WeightInitConfig (weight_init.h:113-141) in one POD.
+ * Call tmnn_model_desc_init() for the reference defaults. */
+typedef struct tmnn_model_desc {
+  uint32_t struct_size;       /* sizeof(tmnn_model_desc) */
+  /* encoding */
+  int32_t spatial_dims;       /* 2 (the reference lifts to (x,y,0)), 3 or 4 */
+  int32_t num_levels;         /* 1..32 */
+  int32_t features_per_level; /* 1, 2 or 4 */
+  int32_t log2_hashmap_size;  /* 10..24 */
+  float base_resolution;
+  float per_level_scale;
+  /* network */
+  int32_t hidden_dim;         /* 1..64 in this build */
+  int32_t num_hidden_layers;  /* 1..8 */
+  int32_t num_outputs;        /* 1..16 in this build */
+  /* loss */
+  int32_t loss_kind;          /* TMNN_LOSS_* */
+  float huber_delta;
+  /* optimizer (Adam) */
+  float lr_encoding;
+  float lr_network;
+  float beta1;
+  float beta2;
+  float epsilon;
+  float l1_reg;
+  float l2_reg;
+  float grad_clip;
+  float weight_decay;
+  /* trainer */
+  int32_t batch_size;         /* steps use min(N, batch_size) points */
+  int32_t precision;          /* TMNN_PRECISION_* (training / split path) */
+  int32_t hash_adam_mode;     /* TMNN_HASH_ADAM_* */
+  int32_t morton_sort;        /* 1: sort each batch by Morton code (reference) */
+  /* weight init */
+  uint64_t seed;
+  float hash_init_range;      /* U(-r, r) for the table */
+} tmnn_model_desc;
+
+/* Result of one fused training step: TrainingStepResult (common.h:97-110). */
+typedef struct tmnn_step_result {
+  float loss;                 /* sum of per-point losses / N */
+  uint32_t step;              /* step counter after the update */
+  uint32_t batch_n;           /* points used (after the batch cap) */
+} tmnn_step_result;
+
+/* Realized kernel geometry: TrainerRuntimeInspection (trainer.h:63-87). */
+typedef struct tmnn_inspection {
+  int32_t family;             /* 0 FullyFusedMFMA (the only family here) */
+  int32_t precision;          /* TMNN_PRECISION_* of the training kernel */
+  int32_t hidden_padded;      /* MFMA tile width of the hidden layers */
+  int32_t input_padded;       /* MFMA tile width of the encoded input */
+  int32_t points_per_wave_tile;
+  int32_t waves_per_block_train;
+  int32_t blocks_train;       /* persistent blocks of the training kernel */
+  int32_t lds_bytes_train;
+  int32_t lds_bytes_infer;
+  int32_t cu_count;
+  uint32_t hash_param_count;
+  uint32_t mlp_param_count;
+  uint32_t batch_size;
+} tmnn_inspection;
+
+typedef struct tmnn_context tmnn_context;
+typedef struct tmnn_trainer tmnn_trainer;
+
+/* ---- errors ----------------------------------------------------------- */
+/* Thread-local message of the calling thread's last failure
+ * (DiagnosticInfo::message, diagnostics.h:199-245). */
+const char *tmnn_last_error(void);
+/* ABI version of this header (bumped on incompatible change). */
+uint32_t tmnn_abi_version(void);
+
+/* ---- context: MetalContext::create (metal_context.h:105-149) ------------ */
+int tmnn_context_create(int32_t device, tmnn_context **out);
+int tmnn_context_destroy(tmnn_context *ctx);
+int tmnn_context_device_info(tmnn_context *ctx, int32_t *cu_count,
+                             uint64_t *global_mem_bytes, char *name,
+                             size_t name_capacity);
+
+/* ---- model: try_create_trainer (default_trainer.cpp:2771-2818) ---------- */
+void tmnn_model_desc_init(tmnn_model_desc *desc);
+int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc,
+                        tmnn_trainer **out);
+int tmnn_trainer_destroy(tmnn_trainer *tr);
+int tmnn_trainer_param_counts(tmnn_trainer *tr, uint32_t *hash_count,
+                              uint32_t *mlp_count);
+int tmnn_trainer_inspect(tmnn_trainer *tr, tmnn_inspection *out);
+
+/* ---- compute ------------------------------------------------------------ */
+/* ITrainerRuntime::training_step (trainer.h:140-141; default_trainer.cpp:
+ * 883-1045). input [N][spatial_dims], target [N][num_outputs], host memory.
+ * Synchronous: returns after Adam, with the loss. */
+int tmnn_training_step(tmnn_trainer *tr, const float *input,
+                       const float *target, int32_t n, tmnn_step_result *out);
+
+/* Device-resident variant of training_step: input/target are device
+ * pointers; the step is only enqueued. If loss_out (device pointer) is
+ * non-null the step's loss is written there when the step executes. */
+int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input,
+                              const float *d_target, int32_t n,
+                              float *d_loss_out);
+
+/* FieldEvaluator::evaluate / Trainer::inference (evaluator.h:22-59;
+ * default_trainer.cpp:321-465): fp32, unsorted, no batch cap.
+ * positions [N][spatial_dims] -> output [N][num_outputs], host memory. */
+int tmnn_inference(tmnn_trainer *tr, const float *positions, float *output,
+                   int32_t n);
+/* Device-pointer variant; only enqueues. */
+int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions,
+                          float *d_output, int32_t n);
+
+/* ITrainerRuntime::forward_for_training (trainer.h:145-150;
+ * default_trainer.cpp:1047-1127): forward in the training precision, output
+ * in the caller's point order. *written = min(N, batch_size) * num_outputs. */
+int tmnn_forward_for_training(tmnn_trainer *tr, const float *input,
+                              float *output, int32_t n, uint32_t *written);
+
+/* ITrainerRuntime::zero_gradients / backward_accumulate / adam_step
+ * (trainer.h:160-174; default_trainer.cpp:1300-1443). */
+int tmnn_zero_gradients(tmnn_trainer *tr);
+int tmnn_backward_accumulate(tmnn_trainer *tr, const float *input,
+                             const float *d_output, int32_t n);
+int tmnn_adam_step(tmnn_trainer *tr);
+
+/* Block until all work enqueued on the trainer's stream has finished
+ * (ITrainerRuntime::sync_weights, trainer.h:182). */
+int tmnn_synchronize(tmnn_trainer *tr);
+
+/* ---- state ----------------------------------------------------------------- */
+/* ITrainerRuntime::step (trainer.h:183). */
+int tmnn_get_step(tmnn_trainer *tr, uint32_t *step);
+
+/* RuntimeAuthority::buffer(HashWeights | MlpWeights) download
+ * (runtime_authority.h:68-79). Layouts: hash [L][T][F] fp32;
+ * MLP [W0 (in x H), b0, W1, b1, ..., WO (H x M), bO] fp32. Either pointer may
+ * be null to skip; counts must match exactly. */
+int tmnn_get_weights(tmnn_trainer *tr, float *hash, size_t hash_count,
+                     float *mlp, size_t mlp_count);
+
+/* ITrainerRuntime::set_initial_weights (trainer.h:197-207;
+ * default_trainer.cpp:1555-1643): replaces weights, resets Adam and step. */
+int tmnn_set_initial_weights(tmnn_trainer *tr, const float *hash,
+                             size_t hash_count, const float *mlp,
+                             size_t mlp_count);
+
+/* OptimizerStateBlob v1 (detail/runtime_authority.h; default_trainer.cpp:
+ * 1645-1768): payload = 4 sections [u32 LE byte_len][fp32 bytes] in the
+ * order m_hash, v_hash, m_mlp, v_mlp. Export: pass payload=NULL to query
+ * *payload_len; version is always 1. */
+int tmnn_export_optimizer_state(tmnn_trainer *tr, uint32_t *version,
+                                uint32_t *step, uint8_t *payload,
+                                size_t capacity, size_t *payload_len);
+int tmnn_import_optimizer_state(tmnn_trainer *tr, uint32_t version,
+                                uint32_t step, const uint8_t *payload,
+                                size_t payload_len);
+
+/* ITrainerRuntime::reset_optimizer / apply_optimizer_config
+ * (trainer.h:208-209): zero m, v and the step; set learning rates. */
+int tmnn_reset_optimizer(tmnn_trainer *tr);
+int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding,
+                           float lr_network);
+
+/* ---- inspection hooks of the path (used by the parity tests) --------------- */
+/* Encode forward only (emitHashEncodeUnified, mlp_kernel_emitter.cpp:
+ * 205-360): features [N][L*F] fp32; corner_index / corner_weight (nullable)
+ * [N][L][2^spatial_dims] in the reference's corner order. Host memory. */
+int tmnn_debug_encode(tmnn_trainer *tr, const float *positions, int32_t n,
+                      float *features, uint32_t *corner_index,
+                      float *corner_weight);
+
+/* Accumulated gradients in reference layout: int32 fixed-point hash grads
+ * [L][T][F] (scale 65536) and fp32 MLP grads. Either pointer may be null. */
+int tmnn_debug_get_gradients(tmnn_trainer *tr, int32_t *grad_hash,
+                             size_t hash_count, float *grad_mlp,
+                             size_t mlp_count);
+
+/* Active-hash mask words (bit per entry pair when F == 2, else per float). */
+int tmnn_debug_get_active_mask(tmnn_trainer *tr, uint32_t *words,
+                               size_t word_count);
+
+/* Per-level resolution table used by every kernel (L floats). */
+int tmnn_debug_get_resolutions(tmnn_trainer *tr, float *out, int32_t count);
+
+/* The seeded Philox-4x32-10 uniform fill used for weight init
+ * (detail::context_dispatch_init_uniform, metal_context.cpp:731-982):
+ * out[count] = low + u * (high - low), counters base, base+1, ...
+ * Host output. */
+int tmnn_debug_philox_uniform(tmnn_context *ctx, uint64_t seed,
+                              uint32_t counter_base, uint32_t count, float low,
+                              float high, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMNN_HIP_H */

@@ -1,0 +1,120 @@
+"""C-ABI library checks that need no GPU: the library loads, exports every
+symbol include/tmnn_hip.h declares, and the struct layouts agree; JSON config
+canonicalization follows the reference's rules (factory_json_detail.h)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "tmnn_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tmnn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for must in ("tmnn_training_step", "tmnn_inference", "tmnn_forward_for_training",
+                 "tmnn_zero_gradients", "tmnn_backward_accumulate", "tmnn_adam_step",
+                 "tmnn_export_optimizer_state", "tmnn_import_optimizer_state",
+                 "tmnn_set_initial_weights", "tmnn_get_weights", "tmnn_last_error"):
+        assert must in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from tiny_metal_nn import _lib
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+    assert lib.tmnn_abi_version() == 1
+
+
+def test_desc_defaults_and_struct_size():
+    from tiny_metal_nn import _lib
+    d = _lib.ModelDesc()
+    _lib.load().tmnn_model_desc_init(ctypes.byref(d))
+    assert d.struct_size == ctypes.sizeof(_lib.ModelDesc)
+    # HashGridEncoding / FullyFusedMLP / TrainerConfig / WeightInitConfig defaults
+    assert (d.num_levels, d.features_per_level, d.log2_hashmap_size) == (16, 2, 19)
+    assert d.base_resolution == 16.0 and d.per_level_scale == pytest.approx(1.447)
+    assert (d.hidden_dim, d.num_hidden_layers, d.batch_size) == (64, 2, 1024)
+    assert d.lr_encoding == pytest.approx(1e-2) and d.lr_network == pytest.approx(1e-3)
+    assert d.beta1 == pytest.approx(0.9) and d.beta2 == pytest.approx(0.99)
+    assert d.epsilon == pytest.approx(1e-15) and d.seed == 42
+    assert d.hash_init_range == pytest.approx(1e-4)
+
+
+def test_null_handles_are_rejected_without_a_gpu():
+    from tiny_metal_nn import _lib
+    lib = _lib.load()
+    assert lib.tmnn_training_step(None, None, None, 4, None) == _lib.TMNN_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.tmnn_last_error()
+    assert lib.tmnn_adam_step(None) == _lib.TMNN_ERR_INVALID_ARGUMENT
+    assert lib.tmnn_trainer_destroy(None) == 0
+
+
+def test_canonicalize_defaults():
+    from tiny_metal_nn import canonicalize_model_config
+    c = canonicalize_model_config(3, 1, {})
+    assert c["encoding"] == {"otype": "HashGrid", "n_input_dims": 3, "n_levels": 16,
+                             "n_features_per_level": 2, "log2_hashmap_size": 19,
+                             "base_resolution": 16.0, "per_level_scale": 1.447,
+                             "interpolation": "Linear"}
+    assert c["network"]["n_neurons"] == 64 and c["network"]["n_hidden_layers"] == 2
+    assert c["network"]["n_input_dims"] == 32
+    assert c["loss"] == {"otype": "L2"}
+    assert c["optimizer"]["learning_rate"] == pytest.approx(1e-3)
+    assert c["batch_size"] == 1024
+
+
+@pytest.mark.parametrize("bad,frag", [
+    ({"network": {"otype": "TiledMLP"}}, "TiledMLP"),
+    ({"network": {"activation": "Tanh"}}, "ReLU"),
+    ({"loss": {"otype": "MSE"}}, "unsupported loss"),
+    ({"loss": {"otype": "Huber", "huber_delta": -1.0}}, "huber_delta"),
+    ({"loss": {"otype": "Cosine", "output_dims": 1}}, "output_dims"),
+    ({"optimizer": {"otype": "SGD"}}, "optimizer"),
+    ({"optimizer": {"learning_rate": 0.0}}, "learning_rate"),
+    ({"encoding": {"interpolation": "Nearest"}}, "Linear"),
+    ({"encoding": {"n_levels": "many"}}, "n_levels"),
+    ({"bogus": 1}, "bogus"),
+])
+def test_canonicalize_rejects(bad, frag):
+    from tiny_metal_nn import ConfigError, canonicalize_model_config
+    with pytest.raises(ConfigError, match=frag):
+        canonicalize_model_config(3, 1, bad)
+
+
+def test_canonicalize_aliases_and_extensions():
+    from tiny_metal_nn import canonicalize_model_config
+    c = canonicalize_model_config(2, 3, {
+        "encoding": {"otype": "MultiresolutionHashGrid", "n_levels": 16},
+        "network": {"output_activation": "Linear"},
+        "loss": {"otype": "RelativeL2"},
+        "mi355x": {"precision": "fp16"}})
+    assert c["encoding"]["otype"] == "HashGrid"
+    assert c["network"]["output_activation"] == "None"
+    assert c["loss"]["otype"] == "RelativeL2"
+    assert c["mi355x"]["precision"] == "fp16"
+
+
+def test_model_desc_from_config():
+    from tiny_metal_nn import _lib, canonicalize_model_config
+    from tiny_metal_nn.config import model_desc
+    c = canonicalize_model_config(2, 3, {
+        "encoding": {"n_levels": 16, "log2_hashmap_size": 15, "per_level_scale": 1.5},
+        "optimizer": {"learning_rate": 1e-2, "beta2": 0.99, "epsilon": 1e-15},
+        "loss": {"otype": "RelativeL2"}, "batch_size": 262144,
+        "mi355x": {"precision": "fp16", "hash_adam": "dense"}})
+    d = model_desc(c)
+    assert (d.spatial_dims, d.num_outputs, d.log2_hashmap_size) == (2, 3, 15)
+    assert d.lr_encoding == pytest.approx(1e-2) and d.lr_network == pytest.approx(1e-2)
+    assert d.loss_kind == _lib.LOSS_RELATIVE_L2 and d.batch_size == 262144
+    assert d.precision == _lib.PRECISION_FP16 and d.hash_adam_mode == _lib.HASH_ADAM_DENSE

@@ -1,0 +1,214 @@
+// aux_kernels.hpp -- the bandwidth-bound kernels around the fused field
+// kernel: seeded Philox init, Morton codes + batch gather, dW partial
+// reduction, the fused (lazy-hash + dense-MLP) Adam pass, loss reduction and
+// the encode-only inspection kernel.
+#pragma once
+
+#include "device_common.hpp"
+
+namespace tmnn_hip {
+
+// init_uniform_philox (metal_context.cpp:766-792): thread t writes
+// out[4t .. 4t+3] = low + u * (high - low), u = float(r) * 2^-32.
+__global__ void philox_uniform_kernel(float *out, uint32_t count, uint32_t k0,
+                                      uint32_t k1, uint32_t counter_base,
+                                      float low, float high) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t base = t * 4u;
+  if (base >= count) return;
+  uint32_t r[4];
+  philox4x32_10(counter_base + t, k0, k1, r);
+  const float kScale = 1.0f / 4294967296.0f;
+  const float span = high - low;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (base + i < count) {
+      const float u = static_cast<float>(r[i]) * kScale;
+      out[base + i] = low + u * span;
+    }
+  }
+}
+
+// Morton code per point (morton_sort.h:14-57); 2D points are lifted to
+// (x, y, 0) like the reference's callers. idx[i] = i for the sort payload.
+__global__ void morton_codes_kernel(const float *pos, int32_t n, int32_t dims,
+                                    uint32_t *codes, uint32_t *idx) {
+  const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float *p = pos + static_cast<size_t>(i) * dims;
+  uint32_t c;
+  if (dims == 4) {
+    c = (expand_bits_4d(morton_quant(p[3], 256.0f, 255.0f)) << 3) |
+        (expand_bits_4d(morton_quant(p[2], 256.0f, 255.0f)) << 2) |
+        (expand_bits_4d(morton_quant(p[1], 256.0f, 255.0f)) << 1) |
+        expand_bits_4d(morton_quant(p[0], 256.0f, 255.0f));
+  } else {
+    const float z = dims == 3 ? p[2] : 0.0f;
+    c = (expand_bits_3d(morton_quant(z, 1024.0f, 1023.0f)) << 2) |
+        (expand_bits_3d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
+        expand_bits_3d(morton_quant(p[0], 1024.0f, 1023.0f));
+  }
+  codes[i] = c;
+  idx[i] = static_cast<uint32_t>(i);
+}
+
+// dst_pos[i] = src_pos[perm[i]], dst_tgt[i] = src_tgt[perm[i]].
+__global__ void gather_rows_kernel(const float *src_pos, const float *src_tgt,
+                                   const uint32_t *perm, int32_t n,
+                                   int32_t pos_dims, int32_t tgt_dims,
+                                   float *dst_pos, float *dst_tgt) {
+  const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const size_t s = perm[i];
+  for (int d = 0; d < pos_dims; ++d)
+    dst_pos[static_cast<size_t>(i) * pos_dims + d] = src_pos[s * pos_dims + d];
+  if (src_tgt)
+    for (int d = 0; d < tgt_dims; ++d)
+      dst_tgt[static_cast<size_t>(i) * tgt_dims + d] = src_tgt[s * tgt_dims + d];
+}
+
+// grad_mlp[i] += sum over blocks b (ascending) of partials[b][i].
+__global__ void reduce_partials_kernel(const float *partials, int32_t blocks,
+                                       int32_t count, float *grad_mlp) {
+  const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  float s = 0.0f;
+  for (int32_t b = 0; b < blocks; ++b) s += partials[static_cast<size_t>(b) * count + i];
+  grad_mlp[i] = grad_mlp[i] + s;
+}
+
+struct AdamArgs {
+  float *params;            // [hash | mlp] fp32
+  float *m;
+  float *v;
+  int32_t *grad_hash;       // [hash] int32 fixed point
+  float *grad_mlp;          // [mlp]
+  uint32_t *mask;           // lazy mask words (nullable => dense hash)
+  uint32_t hash_count;
+  uint32_t mlp_count;
+  uint32_t slot_shift;      // 1 when F == 2 (entry pairs), else 0
+  float lr_hash, lr_mlp, beta1, beta2, eps, bc1, bc2;
+  float l1_hash, l2_mlp, grad_clip, weight_decay;
+  int32_t clear_grads;      // zero consumed gradients (fused step)
+  int32_t clear_mask;       // zero consumed mask words
+};
+
+// One Adam element (adam_kernel_msl.h:67-108, :137-163, :183-202).
+__device__ __forceinline__ void adam_update(float &w, float &mo, float &ve,
+                                            float g, float lr, const AdamArgs &a,
+                                            bool is_mlp) {
+  if (a.grad_clip > 0.0f) g = fminf(fmaxf(g, -a.grad_clip), a.grad_clip);
+  if (a.weight_decay > 0.0f) {
+    w = w - (lr * a.weight_decay) * w;
+  } else {
+    if (!is_mlp && a.l1_hash > 0.0f)
+      g = g + a.l1_hash * (w > 0.0f ? 1.0f : (w < 0.0f ? -1.0f : 0.0f));
+    if (is_mlp && a.l2_mlp > 0.0f) g = g + a.l2_mlp * w;
+  }
+  const float mn = a.beta1 * mo + (1.0f - a.beta1) * g;
+  const float vn = a.beta2 * ve + ((1.0f - a.beta2) * g) * g;
+  mo = mn;
+  ve = vn;
+  const float mh = mn / a.bc1;
+  const float vh = vn / a.bc2;
+  w = w - (lr * mh) / (sqrtf(vh) + a.eps);
+}
+
+// One pass over [hash | mlp]. Thread i owns element i. With a mask, hash
+// element i is updated only if its slot (i >> slot_shift) is marked: the
+// lazy sparse semantics of neural_sdf_adam_hash_sparse without the host-side
+// compaction. A mask word covers 32 slots = 32 << slot_shift consecutive
+// elements, which always lie in one 64-lane wave (blocks are multiples of 64
+// and start at multiples of 64), so every reader of a word loads it in the
+// same instruction before the word's first lane clears it.
+__global__ void adam_kernel(AdamArgs a) {
+  const uint32_t total = a.hash_count + a.mlp_count;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    if (i < a.hash_count) {
+      bool active = true;
+      if (a.mask) {
+        const uint32_t slot = i >> a.slot_shift;
+        const uint32_t word = a.mask[slot >> 5];
+        active = (word >> (slot & 31u)) & 1u;
+        if (a.clear_mask && (i & ((32u << a.slot_shift) - 1u)) == 0u && word != 0u)
+          a.mask[slot >> 5] = 0u;
+      }
+      if (!active) continue;
+      const float g = static_cast<float>(a.grad_hash[i]) * (1.0f / 65536.0f);
+      float w = a.params[i], mo = a.m[i], ve = a.v[i];
+      adam_update(w, mo, ve, g, a.lr_hash, a, false);
+      a.params[i] = w;
+      a.m[i] = mo;
+      a.v[i] = ve;
+      if (a.clear_grads) a.grad_hash[i] = 0;
+    } else {
+      const uint32_t j = i - a.hash_count;
+      float w = a.params[i], mo = a.m[i], ve = a.v[i];
+      adam_update(w, mo, ve, a.grad_mlp[j], a.lr_mlp, a, true);
+      a.params[i] = w;
+      a.m[i] = mo;
+      a.v[i] = ve;
+      if (a.clear_grads) a.grad_mlp[j] = 0.0f;
+    }
+  }
+}
+
+// loss = (sum over block partials, ascending) / N, written to *out.
+__global__ void loss_reduce_kernel(const float *partials, int32_t blocks,
+                                   float inv_count_div, int32_t n, float *out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float t = 0.0f;
+  for (int32_t b = 0; b < blocks; ++b) t += partials[b];
+  (void)inv_count_div;
+  *out = n > 0 ? t / static_cast<float>(n) : 0.0f;
+}
+
+// Encode-only inspection kernel: thread per (point, level).
+template <int D>
+__device__ void encode_debug_point(const float *table, uint32_t log2T, int F,
+                                   int L, const float *res, const float *p,
+                                   int l, float *feat_out, uint32_t *idx_out,
+                                   float *w_out) {
+  const Cell<D> c = cell_of<D>(p, res[l]);
+  const uint32_t tmask = (1u << log2T) - 1u;
+  float feat[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < (1 << D); ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const uint32_t h = hash_corner<D>(co, tmask);
+    const float w = corner_weight<D>(wc);
+    const float *e = table + ((static_cast<size_t>(l) << log2T) + h) * F;
+    for (int f = 0; f < F; ++f) feat[f] = feat[f] + w * e[f];
+    if (idx_out) idx_out[k] = h;
+    if (w_out) w_out[k] = w;
+  }
+  for (int f = 0; f < F; ++f) feat_out[f] = feat[f];
+  (void)L;
+}
+
+__global__ void encode_debug_kernel(const float *table, uint32_t log2T,
+                                    int32_t D, int32_t F, int32_t L,
+                                    const float *res_table, const float *pos,
+                                    int32_t n, float *feats, uint32_t *idx,
+                                    float *wts) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= static_cast<int64_t>(n) * L) return;
+  const int32_t i = static_cast<int32_t>(t / L);
+  const int l = static_cast<int>(t % L);
+  const int C = 1 << D;
+  float p[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < D; ++d) p[d] = pos[static_cast<size_t>(i) * D + d];
+  float *fo = feats + static_cast<size_t>(i) * L * F + l * F;
+  uint32_t *io = idx ? idx + (static_cast<size_t>(i) * L + l) * C : nullptr;
+  float *wo = wts ? wts + (static_cast<size_t>(i) * L + l) * C : nullptr;
+  if (D == 2)
+    encode_debug_point<2>(table, log2T, F, L, res_table, p, l, fo, io, wo);
+  else if (D == 3)
+    encode_debug_point<3>(table, log2T, F, L, res_table, p, l, fo, io, wo);
+  else
+    encode_debug_point<4>(table, log2T, F, L, res_table, p, l, fo, io, wo);
+}
+
+}  // namespace tmnn_hip

@@ -1,0 +1,948 @@
+// field_kernel.hpp -- the fused neural-field kernel for gfx950.
+//
+// One launch runs, per 32-point wave tile:
+//   hash-grid encode (gathers straight into MFMA B-operand registers)
+//   -> MLP forward on MFMA (weights resident in LDS as A-operand fragments)
+//   -> loss + output gradient                          [training modes]
+//   -> MLP backward on MFMA, dW reduced per block in LDS [training modes]
+//   -> input-feature gradient -> int32 fixed-point hash scatter + lazy mask
+//
+// Reference semantics (paths relative to the reference checkout):
+//   encode      mlp_kernel_emitter.cpp:205-360 (emitHashEncodeUnified)
+//   MLP fwd     mlp_kernel_emitter.cpp:362-480, :2987-3036
+//   loss        mlp_kernel_emitter.cpp:562-670 (emitLoss)
+//   MLP bwd     mlp_kernel_emitter.cpp:3055-3113
+//   hash bwd    mlp_kernel_emitter.cpp:672-901 (emitHashScatter),
+//               mask :48-71 (emit_active_hash_tracking)
+//
+// Register layout ("D layout"): within a 64-lane wave, lane = p + 16*q.
+// A 16x16 tile of activations over (unit, point) lives as one f32x4 per lane:
+// item r is unit 16*t + 4*q + r of point 16*nt + p -- exactly the output
+// layout of v_mfma_f32_16x16x{4f32,32f16}. The next layer consumes it as the
+// B operand without any data movement; the K order of each A fragment is
+// permuted to match (see stage_weights).
+#pragma once
+
+#include "device_common.hpp"
+
+namespace tmnn_hip {
+
+enum : int32_t { kModeForward = 0, kModeTrainLoss = 1, kModeTrainExtGrad = 2 };
+enum : int32_t {
+  kLossL2 = 0,
+  kLossL1 = 1,
+  kLossHuber = 2,
+  kLossCosine = 3,
+  kLossRelL2 = 4
+};
+
+constexpr int kNT = 2;             // 16-point MFMA column tiles per wave tile
+constexpr int kTilePts = 16 * kNT; // points per wave tile
+constexpr int kPS = 40;            // LDS row stride (elements) of [unit][point]
+constexpr int kMaxLayers = 9;      // up to 8 hidden layers + the output layer
+constexpr int kBlockThreads = 256;
+
+struct FieldArgs {
+  int32_t D, L, F, IN, H, NHL, M;
+  uint32_t log2T;
+  int32_t n;                // points of this launch
+  int32_t n_tiles;          // ceil(n / kTilePts)
+  int32_t waves_per_block;
+  int32_t mode;             // kMode*
+  int32_t loss_kind;        // kLoss*
+  float huber_delta;
+  float inv_n;              // fl(1/N) of the loss (emitScalarTrainKernelImpl)
+  float loss_scale;         // power of two applied to d_out in the fp16 path
+  float inv_loss_scale;
+  int32_t lift2d_mask;      // mark the lifted z=1 corners of 2D points
+  int32_t mlp_count;
+  float res[kMaxLevels];    // per-level resolution table
+  const float *pos;         // [n][D]
+  const float *target;      // [n][M] target (TrainLoss) or d_out (TrainExtGrad)
+  const float *table;       // [L][T][F] fp32
+  const float *mlp;         // fp32 master MLP params (reference layout)
+  float *out;               // [n][M] (Forward)
+  const uint32_t *out_index;// nullable: row of out[] for point i
+  int32_t *grad_hash;       // [L][T][F] int32 fixed point
+  uint32_t *mask;           // lazy-Adam mask words
+  float *grad_partials;     // [gridDim.x][mlp_count]
+  float *loss_partials;     // [gridDim.x]
+};
+
+// LDS plan of one launch, evaluated identically on host and device. All
+// per-layer offsets are closed-form in the layer index (no runtime-indexed
+// arrays, which would live in scratch memory on the device).
+struct FieldLayout {
+  int32_t INP, HP, IN, H, NHL, M, es, okt;  // okt: K width of output-layer bwd
+  int32_t bwd_base, bias_base;
+  int32_t res_off;              // LDS bytes: fp32 resolution table
+  int32_t dw_off;               // LDS bytes: fp32 dW accumulator
+  int32_t red_off;              // LDS bytes: fp32 per-wave reduction slots
+  int32_t wave_off;             // LDS bytes: first wave's activation region
+  int32_t wave_bytes;
+  int32_t xs_off, hs_off, ds_off;  // within a wave region
+  int32_t total;
+
+  // LDS bytes of the forward A fragments (W_k^T) of layer k (k == NHL: output)
+  __host__ __device__ int32_t fwd_off(int k) const {
+    if (k == 0) return 0;
+    return INP * HP * es + (k - 1) * HP * HP * es;
+  }
+  // LDS bytes of the backward A fragments (W_k) of layer k
+  __host__ __device__ int32_t bwd_off(int k) const {
+    if (k == 0) return bwd_base;
+    return bwd_base + INP * HP * es + (k - 1) * HP * HP * es;
+  }
+  // LDS bytes of the fp32 bias of layer k (padded to HP; output to 16)
+  __host__ __device__ int32_t bias_off(int k) const { return bias_base + k * HP * 4; }
+  // element offsets in the reference weight layout
+  // [W0 (IN x H), b0, (W_k (H x H), b_k)..., WO (H x M), bO]
+  __host__ __device__ int32_t w_off(int k) const {
+    return k == 0 ? 0 : IN * H + H + (k - 1) * (H * H + H);
+  }
+  __host__ __device__ int32_t b_off(int k) const {
+    return w_off(k) + (k == 0 ? IN * H : (k == NHL ? H * M : H * H));
+  }
+  __host__ __device__ int32_t mlp_count() const { return b_off(NHL) + M; }
+};
+
+__host__ __device__ inline int32_t round_up(int32_t v, int32_t m) {
+  return (v + m - 1) / m * m;
+}
+
+__host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
+                                                   int H, int NHL, int M,
+                                                   int mlp_count, bool f16,
+                                                   bool train, int wpb) {
+  FieldLayout s;
+  s.INP = INP; s.HP = HP; s.IN = IN; s.H = H; s.NHL = NHL; s.M = M;
+  s.es = f16 ? 2 : 4;
+  s.okt = f16 ? 32 : 16;
+  const int fwd_bytes = (INP * HP + (NHL - 1) * HP * HP + HP * 16) * s.es;
+  const int bwd_bytes = (INP * HP + (NHL - 1) * HP * HP + HP * s.okt) * s.es;
+  int off = fwd_bytes;
+  s.bwd_base = off;
+  if (train) off += bwd_bytes;
+  s.bias_base = off;
+  off += (NHL * HP + 16) * 4;
+  s.res_off = off;
+  off += kMaxLevels * 4;
+  s.dw_off = off;
+  if (train) off += round_up(mlp_count, 4) * 4;
+  s.red_off = off;
+  off += round_up(wpb, 4) * 4;
+  off = round_up(off, 16);
+  s.wave_off = off;
+  s.xs_off = 0;
+  s.hs_off = INP * kPS * s.es;
+  s.ds_off = s.hs_off + NHL * HP * kPS * s.es;
+  s.wave_bytes = train ? round_up(s.ds_off + HP * kPS * s.es, 16) : 0;
+  off += wpb * s.wave_bytes;
+  s.total = off;
+  return s;
+}
+
+// ---------------------------------------------------------------- helpers --
+
+__device__ __forceinline__ void wave_lds_sync() {
+  // LDS traffic of one wave executes in issue order; this only keeps the
+  // compiler from moving LDS accesses across the point where lanes start
+  // reading what other lanes of the same wave wrote.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ half8 pack8(f32x4 a, f32x4 b) {
+  half8 r;
+  r[0] = static_cast<_Float16>(a[0]);
+  r[1] = static_cast<_Float16>(a[1]);
+  r[2] = static_cast<_Float16>(a[2]);
+  r[3] = static_cast<_Float16>(a[3]);
+  r[4] = static_cast<_Float16>(b[0]);
+  r[5] = static_cast<_Float16>(b[1]);
+  r[6] = static_cast<_Float16>(b[2]);
+  r[7] = static_cast<_Float16>(b[3]);
+  return r;
+}
+
+// out[MT][nt] = A(frag) x in[KT][nt]: one dense layer over the wave tile.
+// f16: K step 32 (two 16-unit input tiles) per v_mfma_f32_16x16x32_f16.
+// f32: four v_mfma_f32_16x16x4_f32 per 16-unit input tile.
+template <bool F16, int KT, int MT>
+__device__ __forceinline__ void layer_mma(const unsigned char *frag,
+                                          const f32x4 (&in)[KT][kNT],
+                                          f32x4 (&out)[MT][kNT], int lane) {
+  if constexpr (F16) {
+    static_assert(KT % 2 == 0, "fp16 K tiles come in pairs");
+    constexpr int KS = KT / 2;
+    half8 b[KS][kNT];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = pack8(in[2 * ks][nt], in[2 * ks + 1][nt]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 acc[kNT];
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8 av =
+            *reinterpret_cast<const half8 *>(frag + ((mt * KS + ks) * 64 + lane) * 16);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[ks][nt], acc[nt], 0, 0, 0);
+      }
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 acc[kNT];
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const f32x4 av =
+            *reinterpret_cast<const f32x4 *>(frag + ((mt * KT + kt) * 64 + lane) * 16);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[r], in[kt][nt][r], acc[nt], 0, 0, 0);
+      }
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
+    }
+  }
+}
+
+// One 16x16 tile of dW^T = sum over the 32 tile points of
+// A[row0 + i][pt] * B[col0 + j][pt], both read from [unit][point] LDS arrays.
+template <bool F16>
+__device__ __forceinline__ f32x4 dw_tile(const unsigned char *A, int row0,
+                                         const unsigned char *B, int col0,
+                                         int p, int q) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (F16) {
+    const half8 av = *reinterpret_cast<const half8 *>(A + ((row0 + p) * kPS + 8 * q) * 2);
+    const half8 bv = *reinterpret_cast<const half8 *>(B + ((col0 + p) * kPS + 8 * q) * 2);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  } else {
+    const float *Af = reinterpret_cast<const float *>(A);
+    const float *Bf = reinterpret_cast<const float *>(B);
+#pragma unroll
+    for (int ks = 0; ks < kTilePts / 4; ++ks)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Af[(row0 + p) * kPS + 4 * ks + q],
+                                                 Bf[(col0 + p) * kPS + 4 * ks + q],
+                                                 acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Store a D-layout tile set to an LDS [unit][point] array.
+template <bool F16, int MT>
+__device__ __forceinline__ void store_tiles(unsigned char *dst,
+                                            const f32x4 (&t)[MT][kNT], int p,
+                                            int q) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = (16 * mt + 4 * q + r) * kPS + 16 * nt + p;
+        if constexpr (F16)
+          reinterpret_cast<_Float16 *>(dst)[idx] = static_cast<_Float16>(t[mt][nt][r]);
+        else
+          reinterpret_cast<float *>(dst)[idx] = t[mt][nt][r];
+      }
+}
+
+// delta *= [h > 0] with h read back from the stored forward activations.
+template <bool F16, int MT>
+__device__ __forceinline__ void relu_mask(f32x4 (&t)[MT][kNT],
+                                          const unsigned char *h, int p,
+                                          int q) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = (16 * mt + 4 * q + r) * kPS + 16 * nt + p;
+        float hv;
+        if constexpr (F16)
+          hv = static_cast<float>(reinterpret_cast<const _Float16 *>(h)[idx]);
+        else
+          hv = reinterpret_cast<const float *>(h)[idx];
+        t[mt][nt][r] = hv > 0.0f ? t[mt][nt][r] : 0.0f;
+      }
+}
+
+// Sum over the 16 lanes p of one q group.
+__device__ __forceinline__ float sum_over_p(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  return v;
+}
+
+// ----------------------------------------------------------- encode / hash --
+
+// Features of one level (F values), corner loop in the reference's order.
+template <int D, int F>
+__device__ __forceinline__ void encode_level(const float *table, uint32_t log2T,
+                                             int l, const float *p, float res,
+                                             float *feat) {
+  const Cell<D> c = cell_of<D>(p, res);
+  const uint32_t tmask = (1u << log2T) - 1u;
+#pragma unroll
+  for (int f = 0; f < F; ++f) feat[f] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < (1 << D); ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const uint32_t h = hash_corner<D>(co, tmask);
+    const float w = corner_weight<D>(wc);
+    const float *e = table + ((static_cast<size_t>(l) << log2T) + h) * F;
+    if constexpr (F == 1) {
+      feat[0] = feat[0] + w * e[0];
+    } else if constexpr (F == 2) {
+      const f32x2 t = *reinterpret_cast<const f32x2 *>(e);
+      feat[0] = feat[0] + w * t[0];
+      feat[1] = feat[1] + w * t[1];
+    } else {
+      const f32x4 t = *reinterpret_cast<const f32x4 *>(e);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) feat[f] = feat[f] + w * t[f];
+    }
+  }
+}
+
+// Input features fb .. fb+3 of one point (zero past L*F).
+template <int D, int F>
+__device__ __forceinline__ f32x4 encode_quad_t(const FieldArgs &a,
+                                               const float *res, int fb,
+                                               const float *p) {
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (F == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int l = fb + r;
+      if (l < a.L) {
+        float v[1];
+        encode_level<D, 1>(a.table, a.log2T, l, p, res[l], v);
+        o[r] = v[0];
+      }
+    }
+  } else if constexpr (F == 2) {
+#pragma unroll
+    for (int lv = 0; lv < 2; ++lv) {
+      const int l = fb / 2 + lv;
+      if (l < a.L) {
+        float v[2];
+        encode_level<D, 2>(a.table, a.log2T, l, p, res[l], v);
+        o[2 * lv] = v[0];
+        o[2 * lv + 1] = v[1];
+      }
+    }
+  } else {
+    const int l = fb / 4;
+    if (l < a.L) {
+      float v[4];
+      encode_level<D, 4>(a.table, a.log2T, l, p, res[l], v);
+      o = f32x4{v[0], v[1], v[2], v[3]};
+    }
+  }
+  return o;
+}
+
+// Encode every input quad of the wave tile for one (D, F): a runtime loop
+// over (kt, nt) keeps one copy of the gather code; results land in the
+// register tile through compile-time-indexed selects.
+template <int D, int F, int KT0>
+__device__ __forceinline__ void encode_tile_t(const FieldArgs &a,
+                                              const float *res, int q,
+                                              const float (&P)[kNT][4],
+                                              f32x4 (&X)[KT0][kNT]) {
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    const float pp[4] = {P[nt][0], P[nt][1], P[nt][2], P[nt][3]};
+#pragma unroll 1
+    for (int kt = 0; kt < KT0; ++kt) {
+      const f32x4 v = encode_quad_t<D, F>(a, res, 16 * kt + 4 * q, pp);
+#pragma unroll
+      for (int j = 0; j < KT0; ++j)
+        if (j == kt) X[j][nt] = v;
+    }
+  }
+}
+
+template <int KT0>
+__device__ __forceinline__ void encode_tile(const FieldArgs &a, const float *res,
+                                            int q, const float (&P)[kNT][4],
+                                            f32x4 (&X)[KT0][kNT]) {
+  switch (a.D * 8 + a.F) {
+    case 2 * 8 + 1: encode_tile_t<2, 1, KT0>(a, res, q, P, X); break;
+    case 2 * 8 + 2: encode_tile_t<2, 2, KT0>(a, res, q, P, X); break;
+    case 2 * 8 + 4: encode_tile_t<2, 4, KT0>(a, res, q, P, X); break;
+    case 3 * 8 + 1: encode_tile_t<3, 1, KT0>(a, res, q, P, X); break;
+    case 3 * 8 + 2: encode_tile_t<3, 2, KT0>(a, res, q, P, X); break;
+    case 3 * 8 + 4: encode_tile_t<3, 4, KT0>(a, res, q, P, X); break;
+    case 4 * 8 + 1: encode_tile_t<4, 1, KT0>(a, res, q, P, X); break;
+    case 4 * 8 + 2: encode_tile_t<4, 2, KT0>(a, res, q, P, X); break;
+    default: encode_tile_t<4, 4, KT0>(a, res, q, P, X); break;
+  }
+}
+
+__device__ __forceinline__ void mark_slot(uint32_t *mask, size_t slot) {
+  atomicOr(mask + (slot >> 5), 1u << static_cast<uint32_t>(slot & 31u));
+}
+
+// Gradient scatter of one level: int32((d * w) * 65536) per corner and
+// feature on the reference's float2 path (F == 2, 2D/3D), else
+// int32(d * wx * wy * wz (* wt) * 65536); every visited corner marks the
+// lazy-Adam mask (entry pairs for F == 2, single floats otherwise).
+template <int D, int F>
+__device__ __forceinline__ void scatter_level(const FieldArgs &a, int l,
+                                              const float *p, float res,
+                                              const float *d) {
+  const Cell<D> c = cell_of<D>(p, res);
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+  constexpr bool kVec2 = (F == 2 && D <= 3);
+#pragma unroll
+  for (int k = 0; k < (1 << D); ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const size_t entry = lbase + hash_corner<D>(co, tmask);
+    const float w = corner_weight<D>(wc);
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      float v;
+      if constexpr (kVec2) {
+        v = d[f] * w;
+      } else {
+        v = d[f] * wc[0];
+        v = v * wc[1];
+        if constexpr (D >= 3) v = v * wc[2];
+        if constexpr (D == 4) v = v * wc[3];
+      }
+      const int32_t ci = f2i_trunc(v * kGradScale);
+      if (ci != 0) atomicAdd(a.grad_hash + entry * F + f, ci);
+    }
+    if constexpr (F == 2) {
+      mark_slot(a.mask, entry);
+    } else {
+#pragma unroll
+      for (int f = 0; f < F; ++f) mark_slot(a.mask, entry * F + f);
+    }
+    if constexpr (D == 2) {
+      if (a.lift2d_mask) {
+        const size_t e1 = lbase + hash_corner_lift_z1(co, tmask);
+        if constexpr (F == 2) {
+          mark_slot(a.mask, e1);
+        } else {
+#pragma unroll
+          for (int f = 0; f < F; ++f) mark_slot(a.mask, e1 * F + f);
+        }
+      }
+    }
+  }
+}
+
+template <int D, int F>
+__device__ __forceinline__ void scatter_quad_t(const FieldArgs &a,
+                                               const float *res, int fb,
+                                               const float *p, f32x4 dq) {
+  if constexpr (F == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int l = fb + r;
+      if (l < a.L) {
+        const float d[1] = {dq[r]};
+        scatter_level<D, 1>(a, l, p, res[l], d);
+      }
+    }
+  } else if constexpr (F == 2) {
+#pragma unroll
+    for (int lv = 0; lv < 2; ++lv) {
+      const int l = fb / 2 + lv;
+      if (l < a.L) {
+        const float d[2] = {dq[2 * lv], dq[2 * lv + 1]};
+        scatter_level<D, 2>(a, l, p, res[l], d);
+      }
+    }
+  } else {
+    const int l = fb / 4;
+    if (l < a.L) {
+      const float d[4] = {dq[0], dq[1], dq[2], dq[3]};
+      scatter_level<D, 4>(a, l, p, res[l], d);
+    }
+  }
+}
+
+// Scatter every input-feature gradient quad of the wave tile for one (D, F).
+template <int D, int F, int KT0>
+__device__ __forceinline__ void scatter_tile_t(const FieldArgs &a,
+                                               const float *res, int q,
+                                               const float (&P)[kNT][4],
+                                               const bool (&valid)[kNT],
+                                               const f32x4 (&dx)[KT0][kNT]) {
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    if (!valid[nt]) continue;
+    const float pp[4] = {P[nt][0], P[nt][1], P[nt][2], P[nt][3]};
+#pragma unroll 1
+    for (int kt = 0; kt < KT0; ++kt) {
+      f32x4 dq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KT0; ++j)
+        if (j == kt) dq = dx[j][nt];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dq[r] = dq[r] * a.inv_loss_scale;
+      scatter_quad_t<D, F>(a, res, 16 * kt + 4 * q, pp, dq);
+    }
+  }
+}
+
+template <int KT0>
+__device__ __forceinline__ void scatter_tile(const FieldArgs &a, const float *res,
+                                             int q, const float (&P)[kNT][4],
+                                             const bool (&valid)[kNT],
+                                             const f32x4 (&dx)[KT0][kNT]) {
+  switch (a.D * 8 + a.F) {
+    case 2 * 8 + 1: scatter_tile_t<2, 1, KT0>(a, res, q, P, valid, dx); break;
+    case 2 * 8 + 2: scatter_tile_t<2, 2, KT0>(a, res, q, P, valid, dx); break;
+    case 2 * 8 + 4: scatter_tile_t<2, 4, KT0>(a, res, q, P, valid, dx); break;
+    case 3 * 8 + 1: scatter_tile_t<3, 1, KT0>(a, res, q, P, valid, dx); break;
+    case 3 * 8 + 2: scatter_tile_t<3, 2, KT0>(a, res, q, P, valid, dx); break;
+    case 3 * 8 + 4: scatter_tile_t<3, 4, KT0>(a, res, q, P, valid, dx); break;
+    case 4 * 8 + 1: scatter_tile_t<4, 1, KT0>(a, res, q, P, valid, dx); break;
+    case 4 * 8 + 2: scatter_tile_t<4, 2, KT0>(a, res, q, P, valid, dx); break;
+    default: scatter_tile_t<4, 4, KT0>(a, res, q, P, valid, dx); break;
+  }
+}
+
+// ------------------------------------------------------------ LDS staging --
+
+// K-slot order of one fp16 A fragment: slot (q, j) of K step ks covers unit
+// 32*ks + 4*q + j (j < 4) or 32*ks + 16 + 4*q + (j - 4) (j >= 4), matching
+// pack8() of two D-layout tiles.
+__device__ __forceinline__ int kslot_f16(int ks, int q, int j) {
+  return 32 * ks + (j < 4 ? 4 * q + j : 16 + 4 * q + (j - 4));
+}
+
+template <int HP, int INP, bool F16, bool TRAIN>
+__device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLayout &s,
+                              unsigned char *smem) {
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  for (int k = 0; k <= a.NHL; ++k) {
+    const int kin = k == 0 ? INP : HP;
+    const int kreal = k == 0 ? a.IN : a.H;
+    const int mout = k == a.NHL ? 16 : HP;
+    const int mreal = k == a.NHL ? a.M : a.H;
+    const float *W = a.mlp + s.w_off(k);
+    // forward: A = W_k^T, rows = output units, K = input units
+    const int nf = kin * mout;
+    for (int e = tid; e < nf; e += nthr) {
+      int i, o;
+      if constexpr (F16) {
+        const int j = e & 7, lane = (e >> 3) & 63, f = e >> 9;
+        const int ks_n = kin / 32, mt = f / ks_n, ks = f % ks_n;
+        i = kslot_f16(ks, lane >> 4, j);
+        o = 16 * mt + (lane & 15);
+      } else {
+        const int r = e & 3, lane = (e >> 2) & 63, f = e >> 8;
+        const int kt_n = kin / 16, mt = f / kt_n, kt = f % kt_n;
+        i = 16 * kt + 4 * (lane >> 4) + r;
+        o = 16 * mt + (lane & 15);
+      }
+      const float v = (i < kreal && o < mreal) ? W[i * mreal + o] : 0.0f;
+      if constexpr (F16)
+        reinterpret_cast<_Float16 *>(smem + s.fwd_off(k))[e] = static_cast<_Float16>(v);
+      else
+        reinterpret_cast<float *>(smem + s.fwd_off(k))[e] = v;
+    }
+    if constexpr (TRAIN) {
+      // backward: A = W_k, rows = input units, K = output units
+      const int ko = F16 ? round_up(mout, 32) : mout;
+      const int nb = kin * ko;
+      for (int e = tid; e < nb; e += nthr) {
+        int i, o;
+        if constexpr (F16) {
+          const int j = e & 7, lane = (e >> 3) & 63, f = e >> 9;
+          const int ks_n = ko / 32, mt = f / ks_n, ks = f % ks_n;
+          i = 16 * mt + (lane & 15);
+          o = kslot_f16(ks, lane >> 4, j);
+        } else {
+          const int r = e & 3, lane = (e >> 2) & 63, f = e >> 8;
+          const int kt_n = ko / 16, mt = f / kt_n, kt = f % kt_n;
+          i = 16 * mt + (lane & 15);
+          o = 16 * kt + 4 * (lane >> 4) + r;
+        }
+        const float v = (i < kreal && o < mreal) ? W[i * mreal + o] : 0.0f;
+        if constexpr (F16)
+          reinterpret_cast<_Float16 *>(smem + s.bwd_off(k))[e] = static_cast<_Float16>(v);
+        else
+          reinterpret_cast<float *>(smem + s.bwd_off(k))[e] = v;
+      }
+    }
+    for (int e = tid; e < mout; e += nthr)
+      reinterpret_cast<float *>(smem + s.bias_off(k))[e] =
+          e < mreal ? a.mlp[s.b_off(k) + e] : 0.0f;
+  }
+  for (int e = tid; e < kMaxLevels; e += nthr)
+    reinterpret_cast<float *>(smem + s.res_off)[e] = e < a.L ? a.res[e] : 0.0f;
+  if constexpr (TRAIN) {
+    const int nd = round_up(a.mlp_count, 4);
+    for (int e = tid; e < nd; e += nthr)
+      reinterpret_cast<float *>(smem + s.dw_off)[e] = 0.0f;
+  }
+}
+
+// ------------------------------------------------------------------ loss ----
+
+// Loss term and output gradient of one element (emitLoss, L2/L1/Huber; and
+// RelativeL2 = r^2/(y^2+0.01) with the denominator held constant).
+__device__ __forceinline__ float elem_loss(int kind, float y, float t,
+                                           float delta, float inv_n,
+                                           float *d) {
+  const float r = y - t;
+  switch (kind) {
+    case kLossL1:
+      *d = (r > 0.0f ? 1.0f : (r < 0.0f ? -1.0f : 0.0f)) * inv_n;
+      return fabsf(r);
+    case kLossHuber: {
+      const float ar = fabsf(r);
+      if (ar <= delta) {
+        *d = r * inv_n;
+        return (0.5f * r) * r;
+      }
+      *d = (delta * (r > 0.0f ? 1.0f : -1.0f)) * inv_n;
+      return delta * (ar - 0.5f * delta);
+    }
+    case kLossRelL2: {
+      const float den = y * y + 0.01f;
+      *d = ((2.0f * r) / den) * inv_n;
+      return (r * r) / den;
+    }
+    default:
+      *d = (2.0f * r) * inv_n;
+      return r * r;
+  }
+}
+
+// ---------------------------------------------------------------- kernel ----
+
+template <int HP, int INP, bool F16, bool TRAIN>
+__device__ __forceinline__ void field_body(const FieldArgs &a) {
+  constexpr int HT = HP / 16;
+  constexpr int KT0 = INP / 16;
+  constexpr int OKT = F16 ? 2 : 1;  // K tiles of the output-layer backward
+  constexpr int es = F16 ? 2 : 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const FieldLayout s = make_layout(INP, HP, a.IN, a.H, a.NHL, a.M,
+                                    a.mlp_count, F16, TRAIN, a.waves_per_block);
+  stage_weights<HP, INP, F16, TRAIN>(a, s, smem);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int p = lane & 15;
+  const int q = lane >> 4;
+  const float *res = reinterpret_cast<const float *>(smem + s.res_off);
+  float *dw = reinterpret_cast<float *>(smem + s.dw_off);
+  unsigned char *wb = smem + s.wave_off + wave * s.wave_bytes;
+  unsigned char *Xs = wb + s.xs_off;
+  unsigned char *Hs = wb + s.hs_off;
+  unsigned char *Ds = wb + s.ds_off;
+  const int hs_layer_bytes = HP * kPS * es;
+  float lane_loss = 0.0f;
+
+  for (int tile = blockIdx.x * a.waves_per_block + wave; tile < a.n_tiles;
+       tile += gridDim.x * a.waves_per_block) {
+    int pt[kNT];
+    bool valid[kNT];
+    float P[kNT][4];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      pt[nt] = tile * kTilePts + 16 * nt + p;
+      valid[nt] = pt[nt] < a.n;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        P[nt][d] = (valid[nt] && d < a.D) ? a.pos[static_cast<size_t>(pt[nt]) * a.D + d] : 0.0f;
+    }
+
+    // ---- encode: input features 16*kt + 4*q + r of point 16*nt + p
+    f32x4 X[KT0][kNT];
+    encode_tile<KT0>(a, res, q, P, X);
+    if constexpr (TRAIN) store_tiles<F16, KT0>(Xs, X, p, q);
+
+    // ---- MLP forward
+    f32x4 act[HT][kNT];
+    layer_mma<F16, KT0, HT>(smem + s.fwd_off(0), X, act, lane);
+    for (int k = 0; k < a.NHL; ++k) {
+      if (k > 0) {
+        f32x4 nxt[HT][kNT];
+        layer_mma<F16, HT, HT>(smem + s.fwd_off(k), act, nxt, lane);
+#pragma unroll
+        for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) act[mt][nt] = nxt[mt][nt];
+      }
+      const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(k));
+#pragma unroll
+      for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float v = act[mt][nt][r] + bias[16 * mt + 4 * q + r];
+            act[mt][nt][r] = v > 0.0f ? v : 0.0f;
+          }
+      if constexpr (TRAIN) store_tiles<F16, HT>(Hs + k * hs_layer_bytes, act, p, q);
+    }
+    f32x4 y[1][kNT];
+    layer_mma<F16, HT, 1>(smem + s.fwd_off(a.NHL), act, y, lane);
+    {
+      const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(a.NHL));
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[0][nt][r] = y[0][nt][r] + bias[4 * q + r];
+    }
+
+    if constexpr (!TRAIN) {
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        if (!valid[nt]) continue;
+        const size_t row = a.out_index ? a.out_index[pt[nt]] : static_cast<size_t>(pt[nt]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 4 * q + r;
+          if (o < a.M) a.out[row * a.M + o] = y[0][nt][r];
+        }
+      }
+      continue;
+    } else {
+      // ---- loss / output gradient (D layout: output 4*q + r of point 16*nt + p)
+      f32x4 g[OKT][kNT];
+#pragma unroll
+      for (int t = 0; t < OKT; ++t)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) g[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (a.mode == kModeTrainExtGrad) {
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 4 * q + r;
+            if (valid[nt] && o < a.M)
+              g[0][nt][r] = a.target[static_cast<size_t>(pt[nt]) * a.M + o] * a.loss_scale;
+          }
+      } else if (a.loss_kind == kLossCosine) {
+        // emitLoss cosine branch (mlp_kernel_emitter.cpp:643-662)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+          float tv[4];
+          float dot = 0.0f, pn = 0.0f, tn = 0.0f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 4 * q + r;
+            const bool ok = valid[nt] && o < a.M;
+            tv[r] = ok ? a.target[static_cast<size_t>(pt[nt]) * a.M + o] : 0.0f;
+            const float yv = ok ? y[0][nt][r] : 0.0f;
+            dot = dot + yv * tv[r];
+            pn = pn + yv * yv;
+            tn = tn + tv[r] * tv[r];
+          }
+          dot += __shfl_xor(dot, 16);
+          dot += __shfl_xor(dot, 32);
+          pn += __shfl_xor(pn, 16);
+          pn += __shfl_xor(pn, 32);
+          tn += __shfl_xor(tn, 16);
+          tn += __shfl_xor(tn, 32);
+          const float pnorm = sqrtf(pn + 1e-8f);
+          const float tnorm = sqrtf(tn + 1e-8f);
+          const float denom = pnorm * tnorm;
+          const float cosine = dot / denom;
+          const float pdenom = pn + 1e-8f;
+          if (valid[nt]) {
+            if (q == 0) lane_loss += 1.0f - cosine;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int o = 4 * q + r;
+              if (o < a.M) {
+                const float t1 = (cosine * y[0][nt][r]) / pdenom;
+                const float t2 = tv[r] / denom;
+                g[0][nt][r] = ((t1 - t2) * a.inv_n) * a.loss_scale;
+              }
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 4 * q + r;
+            if (valid[nt] && o < a.M) {
+              float d;
+              lane_loss += elem_loss(a.loss_kind, y[0][nt][r],
+                                     a.target[static_cast<size_t>(pt[nt]) * a.M + o],
+                                     a.huber_delta, a.inv_n, &d);
+              g[0][nt][r] = d * a.loss_scale;
+            }
+          }
+      }
+
+      // ---- output layer backward
+      wave_lds_sync();
+      {
+        f32x4 g0[1][kNT];
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) g0[0][nt] = g[0][nt];
+        store_tiles<F16, 1>(Ds, g0, p, q);
+      }
+      wave_lds_sync();
+      const int last = a.NHL - 1;
+      {
+        const unsigned char *Hl = Hs + last * hs_layer_bytes;
+        const int wo = s.w_off(a.NHL), bo = s.b_off(a.NHL);
+#pragma unroll
+        for (int ut = 0; ut < HT; ++ut) {
+          const f32x4 acc = dw_tile<F16>(Ds, 0, Hl, 16 * ut, p, q);
+          const int u = 16 * ut + p;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 4 * q + r;
+            if (o < a.M && u < a.H) atomicAdd(dw + wo + u * a.M + o, acc[r] * a.inv_loss_scale);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float sv = 0.0f;
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) sv += g[0][nt][r];
+          sv = sum_over_p(sv);
+          const int o = 4 * q + r;
+          if (p == 0 && o < a.M) atomicAdd(dw + bo + o, sv * a.inv_loss_scale);
+        }
+      }
+      f32x4 dl[HT][kNT];
+      layer_mma<F16, OKT, HT>(smem + s.bwd_off(a.NHL), g, dl, lane);
+      relu_mask<F16, HT>(dl, Hs + last * hs_layer_bytes, p, q);
+
+      // ---- hidden layers nhl-1 .. 1
+      for (int k = a.NHL - 1; k >= 1; --k) {
+        wave_lds_sync();
+        store_tiles<F16, HT>(Ds, dl, p, q);
+        wave_lds_sync();
+        const unsigned char *Hin = Hs + (k - 1) * hs_layer_bytes;
+        const int wk = s.w_off(k), bk = s.b_off(k);
+#pragma unroll
+        for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+          for (int it = 0; it < HT; ++it) {
+            const f32x4 acc = dw_tile<F16>(Ds, 16 * mt, Hin, 16 * it, p, q);
+            const int i = 16 * it + p;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int u = 16 * mt + 4 * q + r;
+              if (u < a.H && i < a.H) atomicAdd(dw + wk + i * a.H + u, acc[r] * a.inv_loss_scale);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float sv = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) sv += dl[mt][nt][r];
+            sv = sum_over_p(sv);
+            const int u = 16 * mt + 4 * q + r;
+            if (p == 0 && u < a.H) atomicAdd(dw + bk + u, sv * a.inv_loss_scale);
+          }
+        }
+        f32x4 nd[HT][kNT];
+        layer_mma<F16, HT, HT>(smem + s.bwd_off(k), dl, nd, lane);
+        relu_mask<F16, HT>(nd, Hin, p, q);
+#pragma unroll
+        for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) dl[mt][nt] = nd[mt][nt];
+      }
+
+      // ---- layer 0: dW0, db0, input-feature gradient, hash scatter
+      wave_lds_sync();
+      store_tiles<F16, HT>(Ds, dl, p, q);
+      wave_lds_sync();
+      {
+        const int w0 = s.w_off(0), b0 = s.b_off(0);
+#pragma unroll
+        for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+          for (int ft = 0; ft < KT0; ++ft) {
+            const f32x4 acc = dw_tile<F16>(Ds, 16 * mt, Xs, 16 * ft, p, q);
+            const int f = 16 * ft + p;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int u = 16 * mt + 4 * q + r;
+              if (u < a.H && f < a.IN) atomicAdd(dw + w0 + f * a.H + u, acc[r] * a.inv_loss_scale);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float sv = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) sv += dl[mt][nt][r];
+            sv = sum_over_p(sv);
+            const int u = 16 * mt + 4 * q + r;
+            if (p == 0 && u < a.H) atomicAdd(dw + b0 + u, sv * a.inv_loss_scale);
+          }
+        }
+      }
+      f32x4 dx[KT0][kNT];
+      layer_mma<F16, HT, KT0>(smem + s.bwd_off(0), dl, dx, lane);
+      scatter_tile<KT0>(a, res, q, P, valid, dx);
+    }
+  }
+
+  if constexpr (TRAIN) {
+    float v = lane_loss;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+    float *red = reinterpret_cast<float *>(smem + s.red_off);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.0f;
+      for (int w = 0; w < a.waves_per_block; ++w) t += red[w];
+      a.loss_partials[blockIdx.x] = t;
+    }
+    float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+    for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = dw[e];
+  }
+}
+
+// Training launches are LDS-bound to one 4-wave block per CU (one wave per
+// SIMD), so they may use the whole register file.
+template <int HP, int INP, bool F16>
+__global__ void __launch_bounds__(kBlockThreads)
+    __attribute__((amdgpu_waves_per_eu(1, 1))) field_train_kernel(FieldArgs a) {
+  field_body<HP, INP, F16, true>(a);
+}
+
+template <int HP, int INP, bool F16>
+__global__ void __launch_bounds__(kBlockThreads) field_forward_kernel(FieldArgs a) {
+  field_body<HP, INP, F16, false>(a);
+}
+
+}  // namespace tmnn_hip

@@ -1,0 +1,1042 @@
+// tmnn_hip.hip -- host side of the C-ABI (include/tmnn_hip.h): context,
+// trainer state in a hipMalloc arena, step sequencing and kernel launches.
+//
+// Step sequencing follows DefaultRuntime (src/tiny_metal_nn/runtime/
+// default_trainer.cpp:883-1045 and training_step_execution.cpp:887-1324):
+//   batch cap -> Morton sort -> fused forward/backward -> loss -> Adam
+//   (lazy hash + dense MLP) -> gradients and mask cleared -> step + 1.
+// Everything after the input copy runs on the trainer's HIP stream with no
+// host round trip; the host waits once, for the loss.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/tmnn_hip.h"
+#include "aux_kernels.hpp"
+#include "field_kernel.hpp"
+#include "sort.hpp"
+
+using namespace tmnn_hip;
+
+namespace {
+
+constexpr uint32_t kAbiVersion = 1u;
+constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950 LDS per CU
+constexpr uint32_t kOptimizerBlobVersion = 1u;  // detail/checkpoint_contract.h:14
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+#define TMNN_HIP_TRY(expr)                                                   \
+  do {                                                                       \
+    hipError_t e_ = (expr);                                                  \
+    if (e_ != hipSuccess)                                                    \
+      return fail(TMNN_ERR_GPU, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+// "%.6f" baked constants (mlp_kernel_emitter.cpp:91-92), read back as float.
+float baked6(float v) {
+  char buf[64];
+  std::snprintf(buf, sizeof buf, "%.6f", static_cast<double>(v));
+  return std::strtof(buf, nullptr);
+}
+
+using FieldKernel = void (*)(FieldArgs);
+
+template <int HP, int INP, bool F16, bool TRAIN>
+FieldKernel kernel_ptr() {
+  if constexpr (TRAIN)
+    return field_train_kernel<HP, INP, F16>;
+  else
+    return field_forward_kernel<HP, INP, F16>;
+}
+
+FieldKernel select_kernel(int HP, int INP, bool f16, bool train) {
+#define TMNN_SEL(hp, inp)                                                   \
+  if (HP == hp && INP == inp) {                                             \
+    if (f16) return train ? kernel_ptr<hp, inp, true, true>() : kernel_ptr<hp, inp, true, false>(); \
+    return train ? kernel_ptr<hp, inp, false, true>() : kernel_ptr<hp, inp, false, false>(); \
+  }
+  TMNN_SEL(32, 32)
+  TMNN_SEL(32, 64)
+  TMNN_SEL(64, 32)
+  TMNN_SEL(64, 64)
+#undef TMNN_SEL
+  return nullptr;
+}
+
+struct DevBuf {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  ~DevBuf() {
+    if (ptr) (void)hipFree(ptr);
+  }
+  hipError_t ensure(size_t want) {
+    if (want <= bytes) return hipSuccess;
+    if (ptr) {
+      (void)hipFree(ptr);
+      ptr = nullptr;
+      bytes = 0;
+    }
+    const size_t rounded = (want + 255) / 256 * 256;
+    hipError_t e = hipMalloc(&ptr, rounded);
+    if (e == hipSuccess) bytes = rounded;
+    return e;
+  }
+  template <class T>
+  T *as() const {
+    return static_cast<T *>(ptr);
+  }
+};
+
+struct KernelPlan {
+  FieldKernel fn = nullptr;
+  int wpb = 0;          // waves per block
+  int lds = 0;          // dynamic LDS bytes
+  int max_blocks = 0;   // resident blocks on the whole device
+};
+
+}  // namespace
+
+struct tmnn_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int cu_count = 0;
+  uint64_t mem_bytes = 0;
+  std::string name;
+};
+
+struct tmnn_trainer {
+  tmnn_context *ctx = nullptr;
+  tmnn_model_desc d{};
+  int IN = 0, INP = 0, HP = 0;
+  uint32_t hash_count = 0, mlp_count = 0, mask_words = 0;
+  float res[kMaxLevels] = {};
+  uint32_t step = 0;
+  float lr_enc = 0.f, lr_net = 0.f;
+
+  DevBuf params, m, v, grad_hash, grad_mlp, mask;
+  DevBuf partials, loss_partials, loss_out;
+  DevBuf in_pos, in_tgt, s_pos, s_tgt, keys0, keys1, vals0, vals1, sort_tmp, out_buf;
+  DevBuf dbg_a, dbg_b, dbg_c;
+
+  KernelPlan train_plan, fwd_plan, infer_plan;
+};
+
+namespace {
+
+bool desc_ok(const tmnn_model_desc *d, std::string &why) {
+  auto bad = [&](const char *m) {
+    why = m;
+    return false;
+  };
+  if (d->spatial_dims < 2 || d->spatial_dims > 4) return bad("spatial_dims must be 2, 3 or 4");
+  if (d->num_levels < 1 || d->num_levels > 32) return bad("num_levels must be in [1, 32]");
+  if (d->features_per_level != 1 && d->features_per_level != 2 && d->features_per_level != 4)
+    return bad("features_per_level must be 1, 2, or 4");
+  if (d->log2_hashmap_size < 10 || d->log2_hashmap_size > 24)
+    return bad("log2_hashmap_size must be in [10, 24]");
+  if (!(d->base_resolution > 0.f)) return bad("base_resolution must be > 0");
+  if (!(d->per_level_scale > 0.f)) return bad("per_level_scale must be > 0");
+  if (d->hidden_dim < 1 || d->hidden_dim > 512) return bad("hidden_dim must be in (0, 512]");
+  if (d->num_hidden_layers < 1 || d->num_hidden_layers > 8)
+    return bad("num_hidden_layers must be in [1, 8]");
+  if (d->num_outputs < 1) return bad("num_outputs must be >= 1");
+  if (d->loss_kind < TMNN_LOSS_L2 || d->loss_kind > TMNN_LOSS_RELATIVE_L2)
+    return bad("invalid loss kind");
+  if (d->loss_kind == TMNN_LOSS_HUBER && !(d->huber_delta > 0.f))
+    return bad("Huber loss requires huber_delta > 0");
+  if (d->loss_kind == TMNN_LOSS_COSINE && d->num_outputs < 2)
+    return bad("Cosine loss requires num_outputs >= 2");
+  if (d->batch_size < 1) return bad("batch_size must be >= 1");
+  if (d->precision != TMNN_PRECISION_FP32 && d->precision != TMNN_PRECISION_FP16)
+    return bad("invalid precision");
+  if (d->hash_adam_mode != TMNN_HASH_ADAM_LAZY && d->hash_adam_mode != TMNN_HASH_ADAM_DENSE)
+    return bad("invalid hash_adam_mode");
+  return true;
+}
+
+int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
+  out.fn = select_kernel(tr->HP, tr->INP, f16, train);
+  if (!out.fn) return fail(TMNN_ERR_UNSUPPORTED, "no kernel for this geometry");
+  int wpb = 4;
+  for (; wpb >= 1; --wpb) {
+    const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
+                                      tr->d.num_hidden_layers, tr->d.num_outputs,
+                                      static_cast<int>(tr->mlp_count), f16, train, wpb);
+    if (s.total <= kMaxLdsBytes) {
+      out.lds = s.total;
+      break;
+    }
+  }
+  if (wpb < 1) return fail(TMNN_ERR_UNSUPPORTED, "model does not fit in LDS");
+  out.wpb = wpb;
+  TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   out.lds));
+  int per_cu = 0;
+  TMNN_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &per_cu, reinterpret_cast<const void *>(out.fn), 64 * wpb, out.lds));
+  if (per_cu < 1) return fail(TMNN_ERR_UNSUPPORTED, "field kernel cannot be resident");
+  out.max_blocks = per_cu * tr->ctx->cu_count;
+  return TMNN_OK;
+}
+
+FieldArgs base_args(const tmnn_trainer *tr) {
+  FieldArgs a{};
+  a.D = tr->d.spatial_dims;
+  a.L = tr->d.num_levels;
+  a.F = tr->d.features_per_level;
+  a.IN = tr->IN;
+  a.H = tr->d.hidden_dim;
+  a.NHL = tr->d.num_hidden_layers;
+  a.M = tr->d.num_outputs;
+  a.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
+  a.loss_kind = tr->d.loss_kind;
+  a.huber_delta = baked6(tr->d.huber_delta);
+  a.loss_scale = 1.0f;
+  a.inv_loss_scale = 1.0f;
+  a.lift2d_mask = tr->d.spatial_dims == 2 ? 1 : 0;
+  a.mlp_count = static_cast<int32_t>(tr->mlp_count);
+  for (int l = 0; l < kMaxLevels; ++l) a.res[l] = tr->res[l];
+  a.table = tr->params.as<float>();
+  a.mlp = tr->params.as<float>() + tr->hash_count;
+  a.grad_hash = tr->grad_hash.as<int32_t>();
+  a.mask = tr->mask.as<uint32_t>();
+  return a;
+}
+
+int launch_field(tmnn_trainer *tr, const KernelPlan &plan, FieldArgs a, int n) {
+  a.n = n;
+  a.n_tiles = (n + kTilePts - 1) / kTilePts;
+  a.waves_per_block = plan.wpb;
+  const int need = (a.n_tiles + plan.wpb - 1) / plan.wpb;
+  const int blocks = std::max(1, std::min(need, plan.max_blocks));
+  hipLaunchKernelGGL(plan.fn, dim3(blocks), dim3(64 * plan.wpb), plan.lds,
+                     tr->ctx->stream, a);
+  TMNN_HIP_TRY(hipGetLastError());
+  return blocks;
+}
+
+// Power-of-two loss scale for the fp16 backward: d_out carries 1/N, which
+// puts it in fp16's subnormal range at large N; scaling by ~N keeps the
+// backward operands normal and the rescale exact.
+float loss_scale_for(int n, bool f16) {
+  if (!f16 || n <= 1) return 1.0f;
+  int e = 0;
+  std::frexp(static_cast<float>(n), &e);
+  return std::ldexp(1.0f, std::min(e, 24));
+}
+
+int ensure_batch(tmnn_trainer *tr, int n) {
+  const size_t D = tr->d.spatial_dims, M = tr->d.num_outputs;
+  TMNN_HIP_TRY(tr->in_pos.ensure(n * D * sizeof(float)));
+  TMNN_HIP_TRY(tr->in_tgt.ensure(n * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->s_pos.ensure(n * D * sizeof(float)));
+  TMNN_HIP_TRY(tr->s_tgt.ensure(n * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->keys0.ensure(n * sizeof(uint32_t)));
+  TMNN_HIP_TRY(tr->keys1.ensure(n * sizeof(uint32_t)));
+  TMNN_HIP_TRY(tr->vals0.ensure(n * sizeof(uint32_t)));
+  TMNN_HIP_TRY(tr->vals1.ensure(n * sizeof(uint32_t)));
+  size_t tmp = 0;
+  TMNN_HIP_TRY(morton_sort_temp_bytes(n, &tmp));
+  TMNN_HIP_TRY(tr->sort_tmp.ensure(std::max<size_t>(tmp, 256)));
+  return TMNN_OK;
+}
+
+// Sorted copies of (pos, tgt) into s_pos / s_tgt; returns the permutation
+// (sorted i -> original row) or nullptr when sorting is off.
+int sort_batch(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
+               int tgt_dims, int n, const float **pos_out,
+               const float **tgt_out, const uint32_t **perm_out) {
+  hipStream_t st = tr->ctx->stream;
+  if (!tr->d.morton_sort || n <= 1) {
+    *pos_out = d_pos;
+    *tgt_out = d_tgt;
+    *perm_out = nullptr;
+    return TMNN_OK;
+  }
+  const int threads = 256, blocks = (n + threads - 1) / threads;
+  hipLaunchKernelGGL(morton_codes_kernel, dim3(blocks), dim3(threads), 0, st, d_pos, n,
+                     tr->d.spatial_dims, tr->keys0.as<uint32_t>(), tr->vals0.as<uint32_t>());
+  TMNN_HIP_TRY(hipGetLastError());
+  const int end_bit = tr->d.spatial_dims == 4 ? 32 : 30;
+  size_t tmp = tr->sort_tmp.bytes;
+  TMNN_HIP_TRY(morton_sort_pairs(tr->sort_tmp.ptr, tmp, tr->keys0.as<uint32_t>(),
+                                 tr->keys1.as<uint32_t>(), tr->vals0.as<uint32_t>(),
+                                 tr->vals1.as<uint32_t>(), n, end_bit, st));
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks), dim3(threads), 0, st, d_pos, d_tgt,
+                     tr->vals1.as<uint32_t>(), n, tr->d.spatial_dims, tgt_dims,
+                     tr->s_pos.as<float>(), d_tgt ? tr->s_tgt.as<float>() : nullptr);
+  TMNN_HIP_TRY(hipGetLastError());
+  *pos_out = tr->s_pos.as<float>();
+  *tgt_out = d_tgt ? tr->s_tgt.as<float>() : nullptr;
+  *perm_out = tr->vals1.as<uint32_t>();
+  return TMNN_OK;
+}
+
+// Fused forward/backward over n device-resident points, gradients
+// accumulated into grad_hash / grad_mlp / mask. Returns the block count used
+// (for the loss reduction) or a negative status.
+int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
+                         int n, bool external_grad) {
+  const bool f16 = tr->d.precision == TMNN_PRECISION_FP16;
+  const float *pos = d_pos, *tgt = d_tgt;
+  const uint32_t *perm = nullptr;
+  int rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm);
+  if (rc != TMNN_OK) return rc;
+  FieldArgs a = base_args(tr);
+  a.mode = external_grad ? kModeTrainExtGrad : kModeTrainLoss;
+  a.inv_n = 1.0f / static_cast<float>(n);
+  a.loss_scale = loss_scale_for(n, f16);
+  a.inv_loss_scale = 1.0f / a.loss_scale;
+  a.pos = pos;
+  a.target = tgt;
+  a.grad_partials = tr->partials.as<float>();
+  a.loss_partials = tr->loss_partials.as<float>();
+  const int blocks = launch_field(tr, tr->train_plan, a, n);
+  if (blocks < 0) return blocks;
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + 255) / 256), dim3(256), 0,
+                     tr->ctx->stream, tr->partials.as<float>(), blocks,
+                     static_cast<int32_t>(tr->mlp_count), tr->grad_mlp.as<float>());
+  TMNN_HIP_TRY(hipGetLastError());
+  return blocks;
+}
+
+int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
+  AdamArgs a{};
+  a.params = tr->params.as<float>();
+  a.m = tr->m.as<float>();
+  a.v = tr->v.as<float>();
+  a.grad_hash = tr->grad_hash.as<int32_t>();
+  a.grad_mlp = tr->grad_mlp.as<float>();
+  // Sparse hash Adam needs l1_reg == 0 (default_trainer.cpp:1868-1876).
+  const bool lazy = tr->d.hash_adam_mode == TMNN_HASH_ADAM_LAZY && tr->d.l1_reg == 0.0f;
+  a.mask = lazy ? tr->mask.as<uint32_t>() : nullptr;
+  a.hash_count = tr->hash_count;
+  a.mlp_count = tr->mlp_count;
+  a.slot_shift = tr->d.features_per_level == 2 ? 1u : 0u;
+  a.lr_hash = tr->lr_enc;
+  a.lr_mlp = tr->lr_net;
+  a.beta1 = tr->d.beta1;
+  a.beta2 = tr->d.beta2;
+  a.eps = tr->d.epsilon;
+  // adam_params.h:39-46: bc = 1 - pow(beta, step + 1) in fp32 on the host.
+  const float s = static_cast<float>(tr->step + 1);
+  a.bc1 = 1.0f - std::pow(tr->d.beta1, s);
+  a.bc2 = 1.0f - std::pow(tr->d.beta2, s);
+  a.l1_hash = tr->d.l1_reg;
+  a.l2_mlp = tr->d.l2_reg;
+  a.grad_clip = tr->d.grad_clip;
+  a.weight_decay = tr->d.weight_decay;
+  a.clear_grads = clear_grads ? 1 : 0;
+  a.clear_mask = clear_mask ? 1 : 0;
+  const uint32_t total = tr->hash_count + tr->mlp_count;
+  const uint32_t blocks = std::min<uint32_t>((total + 255) / 256,
+                                             static_cast<uint32_t>(tr->ctx->cu_count) * 16u);
+  hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, tr->ctx->stream, a);
+  TMNN_HIP_TRY(hipGetLastError());
+  if (!lazy && clear_mask)
+    TMNN_HIP_TRY(hipMemsetAsync(tr->mask.ptr, 0, tr->mask_words * sizeof(uint32_t),
+                                tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, int n,
+                      float *d_loss) {
+  const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false);
+  if (blocks < 0) return blocks;
+  hipLaunchKernelGGL(loss_reduce_kernel, dim3(1), dim3(64), 0, tr->ctx->stream,
+                     tr->loss_partials.as<float>(), blocks, 0.0f, n,
+                     d_loss ? d_loss : tr->loss_out.as<float>());
+  TMNN_HIP_TRY(hipGetLastError());
+  const int rc = run_adam(tr, true, true);
+  if (rc != TMNN_OK) return rc;
+  ++tr->step;
+  return TMNN_OK;
+}
+
+int zero_training_state(tmnn_trainer *tr) {
+  hipStream_t st = tr->ctx->stream;
+  TMNN_HIP_TRY(hipMemsetAsync(tr->grad_hash.ptr, 0, tr->hash_count * sizeof(int32_t), st));
+  TMNN_HIP_TRY(hipMemsetAsync(tr->grad_mlp.ptr, 0, tr->mlp_count * sizeof(float), st));
+  TMNN_HIP_TRY(hipMemsetAsync(tr->mask.ptr, 0, tr->mask_words * sizeof(uint32_t), st));
+  return TMNN_OK;
+}
+
+int reset_moments(tmnn_trainer *tr) {
+  const size_t total = (static_cast<size_t>(tr->hash_count) + tr->mlp_count) * sizeof(float);
+  TMNN_HIP_TRY(hipMemsetAsync(tr->m.ptr, 0, total, tr->ctx->stream));
+  TMNN_HIP_TRY(hipMemsetAsync(tr->v.ptr, 0, total, tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int philox_fill(hipStream_t st, float *dst, uint32_t count, uint64_t seed, uint32_t base,
+                float low, float high) {
+  if (count == 0) return TMNN_OK;
+  const uint32_t threads = (count + 3u) / 4u;
+  hipLaunchKernelGGL(philox_uniform_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, dst,
+                     count, static_cast<uint32_t>(seed & 0xFFFFFFFFu),
+                     static_cast<uint32_t>(seed >> 32), base, low, high);
+  TMNN_HIP_TRY(hipGetLastError());
+  return TMNN_OK;
+}
+
+// init_weights_with_config (default_trainer.cpp:1978-2180): one Philox
+// stream; hash at counter 0, then per layer W (Kaiming uniform, ReLU gain)
+// and b (U(+-1/sqrt(fan_in))), each advancing the counter by ceil(count/4).
+int init_weights(tmnn_trainer *tr) {
+  hipStream_t st = tr->ctx->stream;
+  float *hash = tr->params.as<float>();
+  const float r = tr->d.hash_init_range;
+  int rc = philox_fill(st, hash, tr->hash_count, tr->d.seed, 0u, -r, r);
+  if (rc != TMNN_OK) return rc;
+  uint32_t ctr = (tr->hash_count + 3u) / 4u;
+  const float gain = std::sqrt(2.0f);
+  const int H = tr->d.hidden_dim, M = tr->d.num_outputs;
+  struct Slice { int wc, bc, fan_in; };
+  std::vector<Slice> layers;
+  layers.push_back({tr->IN * H, H, tr->IN});
+  for (int k = 1; k < tr->d.num_hidden_layers; ++k) layers.push_back({H * H, H, H});
+  layers.push_back({H * M, M, H});
+  float *dst = hash + tr->hash_count;
+  for (const Slice &s : layers) {
+    const float fin = static_cast<float>(s.fan_in);
+    const float bw = gain * std::sqrt(3.0f / fin);
+    rc = philox_fill(st, dst, static_cast<uint32_t>(s.wc), tr->d.seed, ctr, -bw, bw);
+    if (rc != TMNN_OK) return rc;
+    ctr += static_cast<uint32_t>((s.wc + 3) / 4);
+    dst += s.wc;
+    const float bb = 1.0f / std::sqrt(fin);
+    rc = philox_fill(st, dst, static_cast<uint32_t>(s.bc), tr->d.seed, ctr, -bb, bb);
+    if (rc != TMNN_OK) return rc;
+    ctr += static_cast<uint32_t>((s.bc + 3) / 4);
+    dst += s.bc;
+  }
+  return TMNN_OK;
+}
+
+void put_u32(uint8_t *p, uint32_t v) {
+  p[0] = static_cast<uint8_t>(v & 0xFFu);
+  p[1] = static_cast<uint8_t>((v >> 8) & 0xFFu);
+  p[2] = static_cast<uint8_t>((v >> 16) & 0xFFu);
+  p[3] = static_cast<uint8_t>((v >> 24) & 0xFFu);
+}
+
+uint32_t get_u32(const uint8_t *p) {
+  return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) |
+         (static_cast<uint32_t>(p[2]) << 16) | (static_cast<uint32_t>(p[3]) << 24);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *tmnn_last_error(void) { return g_last_error.c_str(); }
+
+uint32_t tmnn_abi_version(void) { return kAbiVersion; }
+
+int tmnn_context_create(int32_t device, tmnn_context **out) {
+  if (!out) return fail(TMNN_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  int count = 0;
+  TMNN_HIP_TRY(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "device ordinal out of range");
+  TMNN_HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  TMNN_HIP_TRY(hipGetDeviceProperties(&prop, device));
+  std::unique_ptr<tmnn_context> ctx(new (std::nothrow) tmnn_context());
+  if (!ctx) return fail(TMNN_ERR_RUNTIME, "out of host memory");
+  ctx->device = device;
+  ctx->cu_count = prop.multiProcessorCount;
+  ctx->mem_bytes = prop.totalGlobalMem;
+  ctx->name = prop.gcnArchName;
+  TMNN_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+  *out = ctx.release();
+  return TMNN_OK;
+}
+
+int tmnn_context_destroy(tmnn_context *ctx) {
+  if (!ctx) return TMNN_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+  }
+  delete ctx;
+  return TMNN_OK;
+}
+
+int tmnn_context_device_info(tmnn_context *ctx, int32_t *cu_count, uint64_t *global_mem_bytes,
+                             char *name, size_t name_capacity) {
+  if (!ctx) return fail(TMNN_ERR_INVALID_ARGUMENT, "context is null");
+  if (cu_count) *cu_count = ctx->cu_count;
+  if (global_mem_bytes) *global_mem_bytes = ctx->mem_bytes;
+  if (name && name_capacity > 0) {
+    std::strncpy(name, ctx->name.c_str(), name_capacity - 1);
+    name[name_capacity - 1] = '\0';
+  }
+  return TMNN_OK;
+}
+
+// Reference defaults: factory_json_detail.h:159-290 (encoding/network),
+// trainer.h:34-61 (optimizer), weight_init.h:113-141 (init).
+void tmnn_model_desc_init(tmnn_model_desc *d) {
+  if (!d) return;
+  std::memset(d, 0, sizeof *d);
+  d->struct_size = sizeof *d;
+  d->spatial_dims = 3;
+  d->num_levels = 16;
+  d->features_per_level = 2;
+  d->log2_hashmap_size = 19;
+  d->base_resolution = 16.0f;
+  d->per_level_scale = 1.447f;
+  d->hidden_dim = 64;
+  d->num_hidden_layers = 2;
+  d->num_outputs = 1;
+  d->loss_kind = TMNN_LOSS_L2;
+  d->huber_delta = 1.0f;
+  d->lr_encoding = 1e-2f;
+  d->lr_network = 1e-3f;
+  d->beta1 = 0.9f;
+  d->beta2 = 0.99f;
+  d->epsilon = 1e-15f;
+  d->batch_size = 1024;
+  d->precision = TMNN_PRECISION_FP32;
+  d->hash_adam_mode = TMNN_HASH_ADAM_LAZY;
+  d->morton_sort = 1;
+  d->seed = 42u;
+  d->hash_init_range = 1.0e-4f;
+}
+
+int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_trainer **out) {
+  if (!ctx || !desc || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  if (desc->struct_size != sizeof(tmnn_model_desc))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_model_desc.struct_size mismatch");
+  std::string why;
+  if (!desc_ok(desc, why)) return fail(TMNN_ERR_INVALID_ARGUMENT, "KernelSpec: " + why);
+  if (desc->hidden_dim > 64)
+    return fail(TMNN_ERR_UNSUPPORTED, "hidden_dim > 64 is not built in this library");
+  if (desc->num_outputs > 16)
+    return fail(TMNN_ERR_UNSUPPORTED, "num_outputs > 16 is not built in this library");
+  const int IN = desc->num_levels * desc->features_per_level;
+  if (IN > 64)
+    return fail(TMNN_ERR_UNSUPPORTED, "num_levels * features_per_level > 64 is not built");
+  TMNN_HIP_TRY(hipSetDevice(ctx->device));
+
+  std::unique_ptr<tmnn_trainer> tr(new (std::nothrow) tmnn_trainer());
+  if (!tr) return fail(TMNN_ERR_RUNTIME, "out of host memory");
+  tr->ctx = ctx;
+  tr->d = *desc;
+  tr->IN = IN;
+  tr->INP = IN <= 32 ? 32 : 64;
+  tr->HP = desc->hidden_dim <= 32 ? 32 : 64;
+  tr->lr_enc = desc->lr_encoding;
+  tr->lr_net = desc->lr_network;
+  tr->hash_count = static_cast<uint32_t>(desc->num_levels) *
+                   (1u << desc->log2_hashmap_size) *
+                   static_cast<uint32_t>(desc->features_per_level);
+  const FieldLayout lay = make_layout(tr->INP, tr->HP, IN, desc->hidden_dim,
+                                      desc->num_hidden_layers, desc->num_outputs, 0, false,
+                                      false, 1);
+  tr->mlp_count = static_cast<uint32_t>(lay.mlp_count());
+  const uint32_t width = desc->features_per_level == 2 ? 2u : 1u;
+  tr->mask_words = (tr->hash_count / width + 31u) / 32u;
+  // One fp32 resolution table for every kernel: r_0 = b, r_l = r_{l-1} * s
+  // (iterated product of the eval path, mlp_kernel_emitter.cpp:224,298).
+  {
+    float r = baked6(desc->base_resolution);
+    const float s = baked6(desc->per_level_scale);
+    for (int l = 0; l < desc->num_levels; ++l) {
+      tr->res[l] = r;
+      r = r * s;
+    }
+  }
+
+  int rc;
+  if ((rc = plan_kernel(tr.get(), desc->precision == TMNN_PRECISION_FP16, true,
+                        tr->train_plan)) != TMNN_OK)
+    return rc;
+  if ((rc = plan_kernel(tr.get(), desc->precision == TMNN_PRECISION_FP16, false,
+                        tr->fwd_plan)) != TMNN_OK)
+    return rc;
+  if ((rc = plan_kernel(tr.get(), false, false, tr->infer_plan)) != TMNN_OK) return rc;
+
+  const size_t total = static_cast<size_t>(tr->hash_count) + tr->mlp_count;
+  TMNN_HIP_TRY(tr->params.ensure(total * sizeof(float)));
+  TMNN_HIP_TRY(tr->m.ensure(total * sizeof(float)));
+  TMNN_HIP_TRY(tr->v.ensure(total * sizeof(float)));
+  TMNN_HIP_TRY(tr->grad_hash.ensure(tr->hash_count * sizeof(int32_t)));
+  TMNN_HIP_TRY(tr->grad_mlp.ensure(tr->mlp_count * sizeof(float)));
+  TMNN_HIP_TRY(tr->mask.ensure(tr->mask_words * sizeof(uint32_t)));
+  TMNN_HIP_TRY(tr->partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
+                                   tr->mlp_count * sizeof(float)));
+  TMNN_HIP_TRY(tr->loss_partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
+                                        sizeof(float)));
+  TMNN_HIP_TRY(tr->loss_out.ensure(sizeof(float)));
+  if ((rc = init_weights(tr.get())) != TMNN_OK) return rc;
+  if ((rc = reset_moments(tr.get())) != TMNN_OK) return rc;
+  if ((rc = zero_training_state(tr.get())) != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  *out = tr.release();
+  return TMNN_OK;
+}
+
+int tmnn_trainer_destroy(tmnn_trainer *tr) {
+  if (!tr) return TMNN_OK;
+  (void)hipSetDevice(tr->ctx->device);
+  (void)hipStreamSynchronize(tr->ctx->stream);
+  delete tr;
+  return TMNN_OK;
+}
+
+int tmnn_trainer_param_counts(tmnn_trainer *tr, uint32_t *hash_count, uint32_t *mlp_count) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (hash_count) *hash_count = tr->hash_count;
+  if (mlp_count) *mlp_count = tr->mlp_count;
+  return TMNN_OK;
+}
+
+int tmnn_trainer_inspect(tmnn_trainer *tr, tmnn_inspection *o) {
+  if (!tr || !o) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  std::memset(o, 0, sizeof *o);
+  o->family = 0;
+  o->precision = tr->d.precision;
+  o->hidden_padded = tr->HP;
+  o->input_padded = tr->INP;
+  o->points_per_wave_tile = kTilePts;
+  o->waves_per_block_train = tr->train_plan.wpb;
+  o->blocks_train = tr->train_plan.max_blocks;
+  o->lds_bytes_train = tr->train_plan.lds;
+  o->lds_bytes_infer = tr->infer_plan.lds;
+  o->cu_count = tr->ctx->cu_count;
+  o->hash_param_count = tr->hash_count;
+  o->mlp_param_count = tr->mlp_count;
+  o->batch_size = static_cast<uint32_t>(tr->d.batch_size);
+  return TMNN_OK;
+}
+
+int tmnn_training_step(tmnn_trainer *tr, const float *input, const float *target, int32_t n,
+                       tmnn_step_result *out) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
+  if (!input || !target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int bn = std::min(n, tr->d.batch_size);
+  int rc = ensure_batch(tr, bn);
+  if (rc != TMNN_OK) return rc;
+  hipStream_t st = tr->ctx->stream;
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, input,
+                              static_cast<size_t>(bn) * tr->d.spatial_dims * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_tgt.ptr, target,
+                              static_cast<size_t>(bn) * tr->d.num_outputs * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  rc = train_step_device(tr, tr->in_pos.as<float>(), tr->in_tgt.as<float>(), bn,
+                         tr->loss_out.as<float>());
+  if (rc != TMNN_OK) return rc;
+  float loss = 0.0f;
+  TMNN_HIP_TRY(hipMemcpyAsync(&loss, tr->loss_out.ptr, sizeof(float), hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  if (out) {
+    out->loss = loss;
+    out->step = tr->step;
+    out->batch_n = static_cast<uint32_t>(bn);
+  }
+  return TMNN_OK;
+}
+
+int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input, const float *d_target,
+                              int32_t n, float *d_loss_out) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
+  if (!d_input || !d_target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int bn = std::min(n, tr->d.batch_size);
+  const int rc = ensure_batch(tr, bn);
+  if (rc != TMNN_OK) return rc;
+  return train_step_device(tr, d_input, d_target, bn, d_loss_out);
+}
+
+int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions, float *d_output,
+                          int32_t n) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "FieldEvaluator::evaluate: N must be non-negative");
+  if (n == 0) return TMNN_OK;
+  if (!d_positions || !d_output)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "positions and output must be non-null when N > 0");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  FieldArgs a = base_args(tr);
+  a.mode = kModeForward;
+  a.pos = d_positions;
+  a.out = d_output;
+  const int blocks = launch_field(tr, tr->infer_plan, a, n);
+  return blocks < 0 ? blocks : TMNN_OK;
+}
+
+int tmnn_inference(tmnn_trainer *tr, const float *positions, float *output, int32_t n) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "FieldEvaluator::evaluate: N must be non-negative");
+  if (n == 0) return TMNN_OK;
+  if (!positions || !output)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "positions and output must be non-null when N > 0");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  const size_t D = tr->d.spatial_dims, M = tr->d.num_outputs;
+  TMNN_HIP_TRY(tr->in_pos.ensure(n * D * sizeof(float)));
+  TMNN_HIP_TRY(tr->out_buf.ensure(n * M * sizeof(float)));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, positions, n * D * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const int rc = tmnn_inference_device(tr, tr->in_pos.as<float>(), tr->out_buf.as<float>(), n);
+  if (rc != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipMemcpyAsync(output, tr->out_buf.ptr, n * M * sizeof(float),
+                              hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_forward_for_training(tmnn_trainer *tr, const float *input, float *output, int32_t n,
+                              uint32_t *written) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (written) *written = 0;
+  if (n <= 0)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "Trainer::forward_for_training: N must be greater than zero");
+  if (!input || !output) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/output is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int bn = std::min(n, tr->d.batch_size);
+  int rc = ensure_batch(tr, bn);
+  if (rc != TMNN_OK) return rc;
+  hipStream_t st = tr->ctx->stream;
+  const size_t D = tr->d.spatial_dims, M = tr->d.num_outputs;
+  TMNN_HIP_TRY(tr->out_buf.ensure(bn * M * sizeof(float)));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, input, bn * D * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const float *pos = nullptr, *unused = nullptr;
+  const uint32_t *perm = nullptr;
+  rc = sort_batch(tr, tr->in_pos.as<float>(), nullptr, 0, bn, &pos, &unused, &perm);
+  if (rc != TMNN_OK) return rc;
+  FieldArgs a = base_args(tr);
+  a.mode = kModeForward;
+  a.pos = pos;
+  a.out = tr->out_buf.as<float>();
+  a.out_index = perm;  // write each sorted point back to its caller row
+  const int blocks = launch_field(tr, tr->fwd_plan, a, bn);
+  if (blocks < 0) return blocks;
+  TMNN_HIP_TRY(hipMemcpyAsync(output, tr->out_buf.ptr, bn * M * sizeof(float),
+                              hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  if (written) *written = static_cast<uint32_t>(bn * M);
+  return TMNN_OK;
+}
+
+int tmnn_zero_gradients(tmnn_trainer *tr) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int rc = zero_training_state(tr);
+  if (rc != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int tmnn_backward_accumulate(tmnn_trainer *tr, const float *input, const float *d_output,
+                             int32_t n) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "backward_accumulate: N must be > 0");
+  if (!input || !d_output) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/d_output is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int bn = std::min(n, tr->d.batch_size);
+  int rc = ensure_batch(tr, bn);
+  if (rc != TMNN_OK) return rc;
+  hipStream_t st = tr->ctx->stream;
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, input,
+                              static_cast<size_t>(bn) * tr->d.spatial_dims * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_tgt.ptr, d_output,
+                              static_cast<size_t>(bn) * tr->d.num_outputs * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const int blocks = run_forward_backward(tr, tr->in_pos.as<float>(), tr->in_tgt.as<float>(), bn,
+                                          true);
+  if (blocks < 0) return blocks;
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_adam_step(tmnn_trainer *tr) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  // Split-path Adam keeps the accumulated gradients (they persist until the
+  // next zero_gradients) and consumes the mask (default_trainer.cpp:1396-1443).
+  const int rc = run_adam(tr, false, true);
+  if (rc != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  ++tr->step;
+  return TMNN_OK;
+}
+
+int tmnn_synchronize(tmnn_trainer *tr) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int tmnn_get_step(tmnn_trainer *tr, uint32_t *step) {
+  if (!tr || !step) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  *step = tr->step;
+  return TMNN_OK;
+}
+
+int tmnn_get_weights(tmnn_trainer *tr, float *hash, size_t hash_count, float *mlp,
+                     size_t mlp_count) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (hash && hash_count != tr->hash_count)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "hash_weights count mismatch");
+  if (mlp && mlp_count != tr->mlp_count)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "mlp_weights count mismatch");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  if (hash)
+    TMNN_HIP_TRY(hipMemcpyAsync(hash, tr->params.ptr, hash_count * sizeof(float),
+                                hipMemcpyDeviceToHost, st));
+  if (mlp)
+    TMNN_HIP_TRY(hipMemcpyAsync(mlp, tr->params.as<float>() + tr->hash_count,
+                                mlp_count * sizeof(float), hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_set_initial_weights(tmnn_trainer *tr, const float *hash, size_t hash_count,
+                             const float *mlp, size_t mlp_count) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (hash && hash_count != tr->hash_count)
+    return fail(TMNN_ERR_RUNTIME, "set_initial_weights: hash_weights count mismatch: got " +
+                                      std::to_string(hash_count) + " expected " +
+                                      std::to_string(tr->hash_count));
+  if (mlp && mlp_count != tr->mlp_count)
+    return fail(TMNN_ERR_RUNTIME, "set_initial_weights: mlp_weights count mismatch: got " +
+                                      std::to_string(mlp_count) + " expected " +
+                                      std::to_string(tr->mlp_count));
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  if (hash && hash_count)
+    TMNN_HIP_TRY(hipMemcpyAsync(tr->params.ptr, hash, hash_count * sizeof(float),
+                                hipMemcpyHostToDevice, st));
+  if (mlp && mlp_count)
+    TMNN_HIP_TRY(hipMemcpyAsync(tr->params.as<float>() + tr->hash_count, mlp,
+                                mlp_count * sizeof(float), hipMemcpyHostToDevice, st));
+  int rc = reset_moments(tr);
+  if (rc != TMNN_OK) return rc;
+  rc = zero_training_state(tr);
+  if (rc != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  tr->step = 0;
+  return TMNN_OK;
+}
+
+int tmnn_export_optimizer_state(tmnn_trainer *tr, uint32_t *version, uint32_t *step,
+                                uint8_t *payload, size_t capacity, size_t *payload_len) {
+  if (!tr || !payload_len) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  const size_t hb = static_cast<size_t>(tr->hash_count) * sizeof(float);
+  const size_t mb = static_cast<size_t>(tr->mlp_count) * sizeof(float);
+  const size_t need = 4 * 4 + 2 * hb + 2 * mb;
+  *payload_len = need;
+  if (version) *version = kOptimizerBlobVersion;
+  if (step) *step = tr->step;
+  if (!payload) return TMNN_OK;
+  if (capacity < need) return fail(TMNN_ERR_INVALID_ARGUMENT, "payload capacity too small");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  // sections: m_hash, v_hash, m_mlp, v_mlp (default_trainer.cpp:1656-1661)
+  const struct { const DevBuf *buf; size_t off, bytes; } sec[4] = {
+      {&tr->m, 0, hb}, {&tr->v, 0, hb}, {&tr->m, hb, mb}, {&tr->v, hb, mb}};
+  uint8_t *cur = payload;
+  for (const auto &s : sec) {
+    put_u32(cur, static_cast<uint32_t>(s.bytes));
+    cur += 4;
+    if (s.bytes)
+      TMNN_HIP_TRY(hipMemcpyAsync(cur, static_cast<const uint8_t *>(s.buf->ptr) + s.off, s.bytes,
+                                  hipMemcpyDeviceToHost, st));
+    cur += s.bytes;
+  }
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_import_optimizer_state(tmnn_trainer *tr, uint32_t version, uint32_t step,
+                                const uint8_t *payload, size_t payload_len) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (version != kOptimizerBlobVersion)
+    return fail(TMNN_ERR_RUNTIME, "DefaultRuntime: unsupported optimizer blob version");
+  if (!payload && payload_len) return fail(TMNN_ERR_INVALID_ARGUMENT, "payload is null");
+  const size_t hb = static_cast<size_t>(tr->hash_count) * sizeof(float);
+  const size_t mb = static_cast<size_t>(tr->mlp_count) * sizeof(float);
+  const size_t expect[4] = {hb, hb, mb, mb};
+  const char *names[4] = {"adam_m_hash", "adam_v_hash", "adam_m_mlp", "adam_v_mlp"};
+  const uint8_t *cur = payload;
+  size_t remaining = payload_len;
+  const uint8_t *data[4];
+  for (int i = 0; i < 4; ++i) {
+    if (remaining < 4) return fail(TMNN_ERR_RUNTIME, "DefaultRuntime: optimizer blob truncated");
+    const uint32_t sz = get_u32(cur);
+    cur += 4;
+    remaining -= 4;
+    if (remaining < sz)
+      return fail(TMNN_ERR_RUNTIME, "DefaultRuntime: optimizer blob section truncated");
+    if (sz != expect[i])
+      return fail(TMNN_ERR_RUNTIME, std::string("DefaultRuntime: ") + names[i] + " size mismatch");
+    data[i] = cur;
+    cur += sz;
+    remaining -= sz;
+  }
+  if (remaining != 0)
+    return fail(TMNN_ERR_RUNTIME, "DefaultRuntime: optimizer blob has trailing bytes");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  uint8_t *mp = static_cast<uint8_t *>(tr->m.ptr);
+  uint8_t *vp = static_cast<uint8_t *>(tr->v.ptr);
+  if (hb) {
+    TMNN_HIP_TRY(hipMemcpyAsync(mp, data[0], hb, hipMemcpyHostToDevice, st));
+    TMNN_HIP_TRY(hipMemcpyAsync(vp, data[1], hb, hipMemcpyHostToDevice, st));
+  }
+  if (mb) {
+    TMNN_HIP_TRY(hipMemcpyAsync(mp + hb, data[2], mb, hipMemcpyHostToDevice, st));
+    TMNN_HIP_TRY(hipMemcpyAsync(vp + hb, data[3], mb, hipMemcpyHostToDevice, st));
+  }
+  const int rc = zero_training_state(tr);
+  if (rc != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  tr->step = step;
+  return TMNN_OK;
+}
+
+int tmnn_reset_optimizer(tmnn_trainer *tr) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  int rc = reset_moments(tr);
+  if (rc != TMNN_OK) return rc;
+  rc = zero_training_state(tr);
+  if (rc != TMNN_OK) return rc;
+  TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  tr->step = 0;
+  return TMNN_OK;
+}
+
+int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding, float lr_network) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  tr->lr_enc = lr_encoding;
+  tr->lr_net = lr_network;
+  return TMNN_OK;
+}
+
+int tmnn_debug_encode(tmnn_trainer *tr, const float *positions, int32_t n, float *features,
+                      uint32_t *corner_index, float *corner_weight) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "N must be non-negative");
+  if (n == 0) return TMNN_OK;
+  if (!positions || !features) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  const size_t D = tr->d.spatial_dims, L = tr->d.num_levels, F = tr->d.features_per_level;
+  const size_t C = size_t(1) << D;
+  TMNN_HIP_TRY(tr->in_pos.ensure(n * D * sizeof(float)));
+  TMNN_HIP_TRY(tr->dbg_a.ensure(n * L * F * sizeof(float)));
+  TMNN_HIP_TRY(tr->dbg_b.ensure(n * L * C * sizeof(uint32_t)));
+  TMNN_HIP_TRY(tr->dbg_c.ensure(n * L * C * sizeof(float) + kMaxLevels * sizeof(float)));
+  float *res_dev = reinterpret_cast<float *>(static_cast<uint8_t *>(tr->dbg_c.ptr) +
+                                             n * L * C * sizeof(float));
+  TMNN_HIP_TRY(hipMemcpyAsync(res_dev, tr->res, kMaxLevels * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, positions, n * D * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const int64_t threads = static_cast<int64_t>(n) * static_cast<int64_t>(L);
+  hipLaunchKernelGGL(encode_debug_kernel, dim3(static_cast<uint32_t>((threads + 255) / 256)),
+                     dim3(256), 0, st, tr->params.as<float>(),
+                     static_cast<uint32_t>(tr->d.log2_hashmap_size), tr->d.spatial_dims,
+                     tr->d.features_per_level, tr->d.num_levels, res_dev, tr->in_pos.as<float>(),
+                     n, tr->dbg_a.as<float>(), tr->dbg_b.as<uint32_t>(),
+                     tr->dbg_c.as<float>());
+  TMNN_HIP_TRY(hipGetLastError());
+  TMNN_HIP_TRY(hipMemcpyAsync(features, tr->dbg_a.ptr, n * L * F * sizeof(float),
+                              hipMemcpyDeviceToHost, st));
+  if (corner_index)
+    TMNN_HIP_TRY(hipMemcpyAsync(corner_index, tr->dbg_b.ptr, n * L * C * sizeof(uint32_t),
+                                hipMemcpyDeviceToHost, st));
+  if (corner_weight)
+    TMNN_HIP_TRY(hipMemcpyAsync(corner_weight, tr->dbg_c.ptr, n * L * C * sizeof(float),
+                                hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_debug_get_gradients(tmnn_trainer *tr, int32_t *grad_hash, size_t hash_count,
+                             float *grad_mlp, size_t mlp_count) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (grad_hash && hash_count != tr->hash_count)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "grad_hash count mismatch");
+  if (grad_mlp && mlp_count != tr->mlp_count)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "grad_mlp count mismatch");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  if (grad_hash)
+    TMNN_HIP_TRY(hipMemcpyAsync(grad_hash, tr->grad_hash.ptr, hash_count * sizeof(int32_t),
+                                hipMemcpyDeviceToHost, st));
+  if (grad_mlp)
+    TMNN_HIP_TRY(hipMemcpyAsync(grad_mlp, tr->grad_mlp.ptr, mlp_count * sizeof(float),
+                                hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_debug_get_active_mask(tmnn_trainer *tr, uint32_t *words, size_t word_count) {
+  if (!tr || !words) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (word_count != tr->mask_words) return fail(TMNN_ERR_INVALID_ARGUMENT, "word count mismatch");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  TMNN_HIP_TRY(hipMemcpyAsync(words, tr->mask.ptr, word_count * sizeof(uint32_t),
+                              hipMemcpyDeviceToHost, tr->ctx->stream));
+  TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int tmnn_debug_get_resolutions(tmnn_trainer *tr, float *out, int32_t count) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (count != tr->d.num_levels) return fail(TMNN_ERR_INVALID_ARGUMENT, "count must equal num_levels");
+  for (int l = 0; l < count; ++l) out[l] = tr->res[l];
+  return TMNN_OK;
+}
+
+int tmnn_debug_philox_uniform(tmnn_context *ctx, uint64_t seed, uint32_t counter_base,
+                              uint32_t count, float low, float high, float *out) {
+  if (!ctx || (!out && count)) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (count == 0) return TMNN_OK;
+  TMNN_HIP_TRY(hipSetDevice(ctx->device));
+  float *dev = nullptr;
+  TMNN_HIP_TRY(hipMalloc(&dev, count * sizeof(float)));
+  int rc = philox_fill(ctx->stream, dev, count, seed, counter_base, low, high);
+  if (rc == TMNN_OK) {
+    hipError_t e = hipMemcpyAsync(out, dev, count * sizeof(float), hipMemcpyDeviceToHost,
+                                  ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) rc = fail(TMNN_ERR_GPU, hipGetErrorString(e));
+  }
+  (void)hipFree(dev);
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,164 @@
+"""ctypes binding of libtmnn_hip.so (the C-ABI declared in include/tmnn_hip.h).
+
+The shared library is built in-tree by tiny-metal-nn_amd/build.py. There is
+no fallback: if the library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("TMNN_HIP_LIB", PKG_ROOT / "libtmnn_hip.so"))
+
+TMNN_OK = 0
+TMNN_ERR_INVALID_ARGUMENT = -1
+TMNN_ERR_RUNTIME = -2
+TMNN_ERR_GPU = -3
+TMNN_ERR_UNSUPPORTED = -4
+
+LOSS_L2, LOSS_L1, LOSS_HUBER, LOSS_COSINE, LOSS_RELATIVE_L2 = range(5)
+PRECISION_FP32, PRECISION_FP16 = 0, 1
+HASH_ADAM_LAZY, HASH_ADAM_DENSE = 0, 1
+
+c_float_p = ctypes.POINTER(ctypes.c_float)
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("spatial_dims", ctypes.c_int32),
+        ("num_levels", ctypes.c_int32),
+        ("features_per_level", ctypes.c_int32),
+        ("log2_hashmap_size", ctypes.c_int32),
+        ("base_resolution", ctypes.c_float),
+        ("per_level_scale", ctypes.c_float),
+        ("hidden_dim", ctypes.c_int32),
+        ("num_hidden_layers", ctypes.c_int32),
+        ("num_outputs", ctypes.c_int32),
+        ("loss_kind", ctypes.c_int32),
+        ("huber_delta", ctypes.c_float),
+        ("lr_encoding", ctypes.c_float),
+        ("lr_network", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("epsilon", ctypes.c_float),
+        ("l1_reg", ctypes.c_float),
+        ("l2_reg", ctypes.c_float),
+        ("grad_clip", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("batch_size", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+        ("hash_adam_mode", ctypes.c_int32),
+        ("morton_sort", ctypes.c_int32),
+        ("seed", ctypes.c_uint64),
+        ("hash_init_range", ctypes.c_float),
+    ]
+
+
+class StepResult(ctypes.Structure):
+    _fields_ = [
+        ("loss", ctypes.c_float),
+        ("step", ctypes.c_uint32),
+        ("batch_n", ctypes.c_uint32),
+    ]
+
+
+class Inspection(ctypes.Structure):
+    _fields_ = [
+        ("family", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+        ("hidden_padded", ctypes.c_int32),
+        ("input_padded", ctypes.c_int32),
+        ("points_per_wave_tile", ctypes.c_int32),
+        ("waves_per_block_train", ctypes.c_int32),
+        ("blocks_train", ctypes.c_int32),
+        ("lds_bytes_train", ctypes.c_int32),
+        ("lds_bytes_infer", ctypes.c_int32),
+        ("cu_count", ctypes.c_int32),
+        ("hash_param_count", ctypes.c_uint32),
+        ("mlp_param_count", ctypes.c_uint32),
+        ("batch_size", ctypes.c_uint32),
+    ]
+
+
+_V = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_U32 = ctypes.c_uint32
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); every symbol include/tmnn_hip.h declares.
+SIGNATURES = {
+    "tmnn_last_error": (ctypes.c_char_p, []),
+    "tmnn_abi_version": (_U32, []),
+    "tmnn_context_create": (ctypes.c_int, [_I32, ctypes.POINTER(_V)]),
+    "tmnn_context_destroy": (ctypes.c_int, [_V]),
+    "tmnn_context_device_info": (ctypes.c_int, [_V, ctypes.POINTER(_I32),
+                                                ctypes.POINTER(ctypes.c_uint64),
+                                                ctypes.c_char_p, _SZ]),
+    "tmnn_model_desc_init": (None, [ctypes.POINTER(ModelDesc)]),
+    "tmnn_trainer_create": (ctypes.c_int, [_V, ctypes.POINTER(ModelDesc), ctypes.POINTER(_V)]),
+    "tmnn_trainer_destroy": (ctypes.c_int, [_V]),
+    "tmnn_trainer_param_counts": (ctypes.c_int, [_V, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
+    "tmnn_trainer_inspect": (ctypes.c_int, [_V, ctypes.POINTER(Inspection)]),
+    "tmnn_training_step": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(StepResult)]),
+    "tmnn_training_step_device": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
+    "tmnn_inference": (ctypes.c_int, [_V, _V, _V, _I32]),
+    "tmnn_inference_device": (ctypes.c_int, [_V, _V, _V, _I32]),
+    "tmnn_forward_for_training": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(_U32)]),
+    "tmnn_zero_gradients": (ctypes.c_int, [_V]),
+    "tmnn_backward_accumulate": (ctypes.c_int, [_V, _V, _V, _I32]),
+    "tmnn_adam_step": (ctypes.c_int, [_V]),
+    "tmnn_synchronize": (ctypes.c_int, [_V]),
+    "tmnn_get_step": (ctypes.c_int, [_V, ctypes.POINTER(_U32)]),
+    "tmnn_get_weights": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
+    "tmnn_set_initial_weights": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
+    "tmnn_export_optimizer_state": (ctypes.c_int, [_V, ctypes.POINTER(_U32), ctypes.POINTER(_U32),
+                                                   _V, _SZ, ctypes.POINTER(_SZ)]),
+    "tmnn_import_optimizer_state": (ctypes.c_int, [_V, _U32, _U32, _V, _SZ]),
+    "tmnn_reset_optimizer": (ctypes.c_int, [_V]),
+    "tmnn_set_learning_rate": (ctypes.c_int, [_V, _F, _F]),
+    "tmnn_debug_encode": (ctypes.c_int, [_V, _V, _I32, _V, _V, _V]),
+    "tmnn_debug_get_gradients": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
+    "tmnn_debug_get_active_mask": (ctypes.c_int, [_V, _V, _SZ]),
+    "tmnn_debug_get_resolutions": (ctypes.c_int, [_V, _V, _I32]),
+    "tmnn_debug_philox_uniform": (ctypes.c_int, [_V, ctypes.c_uint64, _U32, _U32, _F, _F, _V]),
+}
+
+
+class TmnnError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python tiny-metal-nn_amd/build.py`")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != TMNN_OK:
+        msg = load().tmnn_last_error().decode(errors="replace")
+        if rc == TMNN_ERR_INVALID_ARGUMENT:
+            raise ValueError(msg)
+        raise TmnnError(rc, msg)

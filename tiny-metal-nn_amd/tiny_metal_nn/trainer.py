@@ -1,0 +1,334 @@
+"""Trainer: the reference's Python surface (src/python/tmnn_pybind.cpp:274-600)
+over the MI355X C-ABI.
+
+Same construction (`Trainer.from_config(config, n_input=, n_output=)`), same
+calls (`training_step`, `inference`, `step`, `close`, context manager), same
+errors (ConfigError, DTypeError, ClosedError, ConcurrentTrainingStepError),
+plus the split/accumulate API and checkpoint calls of the C++ Trainer
+(include/tiny-metal-nn/trainer.h) and device-pointer entry points for
+callers whose batches already live in GPU memory.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .config import ConfigError, canonicalize_model_config, model_desc
+
+
+class DTypeError(TypeError):
+    """An input array is not float32 (the reference's DTypeError)."""
+
+
+class ClosedError(RuntimeError):
+    """The trainer was already closed."""
+
+
+class ConcurrentTrainingStepError(RuntimeError):
+    """A second thread entered the single-threaded trainer."""
+
+
+@dataclass
+class OptimizerStateBlob:
+    """OptimizerStateBlob v1 (include/tiny-metal-nn/detail/runtime_authority.h)."""
+
+    version: int
+    step: int
+    payload: bytes
+
+
+def _as_f32_2d(x, name: str, cols: int | None = None) -> np.ndarray:
+    arr = np.asarray(x)
+    if arr.dtype != np.float32:
+        raise DTypeError(f"{name} must be float32, got {arr.dtype}")
+    if arr.ndim != 2:
+        raise ValueError(f"{name} must be 2D (batch_size, dims)")
+    if not arr.flags["C_CONTIGUOUS"]:
+        raise ValueError(f"{name} must be C-contiguous")
+    if cols is not None and arr.shape[1] != cols:
+        raise ValueError(f"{name} must have {cols} columns, got {arr.shape[1]}")
+    return arr
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class _Context:
+    """One HIP device + stream shared by trainers (MetalContext analogue)."""
+
+    _lock = threading.Lock()
+    _by_device: dict[int, "_Context"] = {}
+
+    def __init__(self, device: int):
+        lib = _lib.load()
+        h = ctypes.c_void_p()
+        _lib.check(lib.tmnn_context_create(device, ctypes.byref(h)))
+        self.handle = h
+        self.device = device
+
+    @classmethod
+    def get(cls, device: int = 0) -> "_Context":
+        with cls._lock:
+            ctx = cls._by_device.get(device)
+            if ctx is None:
+                ctx = cls._by_device[device] = _Context(device)
+            return ctx
+
+
+class Trainer:
+    """The single object for training and inference on hash-grid + MLP."""
+
+    def __init__(self, canonical: dict, device: int = 0):
+        self._lib = _lib.load()
+        self.config = canonical
+        self.n_input = canonical["encoding"]["n_input_dims"]
+        self.n_output = canonical["network"]["n_output_dims"]
+        self._ctx = _Context.get(device)
+        h = ctypes.c_void_p()
+        desc = model_desc(canonical)
+        _lib.check(self._lib.tmnn_trainer_create(self._ctx.handle, ctypes.byref(desc),
+                                                 ctypes.byref(h)))
+        self._h = h
+        hc, mc = ctypes.c_uint32(), ctypes.c_uint32()
+        _lib.check(self._lib.tmnn_trainer_param_counts(h, ctypes.byref(hc), ctypes.byref(mc)))
+        self.hash_param_count = hc.value
+        self.mlp_param_count = mc.value
+        self._busy = threading.Lock()
+        self._closed = False
+
+    # ---- construction ---------------------------------------------------
+    @classmethod
+    def from_config(cls, config: dict, *, n_input: int, n_output: int,
+                    device: int = 0) -> "Trainer":
+        """Construct from a JSON-shaped dict (try_create_from_config)."""
+        canonical = canonicalize_model_config(int(n_input), int(n_output), config)
+        return cls(canonical, device=device)
+
+    # ---- lifetime ---------------------------------------------------------
+    def close(self) -> None:
+        if not self._closed:
+            self._closed = True
+            self._lib.tmnn_trainer_destroy(self._h)
+            self._h = None
+
+    @property
+    def closed(self) -> bool:
+        return self._closed
+
+    def __enter__(self) -> "Trainer":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __repr__(self) -> str:
+        if self._closed:
+            return "<tmnn.Trainer closed>"
+        return (f"<tmnn.Trainer n_input={self.n_input} n_output={self.n_output} "
+                f"step={self.step()}>")
+
+    def _check_open(self) -> None:
+        if self._closed:
+            raise ClosedError("Trainer is closed")
+
+    def _enter(self, what: str):
+        self._check_open()
+        if not self._busy.acquire(blocking=False):
+            raise ConcurrentTrainingStepError(
+                f"{what} is already in progress on another thread. tmnn.Trainer is "
+                "single-threaded; use one Trainer per thread.")
+        return self._busy
+
+    # ---- accessors ----------------------------------------------------------
+    def step(self) -> int:
+        self._check_open()
+        s = ctypes.c_uint32()
+        _lib.check(self._lib.tmnn_get_step(self._h, ctypes.byref(s)))
+        return s.value
+
+    def is_gpu_available(self) -> bool:
+        self._check_open()
+        return True
+
+    def inspect_runtime(self) -> dict:
+        self._check_open()
+        ins = _lib.Inspection()
+        _lib.check(self._lib.tmnn_trainer_inspect(self._h, ctypes.byref(ins)))
+        return {k: getattr(ins, k) for k, _ in _lib.Inspection._fields_}
+
+    # ---- fused path -----------------------------------------------------------
+    def training_step(self, input, target) -> float:
+        """One fused step (forward + backward + Adam); returns the loss."""
+        x = _as_f32_2d(input, "input", self.n_input)
+        y = _as_f32_2d(target, "target", self.n_output)
+        if x.shape[0] != y.shape[0]:
+            raise ValueError("input and target must have matching batch_size")
+        with self._enter("training_step"):
+            res = _lib.StepResult()
+            _lib.check(self._lib.tmnn_training_step(self._h, _ptr(x), _ptr(y), x.shape[0],
+                                                    ctypes.byref(res)))
+            return float(res.loss)
+
+    def training_step_device(self, input_ptr: int, target_ptr: int, n: int,
+                             loss_ptr: int = 0) -> None:
+        """Enqueue one step on device-resident data (no host synchronization)."""
+        self._check_open()
+        _lib.check(self._lib.tmnn_training_step_device(
+            self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(target_ptr), int(n),
+            ctypes.c_void_p(loss_ptr) if loss_ptr else None))
+
+    def inference(self, input) -> np.ndarray:
+        """Evaluate at N positions; returns a fresh (N, n_output) float32 array."""
+        x = _as_f32_2d(input, "input", self.n_input)
+        out = np.empty((x.shape[0], self.n_output), np.float32)
+        with self._enter("inference"):
+            if x.shape[0]:
+                _lib.check(self._lib.tmnn_inference(self._h, _ptr(x), _ptr(out), x.shape[0]))
+        return out
+
+    evaluate = inference
+
+    def inference_device(self, input_ptr: int, output_ptr: int, n: int) -> None:
+        self._check_open()
+        _lib.check(self._lib.tmnn_inference_device(
+            self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(output_ptr), int(n)))
+
+    def synchronize(self) -> None:
+        self._check_open()
+        _lib.check(self._lib.tmnn_synchronize(self._h))
+
+    # ---- split / accumulate path -------------------------------------------
+    def forward_for_training(self, input) -> np.ndarray:
+        x = _as_f32_2d(input, "input", self.n_input)
+        out = np.empty((x.shape[0], self.n_output), np.float32)
+        written = ctypes.c_uint32()
+        with self._enter("forward_for_training"):
+            _lib.check(self._lib.tmnn_forward_for_training(self._h, _ptr(x), _ptr(out),
+                                                           x.shape[0], ctypes.byref(written)))
+        return out[: written.value // self.n_output]
+
+    def zero_gradients(self) -> None:
+        self._check_open()
+        _lib.check(self._lib.tmnn_zero_gradients(self._h))
+
+    def backward_accumulate(self, input, d_output) -> None:
+        x = _as_f32_2d(input, "input", self.n_input)
+        g = _as_f32_2d(d_output, "d_output", self.n_output)
+        if x.shape[0] != g.shape[0]:
+            raise ValueError("input and d_output must have matching batch_size")
+        with self._enter("backward_accumulate"):
+            _lib.check(self._lib.tmnn_backward_accumulate(self._h, _ptr(x), _ptr(g), x.shape[0]))
+
+    def adam_step(self) -> None:
+        self._check_open()
+        _lib.check(self._lib.tmnn_adam_step(self._h))
+
+    # ---- state ---------------------------------------------------------------
+    def get_weights(self) -> tuple[np.ndarray, np.ndarray]:
+        self._check_open()
+        hw = np.empty(self.hash_param_count, np.float32)
+        mw = np.empty(self.mlp_param_count, np.float32)
+        _lib.check(self._lib.tmnn_get_weights(self._h, _ptr(hw), hw.size, _ptr(mw), mw.size))
+        return hw, mw
+
+    def set_initial_weights(self, hash_weights=None, mlp_weights=None) -> None:
+        self._check_open()
+        hp, hn, mp, mn = None, 0, None, 0
+        if hash_weights is not None:
+            hash_weights = np.ascontiguousarray(hash_weights, np.float32).ravel()
+            hp, hn = _ptr(hash_weights), hash_weights.size
+        if mlp_weights is not None:
+            mlp_weights = np.ascontiguousarray(mlp_weights, np.float32).ravel()
+            mp, mn = _ptr(mlp_weights), mlp_weights.size
+        _lib.check(self._lib.tmnn_set_initial_weights(self._h, hp, hn, mp, mn))
+
+    def export_optimizer_state(self) -> OptimizerStateBlob:
+        self._check_open()
+        n = ctypes.c_size_t()
+        ver, st = ctypes.c_uint32(), ctypes.c_uint32()
+        _lib.check(self._lib.tmnn_export_optimizer_state(self._h, ctypes.byref(ver),
+                                                         ctypes.byref(st), None, 0,
+                                                         ctypes.byref(n)))
+        buf = (ctypes.c_uint8 * n.value)()
+        _lib.check(self._lib.tmnn_export_optimizer_state(self._h, ctypes.byref(ver),
+                                                         ctypes.byref(st), buf, n.value,
+                                                         ctypes.byref(n)))
+        return OptimizerStateBlob(ver.value, st.value, bytes(buf))
+
+    def import_optimizer_state(self, blob: OptimizerStateBlob) -> None:
+        self._check_open()
+        data = (ctypes.c_uint8 * len(blob.payload)).from_buffer_copy(blob.payload)
+        _lib.check(self._lib.tmnn_import_optimizer_state(self._h, blob.version, blob.step,
+                                                         data, len(blob.payload)))
+
+    def reset_optimizer(self) -> None:
+        self._check_open()
+        _lib.check(self._lib.tmnn_reset_optimizer(self._h))
+
+    def set_learning_rate(self, lr: float) -> None:
+        self._check_open()
+        _lib.check(self._lib.tmnn_set_learning_rate(self._h, float(lr), float(lr)))
+
+    # ---- inspection hooks (parity tests) --------------------------------------
+    def debug_encode(self, positions, with_corners: bool = False):
+        x = _as_f32_2d(positions, "positions", self.n_input)
+        e = self.config["encoding"]
+        L, F = e["n_levels"], e["n_features_per_level"]
+        C = 1 << self.n_input
+        n = x.shape[0]
+        feats = np.empty((n, L * F), np.float32)
+        idx = np.empty((n, L, C), np.uint32) if with_corners else None
+        w = np.empty((n, L, C), np.float32) if with_corners else None
+        _lib.check(self._lib.tmnn_debug_encode(
+            self._h, _ptr(x), n, _ptr(feats), _ptr(idx) if with_corners else None,
+            _ptr(w) if with_corners else None))
+        return (feats, idx, w) if with_corners else feats
+
+    def debug_gradients(self) -> tuple[np.ndarray, np.ndarray]:
+        self._check_open()
+        gh = np.empty(self.hash_param_count, np.int32)
+        gm = np.empty(self.mlp_param_count, np.float32)
+        _lib.check(self._lib.tmnn_debug_get_gradients(self._h, _ptr(gh), gh.size, _ptr(gm),
+                                                      gm.size))
+        return gh, gm
+
+    def debug_active_mask(self) -> np.ndarray:
+        self._check_open()
+        F = self.config["encoding"]["n_features_per_level"]
+        width = 2 if F == 2 else 1
+        words = (self.hash_param_count // width + 31) // 32
+        out = np.empty(words, np.uint32)
+        _lib.check(self._lib.tmnn_debug_get_active_mask(self._h, _ptr(out), words))
+        return out
+
+    def debug_resolutions(self) -> np.ndarray:
+        self._check_open()
+        L = self.config["encoding"]["n_levels"]
+        out = np.empty(L, np.float32)
+        _lib.check(self._lib.tmnn_debug_get_resolutions(self._h, _ptr(out), L))
+        return out
+
+
+def philox_uniform(seed: int, counter_base: int, count: int, low: float, high: float,
+                   device: int = 0) -> np.ndarray:
+    """The GPU's seeded Philox-4x32-10 uniform fill (weight-init stream)."""
+    ctx = _Context.get(device)
+    out = np.empty(count, np.float32)
+    _lib.check(_lib.load().tmnn_debug_philox_uniform(ctx.handle, seed, counter_base, count,
+                                                     low, high, _ptr(out)))
+    return out
+
+
+__all__ = ["Trainer", "ConfigError", "DTypeError", "ClosedError",
+           "ConcurrentTrainingStepError", "OptimizerStateBlob", "philox_uniform"]
