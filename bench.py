@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""bench.py -- throughput of the neural-field hot path on one MI355X.
+
+Workload ("C2"): the image-fit training step.
+  * 2D multiresolution hash grid: 16 levels x 2 features, T = 2^15 entries per
+    level, base resolution 16, per-level scale 1.5, fp32 table;
+  * MLP 32 -> 64 -> 64 -> 3, ReLU hidden, no output activation, fp16 MFMA
+    operands with fp32 accumulation and fp32 master parameters;
+  * RelativeL2 loss against a seeded procedural 1024x1024 RGB image
+    (8 random-frequency sinusoids + a 32-px checkerboard, in [0, 1]) sampled
+    bilinearly at 2^18 uniform random coordinates per step;
+  * full backward through the MLP and the hash table (int32 fixed-point
+    scatter), then the fused Adam pass (lr 1e-2, b1 0.9, b2 0.99, eps 1e-15).
+One step = Morton sort + fused encode/MLP/loss/backward kernel + dW reduction
++ loss reduction + Adam, all on the library's HIP stream, inputs resident in
+HBM before the timed region starts.
+
+Also reported: inference samples/s on configs[0] ("C1": the same field shape,
+fp32, 2^16 points per call), the dominant kernel's roofline fraction (HIP
+event time of the fused kernel inside the timed region) and the CPU
+restatement of the reference math timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "tiny-metal-nn_amd"))
+
+METRIC = "train samples/s (hash-grid+64w MLP, B=2^18); infer samples/s; % roofline"
+B_TRAIN = 1 << 18
+B_INFER = 1 << 16
+IMG = 1024
+HBM_PEAK_GBS = 8000.0
+
+C2_CONFIG = {
+    "encoding": {"otype": "HashGrid", "n_levels": 16, "n_features_per_level": 2,
+                 "log2_hashmap_size": 15, "base_resolution": 16.0, "per_level_scale": 1.5},
+    "network": {"otype": "FullyFusedMLP", "n_neurons": 64, "n_hidden_layers": 2,
+                "activation": "ReLU", "output_activation": "None"},
+    "loss": {"otype": "RelativeL2"},
+    "optimizer": {"otype": "Adam", "learning_rate": 1e-2, "beta1": 0.9, "beta2": 0.99,
+                  "epsilon": 1e-15},
+    "weight_init": {"seed": 42, "hash_grid_range": 1e-4},
+    "batch_size": B_TRAIN,
+    "mi355x": {"precision": "fp16", "hash_adam": "lazy", "morton_sort": True},
+}
+
+
+def alg_bytes_per_point(d: int, levels: int, feats: int, n_out: int) -> int:
+    """Algorithmic HBM bytes of the fused train kernel per point: position and
+    target reads, the 2^D corner gathers of every level (fp32 features) and one
+    int32 atomic per corner feature of the hash-gradient scatter."""
+    corners = 1 << d
+    return 4 * d + 4 * n_out + 2 * (corners * levels * feats * 4)
+
+
+def make_image(torch, seed: int, device):
+    """Seeded procedural RGB image in [0, 1]: 8 random-frequency sinusoids per
+    channel plus a 32-pixel checkerboard, min-max normalised per channel."""
+    g = torch.Generator().manual_seed(seed)
+    v, u = torch.meshgrid(torch.arange(IMG, dtype=torch.float64) / IMG,
+                          torch.arange(IMG, dtype=torch.float64) / IMG, indexing="ij")
+    chans = []
+    for _ in range(3):
+        acc = torch.zeros(IMG, IMG, dtype=torch.float64)
+        for _ in range(8):
+            amp = 0.5 + 0.5 * torch.rand((), generator=g, dtype=torch.float64)
+            fx, fy = (torch.rand(2, generator=g, dtype=torch.float64) * 80.0 - 40.0)
+            ph = torch.rand((), generator=g, dtype=torch.float64) * 2 * math.pi
+            acc += amp * torch.sin(2 * math.pi * (fx * u + fy * v) + ph)
+        chans.append(acc)
+    img = torch.stack(chans, 0)
+    iy = torch.arange(IMG).view(IMG, 1) // 32
+    ix = torch.arange(IMG).view(1, IMG) // 32
+    img = img + 2.0 * ((ix + iy) % 2).to(torch.float64)
+    lo = img.amin(dim=(1, 2), keepdim=True)
+    hi = img.amax(dim=(1, 2), keepdim=True)
+    img = (img - lo) / (hi - lo)
+    return img.to(torch.float32).to(device)  # [3][H][W]
+
+
+def sample_bilinear(torch, img, pos):
+    """Bilinear image sample at pos in [0,1)^2 (pixel-centre convention)."""
+    grid = (pos * 2.0 - 1.0).view(1, 1, -1, 2)
+    out = torch.nn.functional.grid_sample(img.unsqueeze(0), grid, mode="bilinear",
+                                          padding_mode="border", align_corners=False)
+    return out.view(3, -1).t().contiguous()
+
+
+def cpu_baseline(seconds: float = 12.0) -> dict:
+    """The CPU restatement of the reference math (oracle/, compiled -O3,
+    OpenMP over points) running the same C2 training step on this host, on a
+    bounded sample: batches of 2^16 points (the reference's per-step cap)
+    until `seconds` have elapsed (at least 2 steps)."""
+    sys.path.insert(0, str(REPO / "tests"))
+    from oracle_binding import Oracle  # the checker's binding; CPU baseline only
+
+    o = Oracle()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    e = C2_CONFIG["encoding"]
+    m = o.model(2, e["n_levels"], e["n_features_per_level"], e["log2_hashmap_size"],
+                e["base_resolution"], e["per_level_scale"], 64, 2, 3, "RelativeL2")
+    adam = o.adam(1e-2, 1e-2)
+    hw, mw = o.init_params(m, 42, 1e-4)
+    params = np.concatenate([hw, mw])
+    m1, m2 = np.zeros_like(params), np.zeros_like(params)
+    rng = np.random.default_rng(0)
+    n = 1 << 16
+    pos = rng.random((n, 2), dtype=np.float32)
+    tgt = rng.random((n, 3), dtype=np.float32)
+    o.training_step(m, adam, 0, params, m1, m2, pos, tgt, threads=threads)  # warm
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        o.training_step(m, adam, steps + 1, params, m1, m2, pos, tgt, threads=threads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and steps >= 2) or el >= 2.5 * seconds:
+            break
+    return {"value": n * steps / el, "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} C2 training steps of 2^16 points (reference batch cap) "
+                      f"in {el:.1f} s on {threads} host threads (oracle/, -O3, OpenMP)"}
+
+
+def traffic_from_profiles() -> float | None:
+    """HBM bytes per launch of the fused train kernel from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated)."""
+    f = REPO / "profiles" / "field_train_kernel_c2_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return float(json.loads(f.read_text())["bytes_per_launch"])
+    except (ValueError, KeyError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one "
+              "MI355X (the hot path runs on a single GPU; see the sharding design in "
+              "DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+    from tiny_metal_nn import Trainer
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    img = make_image(torch, 1234, dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    nb = 4
+    xs = [torch.rand(B_TRAIN, 2, device=dev, generator=gen) for _ in range(nb)]
+    ys = [sample_bilinear(torch, img, x) for x in xs]
+    loss_dev = torch.zeros(args.steps + args.warmup + 1, device=dev)
+    torch.cuda.synchronize()
+
+    tr = Trainer.from_config(C2_CONFIG, n_input=2, n_output=3)
+    ins = tr.inspect_runtime()
+    print(f"# trainer: {ins}", file=sys.stderr, flush=True)
+
+    def step(i: int) -> None:
+        tr.training_step_device(xs[i % nb].data_ptr(), ys[i % nb].data_ptr(), B_TRAIN,
+                                loss_dev[i].data_ptr())
+
+    for i in range(args.warmup):
+        step(i)
+    tr.synchronize()
+    torch.cuda.synchronize()
+    print(f"# warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
+
+    tr.set_training_step_profiling(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    tr.synchronize()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    prof = tr.training_step_profile()
+    tr.set_training_step_profiling(False)
+    elapsed = t1 - t0
+    losses = loss_dev.cpu().numpy()
+    first_loss = float(losses[0])
+    last_loss = float(losses[args.warmup + args.steps - 1])
+    if not (math.isfinite(last_loss) and last_loss < first_loss):
+        print(f"bench.py: training did not progress (loss {first_loss} -> {last_loss})",
+              file=sys.stderr)
+        return 1
+    train_sps = B_TRAIN * args.steps / elapsed
+    print(f"# timed {args.steps} steps in {elapsed * 1e3:.1f} ms; loss {first_loss:.5f} -> "
+          f"{last_loss:.5f}; profile {prof}", file=sys.stderr, flush=True)
+
+    # inference on the C1 shape (same field, fp32, 2^16 points per call)
+    xi = torch.rand(B_INFER, 2, device=dev, generator=gen)
+    yi = torch.empty(B_INFER, 3, device=dev)
+    for _ in range(10):
+        tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
+    tr.synchronize()
+    torch.cuda.synchronize()
+    iters = max(50, args.steps)
+    t2 = time.perf_counter()
+    for _ in range(iters):
+        tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
+    tr.synchronize()
+    torch.cuda.synchronize()
+    infer_sps = B_INFER * iters / (time.perf_counter() - t2)
+    tr.close()
+
+    steps_prof = max(1, prof["steps"])
+    k_us = prof["gpu_fwd_bwd_us"] / steps_prof
+    bpp = alg_bytes_per_point(2, 16, 2, 3)
+    achieved = bpp * B_TRAIN / (k_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic_from_profiles(),
+                "kernel": "field_train_kernel<64,32,fp16>",
+                "kernel_avg_us": round(k_us, 2),
+                "alg_bytes_per_point": bpp}
+    phases = {k: round(prof[k] / steps_prof, 2) for k in
+              ("gpu_sort_us", "gpu_fwd_bwd_us", "gpu_reduce_us", "gpu_adam_us",
+               "gpu_total_us")}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(train_sps, 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA (fp32 accumulate) / f32 encode+Adam / i32 hash grads",
+        "data": "synthetic: seeded procedural 1024x1024 RGB image (8 sinusoids + 32-px "
+                "checkerboard) sampled bilinearly at uniform random coords; Philox-seeded "
+                "weights; inputs resident in HBM",
+        "config": {"workload": "C2 image-fit training step (configs[1])",
+                   "batch": B_TRAIN, "encoding": "2D hash grid L16 F2 T2^15 base16 x1.5",
+                   "mlp": "32-64-64-3 ReLU", "loss": "RelativeL2",
+                   "optimizer": "Adam lr1e-2 (lazy hash + dense MLP)",
+                   "parallelism": "single GPU"},
+        "infer_samples_per_s": round(infer_sps, 1),
+        "infer_config": "C1 (configs[0]): same field, fp32, 2^16 points per call",
+        "phase_us_per_step": phases,
+        "loss_first_last": [round(first_loss, 6), round(last_loss, 6)],
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -218,6 +218,26 @@ int tmnn_reset_optimizer(tmnn_trainer *tr);
 int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding,
                            float lr_network);
 
+/* ---- step profiling ------------------------------------------------------------ */
+/* Opt-in GPU timing of the fused step's phases, the GPU-timestamp fields of
+ * TrainingStepProfile (trainer.h:89-133; set_training_step_profiling,
+ * trainer.h:214-217,422-431). While enabled, every training step brackets
+ * each phase with HIP events on the trainer's stream. The profile holds the
+ * sums over all steps since profiling was (re-)enabled; reading it waits for
+ * the stream. gpu_*_us are GPU execution microseconds between events. */
+typedef struct tmnn_step_profile {
+  uint32_t steps;             /* profiled steps summed below */
+  uint32_t batch_size;        /* points of the last profiled step */
+  double gpu_sort_us;         /* Morton codes + radix sort + gather */
+  double gpu_fwd_bwd_us;      /* the fused field kernel (encode..scatter) */
+  double gpu_reduce_us;       /* dW partial reduction + loss reduction */
+  double gpu_adam_us;         /* fused Adam pass (+ mask/grad clearing) */
+  double gpu_total_us;        /* first event to last event, summed */
+} tmnn_step_profile;
+
+int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled);
+int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
+
 /* ---- inspection hooks of the path (used by the parity tests) --------------- */
 /* Encode forward only (emitHashEncodeUnified, mlp_kernel_emitter.cpp:
  * 205-360): features [N][L*F] fp32; corner_index / corner_weight (nullable)

@@ -118,3 +118,25 @@ def test_model_desc_from_config():
     assert d.lr_encoding == pytest.approx(1e-2) and d.lr_network == pytest.approx(1e-2)
     assert d.loss_kind == _lib.LOSS_RELATIVE_L2 and d.batch_size == 262144
     assert d.precision == _lib.PRECISION_FP16 and d.hash_adam_mode == _lib.HASH_ADAM_DENSE
+
+
+def test_call_guard_releases_and_rejects_concurrent_entry():
+    """The single-caller guard (tmnn_pybind.cpp:366-375) is released after each
+    call and a second entry while held raises instead of blocking."""
+    import threading
+
+    from tiny_metal_nn import ConcurrentTrainingStepError, Trainer
+    tr = object.__new__(Trainer)
+    tr._busy = threading.Lock()
+    tr._closed = False
+    for _ in range(3):
+        with tr._enter("training_step"):
+            with pytest.raises(ConcurrentTrainingStepError):
+                with tr._enter("inference"):
+                    pass
+    assert not tr._busy.locked()
+    with pytest.raises(RuntimeError):
+        with tr._enter("training_step"):
+            raise RuntimeError("boom")
+    assert not tr._busy.locked()
+    tr._closed = True

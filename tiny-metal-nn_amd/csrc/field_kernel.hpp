@@ -55,6 +55,7 @@ struct FieldArgs {
   float loss_scale;         // power of two applied to d_out in the fp16 path
   float inv_loss_scale;
   int32_t lift2d_mask;      // mark the lifted z=1 corners of 2D points
+  int32_t dw_global;        // dW accumulator in grad_partials (LDS too small)
   int32_t mlp_count;
   float res[kMaxLevels];    // per-level resolution table
   const float *pos;         // [n][D]
@@ -74,6 +75,7 @@ struct FieldArgs {
 // arrays, which would live in scratch memory on the device).
 struct FieldLayout {
   int32_t INP, HP, IN, H, NHL, M, es, okt;  // okt: K width of output-layer bwd
+  int32_t lo_base;              // fp16: LDS bytes of the forward low-part fragments
   int32_t bwd_base, bias_base;
   int32_t res_off;              // LDS bytes: fp32 resolution table
   int32_t dw_off;               // LDS bytes: fp32 dW accumulator
@@ -81,6 +83,7 @@ struct FieldLayout {
   int32_t wave_off;             // LDS bytes: first wave's activation region
   int32_t wave_bytes;
   int32_t xs_off, hs_off, ds_off;  // within a wave region
+  int32_t dw_global;            // 1: dW accumulates in the block's global partial row
   int32_t total;
 
   // LDS bytes of the forward A fragments (W_k^T) of layer k (k == NHL: output)
@@ -88,6 +91,8 @@ struct FieldLayout {
     if (k == 0) return 0;
     return INP * HP * es + (k - 1) * HP * HP * es;
   }
+  // LDS bytes of the forward low-part fragments fp16(W - fp16(W)) of layer k
+  __host__ __device__ int32_t fwd_lo_off(int k) const { return lo_base + fwd_off(k); }
   // LDS bytes of the backward A fragments (W_k) of layer k
   __host__ __device__ int32_t bwd_off(int k) const {
     if (k == 0) return bwd_base;
@@ -113,14 +118,18 @@ __host__ __device__ inline int32_t round_up(int32_t v, int32_t m) {
 __host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
                                                    int H, int NHL, int M,
                                                    int mlp_count, bool f16,
-                                                   bool train, int wpb) {
+                                                   bool train, int wpb,
+                                                   bool dw_global = false) {
   FieldLayout s;
   s.INP = INP; s.HP = HP; s.IN = IN; s.H = H; s.NHL = NHL; s.M = M;
   s.es = f16 ? 2 : 4;
   s.okt = f16 ? 32 : 16;
   const int fwd_bytes = (INP * HP + (NHL - 1) * HP * HP + HP * 16) * s.es;
   const int bwd_bytes = (INP * HP + (NHL - 1) * HP * HP + HP * s.okt) * s.es;
-  int off = fwd_bytes;
+  // fp16: the forward runs on split operands (hi + lo halves, three MFMAs per
+  // product), so the low-part fragments follow the high-part ones.
+  s.lo_base = fwd_bytes;
+  int off = f16 ? 2 * fwd_bytes : fwd_bytes;
   s.bwd_base = off;
   if (train) off += bwd_bytes;
   s.bias_base = off;
@@ -128,7 +137,8 @@ __host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
   s.res_off = off;
   off += kMaxLevels * 4;
   s.dw_off = off;
-  if (train) off += round_up(mlp_count, 4) * 4;
+  s.dw_global = dw_global ? 1 : 0;
+  if (train && !dw_global) off += round_up(mlp_count, 4) * 4;
   s.red_off = off;
   off += round_up(wpb, 4) * 4;
   off = round_up(off, 16);
@@ -217,6 +227,70 @@ __device__ __forceinline__ void layer_mma(const unsigned char *frag,
       for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
     }
   }
+}
+
+// fp16 split of two D-layout tiles: hi = fp16(v), lo = fp16(v - hi). hi*hi
+// products are exact in the fp32 accumulator and hi + lo carries ~22 bits.
+__device__ __forceinline__ void pack8_split(f32x4 a, f32x4 b, half8 &hi, half8 &lo) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const _Float16 ha = static_cast<_Float16>(a[r]);
+    const _Float16 hb = static_cast<_Float16>(b[r]);
+    hi[r] = ha;
+    hi[r + 4] = hb;
+    lo[r] = static_cast<_Float16>(a[r] - static_cast<float>(ha));
+    lo[r + 4] = static_cast<_Float16>(b[r] - static_cast<float>(hb));
+  }
+}
+
+// Forward layer on split fp16 operands: out = A x in with A = Ahi + Alo and
+// in = Bhi + Blo, accumulated as Alo*Bhi + Ahi*Blo + Ahi*Bhi in fp32 (the
+// dropped Alo*Blo term is ~2^-22 relative). Keeps the fp16 training forward
+// within fp32 rounding of the reference's fp32 math.
+template <int KT, int MT>
+__device__ __forceinline__ void layer_mma_split(const unsigned char *frag_hi,
+                                                const unsigned char *frag_lo,
+                                                const f32x4 (&in)[KT][kNT],
+                                                f32x4 (&out)[MT][kNT], int lane) {
+  static_assert(KT % 2 == 0, "fp16 K tiles come in pairs");
+  constexpr int KS = KT / 2;
+  half8 bh[KS][kNT], bl[KS][kNT];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+      pack8_split(in[2 * ks][nt], in[2 * ks + 1][nt], bh[ks][nt], bl[ks][nt]);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4 acc[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = ((mt * KS + ks) * 64 + lane) * 16;
+      const half8 ah = *reinterpret_cast<const half8 *>(frag_hi + off);
+      const half8 al = *reinterpret_cast<const half8 *>(frag_lo + off);
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[ks][nt], acc[nt], 0, 0, 0);
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[ks][nt], acc[nt], 0, 0, 0);
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[ks][nt], acc[nt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
+  }
+}
+
+// Forward layer in the kernel's precision: fp32 MFMA, or split fp16.
+template <bool F16, int KT, int MT>
+__device__ __forceinline__ void layer_fwd(const FieldLayout &s, const unsigned char *smem,
+                                          int k, const f32x4 (&in)[KT][kNT],
+                                          f32x4 (&out)[MT][kNT], int lane) {
+  if constexpr (F16)
+    layer_mma_split<KT, MT>(smem + s.fwd_off(k), smem + s.fwd_lo_off(k), in, out, lane);
+  else
+    layer_mma<false, KT, MT>(smem + s.fwd_off(k), in, out, lane);
 }
 
 // One 16x16 tile of dW^T = sum over the 32 tile points of
@@ -566,10 +640,14 @@ __device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLay
         o = 16 * mt + (lane & 15);
       }
       const float v = (i < kreal && o < mreal) ? W[i * mreal + o] : 0.0f;
-      if constexpr (F16)
-        reinterpret_cast<_Float16 *>(smem + s.fwd_off(k))[e] = static_cast<_Float16>(v);
-      else
+      if constexpr (F16) {
+        const _Float16 hi = static_cast<_Float16>(v);
+        reinterpret_cast<_Float16 *>(smem + s.fwd_off(k))[e] = hi;
+        reinterpret_cast<_Float16 *>(smem + s.fwd_lo_off(k))[e] =
+            static_cast<_Float16>(v - static_cast<float>(hi));
+      } else {
         reinterpret_cast<float *>(smem + s.fwd_off(k))[e] = v;
+      }
     }
     if constexpr (TRAIN) {
       // backward: A = W_k, rows = input units, K = output units
@@ -602,9 +680,14 @@ __device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLay
   for (int e = tid; e < kMaxLevels; e += nthr)
     reinterpret_cast<float *>(smem + s.res_off)[e] = e < a.L ? a.res[e] : 0.0f;
   if constexpr (TRAIN) {
-    const int nd = round_up(a.mlp_count, 4);
-    for (int e = tid; e < nd; e += nthr)
-      reinterpret_cast<float *>(smem + s.dw_off)[e] = 0.0f;
+    if (s.dw_global) {
+      float *dwg = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+      for (int e = tid; e < a.mlp_count; e += nthr) dwg[e] = 0.0f;
+    } else {
+      const int nd = round_up(a.mlp_count, 4);
+      for (int e = tid; e < nd; e += nthr)
+        reinterpret_cast<float *>(smem + s.dw_off)[e] = 0.0f;
+    }
   }
 }
 
@@ -651,7 +734,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   extern __shared__ __align__(16) unsigned char smem[];
 
   const FieldLayout s = make_layout(INP, HP, a.IN, a.H, a.NHL, a.M,
-                                    a.mlp_count, F16, TRAIN, a.waves_per_block);
+                                    a.mlp_count, F16, TRAIN, a.waves_per_block,
+                                    a.dw_global != 0);
   stage_weights<HP, INP, F16, TRAIN>(a, s, smem);
   __syncthreads();
 
@@ -660,7 +744,11 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   const int p = lane & 15;
   const int q = lane >> 4;
   const float *res = reinterpret_cast<const float *>(smem + s.res_off);
-  float *dw = reinterpret_cast<float *>(smem + s.dw_off);
+  // dW accumulator: LDS, or (when the model leaves no room) this block's row
+  // of grad_partials, which the block zeroed in stage_weights.
+  float *dw = s.dw_global
+                  ? a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count
+                  : reinterpret_cast<float *>(smem + s.dw_off);
   unsigned char *wb = smem + s.wave_off + wave * s.wave_bytes;
   unsigned char *Xs = wb + s.xs_off;
   unsigned char *Hs = wb + s.hs_off;
@@ -689,11 +777,11 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 
     // ---- MLP forward
     f32x4 act[HT][kNT];
-    layer_mma<F16, KT0, HT>(smem + s.fwd_off(0), X, act, lane);
+    layer_fwd<F16, KT0, HT>(s, smem, 0, X, act, lane);
     for (int k = 0; k < a.NHL; ++k) {
       if (k > 0) {
         f32x4 nxt[HT][kNT];
-        layer_mma<F16, HT, HT>(smem + s.fwd_off(k), act, nxt, lane);
+        layer_fwd<F16, HT, HT>(s, smem, k, act, nxt, lane);
 #pragma unroll
         for (int mt = 0; mt < HT; ++mt)
 #pragma unroll
@@ -712,7 +800,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       if constexpr (TRAIN) store_tiles<F16, HT>(Hs + k * hs_layer_bytes, act, p, q);
     }
     f32x4 y[1][kNT];
-    layer_mma<F16, HT, 1>(smem + s.fwd_off(a.NHL), act, y, lane);
+    layer_fwd<F16, HT, 1>(s, smem, a.NHL, act, y, lane);
     {
       const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(a.NHL));
 #pragma unroll
@@ -927,8 +1015,10 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       for (int w = 0; w < a.waves_per_block; ++w) t += red[w];
       a.loss_partials[blockIdx.x] = t;
     }
-    float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
-    for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = dw[e];
+    if (!s.dw_global) {
+      float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+      for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = dw[e];
+    }
   }
 }
 

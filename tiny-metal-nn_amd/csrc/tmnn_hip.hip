@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -108,6 +109,7 @@ struct KernelPlan {
   FieldKernel fn = nullptr;
   int wpb = 0;          // waves per block
   int lds = 0;          // dynamic LDS bytes
+  bool dw_global = false;  // dW accumulator outside LDS
   int max_blocks = 0;   // resident blocks on the whole device
 };
 
@@ -136,6 +138,21 @@ struct tmnn_trainer {
   DevBuf dbg_a, dbg_b, dbg_c;
 
   KernelPlan train_plan, fwd_plan, infer_plan;
+
+  // Step profiling: one set of phase events per profiled step, summed and
+  // recycled when the profile is read.
+  static constexpr int kProfEvents = 5;  // sort | fwd/bwd | reduce | adam |
+  bool profiling = false;
+  std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
+  size_t prof_used = 0;
+  int prof_cur = -1;  // event set of the step being enqueued, or -1
+  tmnn_step_profile prof_acc{};
+
+  ~tmnn_trainer() {
+    for (auto &set : prof_events)
+      for (hipEvent_t e : set)
+        if (e) (void)hipEventDestroy(e);
+  }
 };
 
 namespace {
@@ -171,17 +188,64 @@ bool desc_ok(const tmnn_model_desc *d, std::string &why) {
   return true;
 }
 
+// Claims the next event set for a profiled step (prof_cur = -1 when off).
+int prof_begin_step(tmnn_trainer *tr) {
+  tr->prof_cur = -1;
+  if (!tr->profiling) return TMNN_OK;
+  if (tr->prof_used == tr->prof_events.size()) {
+    std::array<hipEvent_t, tmnn_trainer::kProfEvents> set{};
+    for (hipEvent_t &e : set) TMNN_HIP_TRY(hipEventCreate(&e));
+    tr->prof_events.push_back(set);
+  }
+  tr->prof_cur = static_cast<int>(tr->prof_used++);
+  return TMNN_OK;
+}
+
+// Records phase boundary k of the current profiled step.
+int prof_mark(tmnn_trainer *tr, int k) {
+  if (tr->prof_cur < 0) return TMNN_OK;
+  TMNN_HIP_TRY(hipEventRecord(tr->prof_events[tr->prof_cur][k], tr->ctx->stream));
+  return TMNN_OK;
+}
+
+// Folds every recorded step into prof_acc and recycles the event sets.
+int prof_collect(tmnn_trainer *tr) {
+  if (tr->prof_used == 0) return TMNN_OK;
+  TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  for (size_t i = 0; i < tr->prof_used; ++i) {
+    const auto &e = tr->prof_events[i];
+    float ms[tmnn_trainer::kProfEvents - 1];
+    for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k)
+      TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[k], e[k + 1]));
+    tr->prof_acc.gpu_sort_us += 1e3 * ms[0];
+    tr->prof_acc.gpu_fwd_bwd_us += 1e3 * ms[1];
+    tr->prof_acc.gpu_reduce_us += 1e3 * ms[2];
+    tr->prof_acc.gpu_adam_us += 1e3 * ms[3];
+    tr->prof_acc.gpu_total_us += 1e3 * (ms[0] + ms[1] + ms[2] + ms[3]);
+    tr->prof_acc.steps += 1;
+  }
+  tr->prof_used = 0;
+  return TMNN_OK;
+}
+
 int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
   out.fn = select_kernel(tr->HP, tr->INP, f16, train);
   if (!out.fn) return fail(TMNN_ERR_UNSUPPORTED, "no kernel for this geometry");
-  int wpb = 4;
-  for (; wpb >= 1; --wpb) {
-    const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
-                                      tr->d.num_hidden_layers, tr->d.num_outputs,
-                                      static_cast<int>(tr->mlp_count), f16, train, wpb);
-    if (s.total <= kMaxLdsBytes) {
-      out.lds = s.total;
-      break;
+  // Most waves per block whose LDS plan fits; failing that, move the dW
+  // accumulator out of LDS (global float atomics into the block's row).
+  int wpb = 0;
+  for (int dwg = 0; dwg <= (train ? 1 : 0) && wpb == 0; ++dwg) {
+    for (int w = 4; w >= 1; --w) {
+      const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
+                                        tr->d.num_hidden_layers, tr->d.num_outputs,
+                                        static_cast<int>(tr->mlp_count), f16, train, w,
+                                        dwg != 0);
+      if (s.total <= kMaxLdsBytes) {
+        out.lds = s.total;
+        out.dw_global = dwg != 0;
+        wpb = w;
+        break;
+      }
     }
   }
   if (wpb < 1) return fail(TMNN_ERR_UNSUPPORTED, "model does not fit in LDS");
@@ -225,6 +289,7 @@ int launch_field(tmnn_trainer *tr, const KernelPlan &plan, FieldArgs a, int n) {
   a.n = n;
   a.n_tiles = (n + kTilePts - 1) / kTilePts;
   a.waves_per_block = plan.wpb;
+  a.dw_global = plan.dw_global ? 1 : 0;
   const int need = (a.n_tiles + plan.wpb - 1) / plan.wpb;
   const int blocks = std::max(1, std::min(need, plan.max_blocks));
   hipLaunchKernelGGL(plan.fn, dim3(blocks), dim3(64 * plan.wpb), plan.lds,
@@ -298,8 +363,11 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   const bool f16 = tr->d.precision == TMNN_PRECISION_FP16;
   const float *pos = d_pos, *tgt = d_tgt;
   const uint32_t *perm = nullptr;
-  int rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm);
+  int rc = prof_mark(tr, 0);
   if (rc != TMNN_OK) return rc;
+  rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm);
+  if (rc != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 1)) != TMNN_OK) return rc;
   FieldArgs a = base_args(tr);
   a.mode = external_grad ? kModeTrainExtGrad : kModeTrainLoss;
   a.inv_n = 1.0f / static_cast<float>(n);
@@ -311,6 +379,7 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   a.loss_partials = tr->loss_partials.as<float>();
   const int blocks = launch_field(tr, tr->train_plan, a, n);
   if (blocks < 0) return blocks;
+  if ((rc = prof_mark(tr, 2)) != TMNN_OK) return rc;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + 255) / 256), dim3(256), 0,
                      tr->ctx->stream, tr->partials.as<float>(), blocks,
                      static_cast<int32_t>(tr->mlp_count), tr->grad_mlp.as<float>());
@@ -359,14 +428,19 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
 
 int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, int n,
                       float *d_loss) {
+  int rc = prof_begin_step(tr);
+  if (rc != TMNN_OK) return rc;
   const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false);
   if (blocks < 0) return blocks;
   hipLaunchKernelGGL(loss_reduce_kernel, dim3(1), dim3(64), 0, tr->ctx->stream,
                      tr->loss_partials.as<float>(), blocks, 0.0f, n,
                      d_loss ? d_loss : tr->loss_out.as<float>());
   TMNN_HIP_TRY(hipGetLastError());
-  const int rc = run_adam(tr, true, true);
-  if (rc != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
+  if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
+  if (tr->prof_cur >= 0) tr->prof_acc.batch_size = static_cast<uint32_t>(n);
+  tr->prof_cur = -1;
   ++tr->step;
   return TMNN_OK;
 }
@@ -442,6 +516,7 @@ uint32_t get_u32(const uint8_t *p) {
   return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) |
          (static_cast<uint32_t>(p[2]) << 16) | (static_cast<uint32_t>(p[3]) << 24);
 }
+
 
 }  // namespace
 
@@ -771,6 +846,7 @@ int tmnn_backward_accumulate(tmnn_trainer *tr, const float *input, const float *
   TMNN_HIP_TRY(hipMemcpyAsync(tr->in_tgt.ptr, d_output,
                               static_cast<size_t>(bn) * tr->d.num_outputs * sizeof(float),
                               hipMemcpyHostToDevice, st));
+  tr->prof_cur = -1;  // only fused steps are profiled
   const int blocks = run_forward_backward(tr, tr->in_pos.as<float>(), tr->in_tgt.as<float>(), bn,
                                           true);
   if (blocks < 0) return blocks;
@@ -942,6 +1018,25 @@ int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding, float lr_network
   if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
   tr->lr_enc = lr_encoding;
   tr->lr_net = lr_network;
+  return TMNN_OK;
+}
+
+int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int rc = prof_collect(tr);  // drop what an earlier window recorded
+  if (rc != TMNN_OK) return rc;
+  tr->prof_acc = tmnn_step_profile{};
+  tr->profiling = enabled != 0;
+  return TMNN_OK;
+}
+
+int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int rc = prof_collect(tr);
+  if (rc != TMNN_OK) return rc;
+  *out = tr->prof_acc;
   return TMNN_OK;
 }
 

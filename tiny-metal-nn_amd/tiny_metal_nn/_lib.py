@@ -83,6 +83,18 @@ class Inspection(ctypes.Structure):
     ]
 
 
+class StepProfile(ctypes.Structure):
+    _fields_ = [
+        ("steps", ctypes.c_uint32),
+        ("batch_size", ctypes.c_uint32),
+        ("gpu_sort_us", ctypes.c_double),
+        ("gpu_fwd_bwd_us", ctypes.c_double),
+        ("gpu_reduce_us", ctypes.c_double),
+        ("gpu_adam_us", ctypes.c_double),
+        ("gpu_total_us", ctypes.c_double),
+    ]
+
+
 _V = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _U32 = ctypes.c_uint32
@@ -120,6 +132,8 @@ SIGNATURES = {
     "tmnn_import_optimizer_state": (ctypes.c_int, [_V, _U32, _U32, _V, _SZ]),
     "tmnn_reset_optimizer": (ctypes.c_int, [_V]),
     "tmnn_set_learning_rate": (ctypes.c_int, [_V, _F, _F]),
+    "tmnn_set_step_profiling": (ctypes.c_int, [_V, _I32]),
+    "tmnn_get_step_profile": (ctypes.c_int, [_V, ctypes.POINTER(StepProfile)]),
     "tmnn_debug_encode": (ctypes.c_int, [_V, _V, _I32, _V, _V, _V]),
     "tmnn_debug_get_gradients": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
     "tmnn_debug_get_active_mask": (ctypes.c_int, [_V, _V, _SZ]),

@@ -10,6 +10,7 @@ callers whose batches already live in GPU memory.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
 from dataclasses import dataclass
@@ -142,13 +143,19 @@ class Trainer:
         if self._closed:
             raise ClosedError("Trainer is closed")
 
+    @contextlib.contextmanager
     def _enter(self, what: str):
+        """Hold the single-caller guard for one call (tmnn_pybind.cpp:366-375):
+        a second thread entering meanwhile gets ConcurrentTrainingStepError."""
         self._check_open()
         if not self._busy.acquire(blocking=False):
             raise ConcurrentTrainingStepError(
                 f"{what} is already in progress on another thread. tmnn.Trainer is "
                 "single-threaded; use one Trainer per thread.")
-        return self._busy
+        try:
+            yield
+        finally:
+            self._busy.release()
 
     # ---- accessors ----------------------------------------------------------
     def step(self) -> int:
@@ -279,6 +286,19 @@ class Trainer:
     def set_learning_rate(self, lr: float) -> None:
         self._check_open()
         _lib.check(self._lib.tmnn_set_learning_rate(self._h, float(lr), float(lr)))
+
+    # ---- step profiling (TrainingStepProfile GPU timestamps) -------------------
+    def set_training_step_profiling(self, enabled: bool) -> None:
+        """Enable/disable per-phase GPU event timing of fused steps; resets the sums."""
+        self._check_open()
+        _lib.check(self._lib.tmnn_set_step_profiling(self._h, 1 if enabled else 0))
+
+    def training_step_profile(self) -> dict:
+        """Per-phase GPU microseconds summed over the profiled steps."""
+        self._check_open()
+        p = _lib.StepProfile()
+        _lib.check(self._lib.tmnn_get_step_profile(self._h, ctypes.byref(p)))
+        return {k: getattr(p, k) for k, _ in _lib.StepProfile._fields_}
 
     # ---- inspection hooks (parity tests) --------------------------------------
     def debug_encode(self, positions, with_corners: bool = False):
