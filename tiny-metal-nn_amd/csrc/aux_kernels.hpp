@@ -83,14 +83,14 @@ struct AdamArgs {
   float *v;
   int32_t *grad_hash;       // [hash] int32 fixed point
   float *grad_mlp;          // [mlp]
-  uint32_t *mask;           // lazy mask words (nullable => dense hash)
-  uint32_t hash_count;
+  uint8_t *mask;            // per-entry visit flags
+  int32_t lazy;             // 1: update visited entries only; 0: every entry
+  uint32_t hash_entries;    // L * T (hash floats = hash_entries * F)
   uint32_t mlp_count;
-  uint32_t slot_shift;      // 1 when F == 2 (entry pairs), else 0
   float lr_hash, lr_mlp, beta1, beta2, eps, bc1, bc2;
   float l1_hash, l2_mlp, grad_clip, weight_decay;
   int32_t clear_grads;      // zero consumed gradients (fused step)
-  int32_t clear_mask;       // zero consumed mask words
+  int32_t clear_mask;       // zero consumed visit flags
 };
 
 // One Adam element (adam_kernel_msl.h:67-108, :137-163, :183-202).
@@ -114,44 +114,55 @@ __device__ __forceinline__ void adam_update(float &w, float &mo, float &ve,
   w = w - (lr * mh) / (sqrtf(vh) + a.eps);
 }
 
-// One pass over [hash | mlp]. Thread i owns element i. With a mask, hash
-// element i is updated only if its slot (i >> slot_shift) is marked: the
-// lazy sparse semantics of neural_sdf_adam_hash_sparse without the host-side
-// compaction. A mask word covers 32 slots = 32 << slot_shift consecutive
-// elements, which always lie in one 64-lane wave (blocks are multiples of 64
-// and start at multiples of 64), so every reader of a word loads it in the
-// same instruction before the word's first lane clears it.
+// One pass over [hash entries | mlp params]. Thread j < hash_entries owns
+// table entry j (its F floats); in lazy mode the entry is updated only if its
+// visit flag is set -- the lazy sparse semantics of
+// neural_sdf_adam_hash_sparse (adam_kernel_msl.h:120-164) without the host
+// compaction (default_trainer.cpp:1882-1960). Threads past the table own one
+// MLP parameter each (neural_sdf_adam_mlp_dense, adam_kernel_msl.h:166-203).
+template <int F>
 __global__ void adam_kernel(AdamArgs a) {
-  const uint32_t total = a.hash_count + a.mlp_count;
+  const uint32_t total = a.hash_entries + a.mlp_count;
   const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    if (i < a.hash_count) {
-      bool active = true;
-      if (a.mask) {
-        const uint32_t slot = i >> a.slot_shift;
-        const uint32_t word = a.mask[slot >> 5];
-        active = (word >> (slot & 31u)) & 1u;
-        if (a.clear_mask && (i & ((32u << a.slot_shift) - 1u)) == 0u && word != 0u)
-          a.mask[slot >> 5] = 0u;
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < total; j += stride) {
+    if (j < a.hash_entries) {
+      const bool visited = a.mask[j] != 0;
+      if (visited && a.clear_mask) a.mask[j] = 0;
+      if (a.lazy && !visited) continue;
+#pragma unroll
+      for (int f = 0; f < F; ++f) {
+        const size_t i = static_cast<size_t>(j) * F + f;
+        const float g = static_cast<float>(a.grad_hash[i]) * (1.0f / 65536.0f);
+        float w = a.params[i], mo = a.m[i], ve = a.v[i];
+        adam_update(w, mo, ve, g, a.lr_hash, a, false);
+        a.params[i] = w;
+        a.m[i] = mo;
+        a.v[i] = ve;
+        if (a.clear_grads) a.grad_hash[i] = 0;
       }
-      if (!active) continue;
-      const float g = static_cast<float>(a.grad_hash[i]) * (1.0f / 65536.0f);
-      float w = a.params[i], mo = a.m[i], ve = a.v[i];
-      adam_update(w, mo, ve, g, a.lr_hash, a, false);
-      a.params[i] = w;
-      a.m[i] = mo;
-      a.v[i] = ve;
-      if (a.clear_grads) a.grad_hash[i] = 0;
     } else {
-      const uint32_t j = i - a.hash_count;
+      const uint32_t k = j - a.hash_entries;
+      const size_t i = static_cast<size_t>(a.hash_entries) * F + k;
       float w = a.params[i], mo = a.m[i], ve = a.v[i];
-      adam_update(w, mo, ve, a.grad_mlp[j], a.lr_mlp, a, true);
+      adam_update(w, mo, ve, a.grad_mlp[k], a.lr_mlp, a, true);
       a.params[i] = w;
       a.m[i] = mo;
       a.v[i] = ve;
-      if (a.clear_grads) a.grad_mlp[j] = 0.0f;
+      if (a.clear_grads) a.grad_mlp[k] = 0.0f;
     }
   }
+}
+
+// dst[0 .. n) = 0 in 16-byte stores (a kernel rather than hipMemsetAsync, so
+// a caller may capture the step in a HIP graph).
+__global__ void zero_bytes_kernel(uint8_t *dst, size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  const size_t n16 = n / 16;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+    reinterpret_cast<uint4 *>(dst)[i] = make_uint4(0u, 0u, 0u, 0u);
+  for (size_t i = n16 * 16 + static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride)
+    dst[i] = 0;
 }
 
 // loss = (sum over block partials, ascending) / N, written to *out.

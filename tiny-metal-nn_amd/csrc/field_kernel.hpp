@@ -65,7 +65,7 @@ struct FieldArgs {
   float *out;               // [n][M] (Forward)
   const uint32_t *out_index;// nullable: row of out[] for point i
   int32_t *grad_hash;       // [L][T][F] int32 fixed point
-  uint32_t *mask;           // lazy-Adam mask words
+  uint8_t *mask;            // lazy-Adam visit flags, one byte per table entry
   float *grad_partials;     // [gridDim.x][mlp_count]
   float *loss_partials;     // [gridDim.x]
 };
@@ -474,14 +474,18 @@ __device__ __forceinline__ void encode_tile(const FieldArgs &a, const float *res
   }
 }
 
-__device__ __forceinline__ void mark_slot(uint32_t *mask, size_t slot) {
-  atomicOr(mask + (slot >> 5), 1u << static_cast<uint32_t>(slot & 31u));
+// Visit flag of one table entry: a plain byte store. Every writer stores the
+// same value, so concurrent marks need no atomics (the reference's bit-mask
+// atomic_fetch_or, mlp_kernel_emitter.cpp:48-71, marks the same set: all F
+// floats of every visited corner, zero-weight corners included).
+__device__ __forceinline__ void mark_entry(uint8_t *mask, size_t entry) {
+  mask[entry] = 1;
 }
 
 // Gradient scatter of one level: int32((d * w) * 65536) per corner and
 // feature on the reference's float2 path (F == 2, 2D/3D), else
-// int32(d * wx * wy * wz (* wt) * 65536); every visited corner marks the
-// lazy-Adam mask (entry pairs for F == 2, single floats otherwise).
+// int32(d * wx * wy * wz (* wt) * 65536); every visited corner sets its
+// entry's lazy-Adam visit flag.
 template <int D, int F>
 __device__ __forceinline__ void scatter_level(const FieldArgs &a, int l,
                                               const float *p, float res,
@@ -511,22 +515,9 @@ __device__ __forceinline__ void scatter_level(const FieldArgs &a, int l,
       const int32_t ci = f2i_trunc(v * kGradScale);
       if (ci != 0) atomicAdd(a.grad_hash + entry * F + f, ci);
     }
-    if constexpr (F == 2) {
-      mark_slot(a.mask, entry);
-    } else {
-#pragma unroll
-      for (int f = 0; f < F; ++f) mark_slot(a.mask, entry * F + f);
-    }
+    mark_entry(a.mask, entry);
     if constexpr (D == 2) {
-      if (a.lift2d_mask) {
-        const size_t e1 = lbase + hash_corner_lift_z1(co, tmask);
-        if constexpr (F == 2) {
-          mark_slot(a.mask, e1);
-        } else {
-#pragma unroll
-          for (int f = 0; f < F; ++f) mark_slot(a.mask, e1 * F + f);
-        }
-      }
+      if (a.lift2d_mask) mark_entry(a.mask, lbase + hash_corner_lift_z1(co, tmask));
     }
   }
 }

@@ -20,7 +20,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/tmnn_hip.h"
+#include "tmnn_hip.h"
 #include "aux_kernels.hpp"
 #include "field_kernel.hpp"
 #include "sort.hpp"
@@ -127,7 +127,9 @@ struct tmnn_trainer {
   tmnn_context *ctx = nullptr;
   tmnn_model_desc d{};
   int IN = 0, INP = 0, HP = 0;
-  uint32_t hash_count = 0, mlp_count = 0, mask_words = 0;
+  uint32_t hash_count = 0, mlp_count = 0;
+  uint32_t hash_entries = 0;  // L * T: one visit flag byte each
+  uint32_t mask_words = 0;    // words of the reference's bit-mask layout (debug view)
   float res[kMaxLevels] = {};
   uint32_t step = 0;
   float lr_enc = 0.f, lr_net = 0.f;
@@ -281,7 +283,7 @@ FieldArgs base_args(const tmnn_trainer *tr) {
   a.table = tr->params.as<float>();
   a.mlp = tr->params.as<float>() + tr->hash_count;
   a.grad_hash = tr->grad_hash.as<int32_t>();
-  a.mask = tr->mask.as<uint32_t>();
+  a.mask = tr->mask.as<uint8_t>();
   return a;
 }
 
@@ -395,11 +397,10 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
   a.grad_hash = tr->grad_hash.as<int32_t>();
   a.grad_mlp = tr->grad_mlp.as<float>();
   // Sparse hash Adam needs l1_reg == 0 (default_trainer.cpp:1868-1876).
-  const bool lazy = tr->d.hash_adam_mode == TMNN_HASH_ADAM_LAZY && tr->d.l1_reg == 0.0f;
-  a.mask = lazy ? tr->mask.as<uint32_t>() : nullptr;
-  a.hash_count = tr->hash_count;
+  a.lazy = (tr->d.hash_adam_mode == TMNN_HASH_ADAM_LAZY && tr->d.l1_reg == 0.0f) ? 1 : 0;
+  a.mask = tr->mask.as<uint8_t>();
+  a.hash_entries = tr->hash_entries;
   a.mlp_count = tr->mlp_count;
-  a.slot_shift = tr->d.features_per_level == 2 ? 1u : 0u;
   a.lr_hash = tr->lr_enc;
   a.lr_mlp = tr->lr_net;
   a.beta1 = tr->d.beta1;
@@ -415,14 +416,26 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
   a.weight_decay = tr->d.weight_decay;
   a.clear_grads = clear_grads ? 1 : 0;
   a.clear_mask = clear_mask ? 1 : 0;
-  const uint32_t total = tr->hash_count + tr->mlp_count;
+  const uint32_t total = tr->hash_entries + tr->mlp_count;
   const uint32_t blocks = std::min<uint32_t>((total + 255) / 256,
                                              static_cast<uint32_t>(tr->ctx->cu_count) * 16u);
-  hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, tr->ctx->stream, a);
+  switch (tr->d.features_per_level) {
+    case 1: hipLaunchKernelGGL(adam_kernel<1>, dim3(blocks), dim3(256), 0, tr->ctx->stream, a); break;
+    case 2: hipLaunchKernelGGL(adam_kernel<2>, dim3(blocks), dim3(256), 0, tr->ctx->stream, a); break;
+    default: hipLaunchKernelGGL(adam_kernel<4>, dim3(blocks), dim3(256), 0, tr->ctx->stream, a); break;
+  }
   TMNN_HIP_TRY(hipGetLastError());
-  if (!lazy && clear_mask)
-    TMNN_HIP_TRY(hipMemsetAsync(tr->mask.ptr, 0, tr->mask_words * sizeof(uint32_t),
-                                tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int zero_device(tmnn_trainer *tr, void *ptr, size_t bytes) {
+  if (bytes == 0) return TMNN_OK;
+  const size_t n16 = (bytes + 15) / 16;
+  const uint32_t blocks = static_cast<uint32_t>(
+      std::min<size_t>((n16 + 255) / 256, static_cast<size_t>(tr->ctx->cu_count) * 8));
+  hipLaunchKernelGGL(zero_bytes_kernel, dim3(std::max<uint32_t>(blocks, 1)), dim3(256), 0,
+                     tr->ctx->stream, static_cast<uint8_t *>(ptr), bytes);
+  TMNN_HIP_TRY(hipGetLastError());
   return TMNN_OK;
 }
 
@@ -446,18 +459,17 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
 }
 
 int zero_training_state(tmnn_trainer *tr) {
-  hipStream_t st = tr->ctx->stream;
-  TMNN_HIP_TRY(hipMemsetAsync(tr->grad_hash.ptr, 0, tr->hash_count * sizeof(int32_t), st));
-  TMNN_HIP_TRY(hipMemsetAsync(tr->grad_mlp.ptr, 0, tr->mlp_count * sizeof(float), st));
-  TMNN_HIP_TRY(hipMemsetAsync(tr->mask.ptr, 0, tr->mask_words * sizeof(uint32_t), st));
-  return TMNN_OK;
+  int rc = zero_device(tr, tr->grad_hash.ptr, tr->hash_count * sizeof(int32_t));
+  if (rc == TMNN_OK) rc = zero_device(tr, tr->grad_mlp.ptr, tr->mlp_count * sizeof(float));
+  if (rc == TMNN_OK) rc = zero_device(tr, tr->mask.ptr, tr->hash_entries);
+  return rc;
 }
 
 int reset_moments(tmnn_trainer *tr) {
   const size_t total = (static_cast<size_t>(tr->hash_count) + tr->mlp_count) * sizeof(float);
-  TMNN_HIP_TRY(hipMemsetAsync(tr->m.ptr, 0, total, tr->ctx->stream));
-  TMNN_HIP_TRY(hipMemsetAsync(tr->v.ptr, 0, total, tr->ctx->stream));
-  return TMNN_OK;
+  int rc = zero_device(tr, tr->m.ptr, total);
+  if (rc == TMNN_OK) rc = zero_device(tr, tr->v.ptr, total);
+  return rc;
 }
 
 int philox_fill(hipStream_t st, float *dst, uint32_t count, uint64_t seed, uint32_t base,
@@ -632,6 +644,8 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
                                       desc->num_hidden_layers, desc->num_outputs, 0, false,
                                       false, 1);
   tr->mlp_count = static_cast<uint32_t>(lay.mlp_count());
+  tr->hash_entries = tr->hash_count / static_cast<uint32_t>(desc->features_per_level);
+  // Reference bit-mask layout: a bit per entry when F == 2, else per float.
   const uint32_t width = desc->features_per_level == 2 ? 2u : 1u;
   tr->mask_words = (tr->hash_count / width + 31u) / 32u;
   // One fp32 resolution table for every kernel: r_0 = b, r_l = r_{l-1} * s
@@ -660,7 +674,7 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
   TMNN_HIP_TRY(tr->v.ensure(total * sizeof(float)));
   TMNN_HIP_TRY(tr->grad_hash.ensure(tr->hash_count * sizeof(int32_t)));
   TMNN_HIP_TRY(tr->grad_mlp.ensure(tr->mlp_count * sizeof(float)));
-  TMNN_HIP_TRY(tr->mask.ensure(tr->mask_words * sizeof(uint32_t)));
+  TMNN_HIP_TRY(tr->mask.ensure(tr->hash_entries));
   TMNN_HIP_TRY(tr->partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
                                    tr->mlp_count * sizeof(float)));
   TMNN_HIP_TRY(tr->loss_partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
@@ -1103,9 +1117,22 @@ int tmnn_debug_get_active_mask(tmnn_trainer *tr, uint32_t *words, size_t word_co
   if (!tr || !words) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
   if (word_count != tr->mask_words) return fail(TMNN_ERR_INVALID_ARGUMENT, "word count mismatch");
   TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
-  TMNN_HIP_TRY(hipMemcpyAsync(words, tr->mask.ptr, word_count * sizeof(uint32_t),
-                              hipMemcpyDeviceToHost, tr->ctx->stream));
+  std::vector<uint8_t> flags(tr->hash_entries);
+  TMNN_HIP_TRY(hipMemcpyAsync(flags.data(), tr->mask.ptr, flags.size(), hipMemcpyDeviceToHost,
+                              tr->ctx->stream));
   TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  // Reference layout (mlp_kernel_emitter.cpp:48-71): bit per entry (F == 2),
+  // else bit per float, all F floats of a visited entry set.
+  std::memset(words, 0, word_count * sizeof(uint32_t));
+  const uint32_t F = static_cast<uint32_t>(tr->d.features_per_level);
+  const uint32_t per = F == 2 ? 1u : F;
+  for (uint32_t e = 0; e < tr->hash_entries; ++e) {
+    if (!flags[e]) continue;
+    for (uint32_t f = 0; f < per; ++f) {
+      const uint32_t bit = e * per + f;
+      words[bit >> 5] |= 1u << (bit & 31u);
+    }
+  }
   return TMNN_OK;
 }
 
