@@ -119,7 +119,8 @@ __host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
                                                    int H, int NHL, int M,
                                                    int mlp_count, bool f16,
                                                    bool train, int wpb,
-                                                   bool dw_global = false) {
+                                                   bool dw_global = false,
+                                                   bool reg_dw = false) {
   FieldLayout s;
   s.INP = INP; s.HP = HP; s.IN = IN; s.H = H; s.NHL = NHL; s.M = M;
   s.es = f16 ? 2 : 4;
@@ -138,7 +139,7 @@ __host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
   off += kMaxLevels * 4;
   s.dw_off = off;
   s.dw_global = dw_global ? 1 : 0;
-  if (train && !dw_global) off += round_up(mlp_count, 4) * 4;
+  if (train && !dw_global && !reg_dw) off += round_up(mlp_count, 4) * 4;
   s.red_off = off;
   off += round_up(wpb, 4) * 4;
   off = round_up(off, 16);
@@ -148,6 +149,9 @@ __host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
   s.ds_off = s.hs_off + NHL * HP * kPS * s.es;
   s.wave_bytes = train ? round_up(s.ds_off + HP * kPS * s.es, 16) : 0;
   off += wpb * s.wave_bytes;
+  // Register-accumulated dW is reduced across the block's waves through LDS
+  // at the end of the kernel, over the then idle weight/activation space.
+  if (train && reg_dw) off = off > mlp_count * 4 ? off : mlp_count * 4;
   s.total = off;
   return s;
 }
@@ -293,13 +297,13 @@ __device__ __forceinline__ void layer_fwd(const FieldLayout &s, const unsigned c
     layer_mma<false, KT, MT>(smem + s.fwd_off(k), in, out, lane);
 }
 
-// One 16x16 tile of dW^T = sum over the 32 tile points of
+// acc + one 16x16 tile of sum over the 32 tile points of
 // A[row0 + i][pt] * B[col0 + j][pt], both read from [unit][point] LDS arrays.
 template <bool F16>
 __device__ __forceinline__ f32x4 dw_tile(const unsigned char *A, int row0,
                                          const unsigned char *B, int col0,
-                                         int p, int q) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                                         int p, int q,
+                                         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}) {
   if constexpr (F16) {
     const half8 av = *reinterpret_cast<const half8 *>(A + ((row0 + p) * kPS + 8 * q) * 2);
     const half8 bv = *reinterpret_cast<const half8 *>(B + ((col0 + p) * kPS + 8 * q) * 2);
@@ -457,10 +461,16 @@ __device__ __forceinline__ void encode_tile_t(const FieldArgs &a,
   }
 }
 
-template <int KT0>
+// DF = D * 8 + F selects the geometry at compile time; DF == 0 dispatches on
+// the runtime geometry.
+template <int KT0, int DF>
 __device__ __forceinline__ void encode_tile(const FieldArgs &a, const float *res,
                                             int q, const float (&P)[kNT][4],
                                             f32x4 (&X)[KT0][kNT]) {
+  if constexpr (DF != 0) {
+    encode_tile_t<DF / 8, DF % 8, KT0>(a, res, q, P, X);
+    return;
+  }
   switch (a.D * 8 + a.F) {
     case 2 * 8 + 1: encode_tile_t<2, 1, KT0>(a, res, q, P, X); break;
     case 2 * 8 + 2: encode_tile_t<2, 2, KT0>(a, res, q, P, X); break;
@@ -577,11 +587,15 @@ __device__ __forceinline__ void scatter_tile_t(const FieldArgs &a,
   }
 }
 
-template <int KT0>
+template <int KT0, int DF>
 __device__ __forceinline__ void scatter_tile(const FieldArgs &a, const float *res,
                                              int q, const float (&P)[kNT][4],
                                              const bool (&valid)[kNT],
                                              const f32x4 (&dx)[KT0][kNT]) {
+  if constexpr (DF != 0) {
+    scatter_tile_t<DF / 8, DF % 8, KT0>(a, res, q, P, valid, dx);
+    return;
+  }
   switch (a.D * 8 + a.F) {
     case 2 * 8 + 1: scatter_tile_t<2, 1, KT0>(a, res, q, P, valid, dx); break;
     case 2 * 8 + 2: scatter_tile_t<2, 2, KT0>(a, res, q, P, valid, dx); break;
@@ -604,7 +618,7 @@ __device__ __forceinline__ int kslot_f16(int ks, int q, int j) {
   return 32 * ks + (j < 4 ? 4 * q + j : 16 + 4 * q + (j - 4));
 }
 
-template <int HP, int INP, bool F16, bool TRAIN>
+template <int HP, int INP, bool F16, bool TRAIN, bool REGDW>
 __device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLayout &s,
                               unsigned char *smem) {
   const int tid = threadIdx.x;
@@ -670,7 +684,7 @@ __device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLay
   }
   for (int e = tid; e < kMaxLevels; e += nthr)
     reinterpret_cast<float *>(smem + s.res_off)[e] = e < a.L ? a.res[e] : 0.0f;
-  if constexpr (TRAIN) {
+  if constexpr (TRAIN && !REGDW) {
     if (s.dw_global) {
       float *dwg = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
       for (int e = tid; e < a.mlp_count; e += nthr) dwg[e] = 0.0f;
@@ -716,18 +730,118 @@ __device__ __forceinline__ float elem_loss(int kind, float y, float t,
 
 // ---------------------------------------------------------------- kernel ----
 
-template <int HP, int INP, bool F16, bool TRAIN>
+// Compile-time layer index for the unrolled backward (value > 0) and the
+// runtime one of the generic kernel (value 0, index in .runtime).
+template <int V>
+struct LayerC {
+  static constexpr int value = V;
+  int runtime = 0;
+};
+struct RuntimeLayer : LayerC<0> {
+  __device__ explicit RuntimeLayer(int k) { runtime = k; }
+};
+
+// f(LayerC<N>), f(LayerC<N-1>), ..., f(LayerC<1>).
+template <int N, class Fn>
+__device__ __forceinline__ void static_for_desc(Fn &&f) {
+  if constexpr (N >= 1) {
+    f(LayerC<N>{});
+    static_for_desc<N - 1>(f);
+  }
+}
+
+// Per-wave dW accumulators, resident in registers across all tiles of a
+// wave (used when the hidden-layer count is a compile-time constant). Tile
+// orientation matches dw_tile: w0[mt][ft] rows = hidden units 16mt + 4q + r,
+// cols = input features 16ft + p; wh[k-1][mt][it] rows = units of layer k,
+// cols = units of layer k-1; wo[ut] rows = outputs 4q + r, cols = hidden
+// units 16ut + p. b[k][mt][r] / bo[r] hold this lane's share (point lanes p)
+// of the bias sums.
+template <int HT, int KT0, int NHLT>
+struct DwRegs {
+  f32x4 w0[HT][KT0];
+  f32x4 wh[NHLT > 1 ? NHLT - 1 : 1][HT][HT];
+  f32x4 wo[HT];
+  float b[NHLT > 0 ? NHLT : 1][HT][4];
+  float bo[4];
+};
+
+// red[idx] (+)= v over the block's waves in wave order: wave 0 stores, the
+// others add, one wave at a time (deterministic).
+__device__ __forceinline__ void red_put(float *red, int idx, float v, bool first) {
+  red[idx] = first ? v : red[idx] + v;
+}
+
+template <int HT, int KT0, int NHLT>
+__device__ __forceinline__ void dw_regs_to_lds(const DwRegs<HT, KT0, NHLT> &R, const FieldArgs &a,
+                                               const FieldLayout &s, float *red, int p,
+                                               int q, bool first, float scale) {
+  const int H = a.H, IN = a.IN, M = a.M;
+#pragma unroll
+  for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+    for (int ft = 0; ft < KT0; ++ft)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int u = 16 * mt + 4 * q + r, f = 16 * ft + p;
+        if (u < H && f < IN) red_put(red, s.w_off(0) + f * H + u, R.w0[mt][ft][r] * scale, first);
+      }
+#pragma unroll
+  for (int k = 1; k < NHLT; ++k)
+#pragma unroll
+    for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+      for (int it = 0; it < HT; ++it)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int u = 16 * mt + 4 * q + r, i = 16 * it + p;
+          if (u < H && i < H) red_put(red, s.w_off(k) + i * H + u, R.wh[k - 1][mt][it][r] * scale, first);
+        }
+#pragma unroll
+  for (int ut = 0; ut < HT; ++ut)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = 4 * q + r, u = 16 * ut + p;
+      if (o < M && u < H) red_put(red, s.w_off(NHLT) + u * M + o, R.wo[ut][r] * scale, first);
+    }
+  // biases: sum the point lanes p, lane p == 0 of each q group writes
+#pragma unroll
+  for (int k = 0; k < NHLT; ++k)
+#pragma unroll
+    for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = sum_over_p(R.b[k][mt][r]);
+        const int u = 16 * mt + 4 * q + r;
+        if (p == 0 && u < H) red_put(red, s.b_off(k) + u, v * scale, first);
+      }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = sum_over_p(R.bo[r]);
+    const int o = 4 * q + r;
+    if (p == 0 && o < M) red_put(red, s.b_off(NHLT) + o, v * scale, first);
+  }
+}
+
+// The fused kernel body. Template parameters: padded hidden width HP and
+// input width INP (MFMA tiles), fp16 (split-fp16 forward, fp16 backward) or
+// fp32 MFMA, training or forward only, DF = D * 8 + F (0: runtime geometry),
+// NHLT = hidden-layer count (0: runtime count, dW accumulated in LDS;
+// > 0: dW accumulated in registers across tiles).
+template <int HP, int INP, bool F16, bool TRAIN, int DF, int NHLT>
 __device__ __forceinline__ void field_body(const FieldArgs &a) {
   constexpr int HT = HP / 16;
   constexpr int KT0 = INP / 16;
   constexpr int OKT = F16 ? 2 : 1;  // K tiles of the output-layer backward
   constexpr int es = F16 ? 2 : 4;
+  constexpr bool REGDW = TRAIN && NHLT > 0;
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const FieldLayout s = make_layout(INP, HP, a.IN, a.H, a.NHL, a.M,
+  const int NHL = NHLT > 0 ? NHLT : a.NHL;
+  const FieldLayout s = make_layout(INP, HP, a.IN, a.H, NHL, a.M,
                                     a.mlp_count, F16, TRAIN, a.waves_per_block,
-                                    a.dw_global != 0);
-  stage_weights<HP, INP, F16, TRAIN>(a, s, smem);
+                                    a.dw_global != 0, REGDW);
+  stage_weights<HP, INP, F16, TRAIN, REGDW>(a, s, smem);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -735,8 +849,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   const int p = lane & 15;
   const int q = lane >> 4;
   const float *res = reinterpret_cast<const float *>(smem + s.res_off);
-  // dW accumulator: LDS, or (when the model leaves no room) this block's row
-  // of grad_partials, which the block zeroed in stage_weights.
+  // LDS dW accumulator (runtime layer count): LDS, or (when the model leaves
+  // no room) this block's row of grad_partials, zeroed in stage_weights.
   float *dw = s.dw_global
                   ? a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count
                   : reinterpret_cast<float *>(smem + s.dw_off);
@@ -746,6 +860,26 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   unsigned char *Ds = wb + s.ds_off;
   const int hs_layer_bytes = HP * kPS * es;
   float lane_loss = 0.0f;
+
+  DwRegs<HT, KT0, NHLT> R;
+  if constexpr (REGDW) {
+#pragma unroll
+    for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+      for (int ft = 0; ft < KT0; ++ft) R.w0[mt][ft] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < (NHLT > 1 ? NHLT - 1 : 1); ++k)
+#pragma unroll
+        for (int it = 0; it < HT; ++it) R.wh[k][mt][it] = f32x4{0.f, 0.f, 0.f, 0.f};
+      R.wo[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < NHLT; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) R.b[k][mt][r] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) R.bo[r] = 0.0f;
+  }
 
   for (int tile = blockIdx.x * a.waves_per_block + wave; tile < a.n_tiles;
        tile += gridDim.x * a.waves_per_block) {
@@ -763,13 +897,13 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 
     // ---- encode: input features 16*kt + 4*q + r of point 16*nt + p
     f32x4 X[KT0][kNT];
-    encode_tile<KT0>(a, res, q, P, X);
+    encode_tile<KT0, DF>(a, res, q, P, X);
     if constexpr (TRAIN) store_tiles<F16, KT0>(Xs, X, p, q);
 
     // ---- MLP forward
     f32x4 act[HT][kNT];
     layer_fwd<F16, KT0, HT>(s, smem, 0, X, act, lane);
-    for (int k = 0; k < a.NHL; ++k) {
+    auto hidden_fwd = [&](int k) {
       if (k > 0) {
         f32x4 nxt[HT][kNT];
         layer_fwd<F16, HT, HT>(s, smem, k, act, nxt, lane);
@@ -789,11 +923,17 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
             act[mt][nt][r] = v > 0.0f ? v : 0.0f;
           }
       if constexpr (TRAIN) store_tiles<F16, HT>(Hs + k * hs_layer_bytes, act, p, q);
+    };
+    if constexpr (NHLT > 0) {
+#pragma unroll
+      for (int k = 0; k < NHLT; ++k) hidden_fwd(k);
+    } else {
+      for (int k = 0; k < NHL; ++k) hidden_fwd(k);
     }
     f32x4 y[1][kNT];
-    layer_fwd<F16, HT, 1>(s, smem, a.NHL, act, y, lane);
+    layer_fwd<F16, HT, 1>(s, smem, NHL, act, y, lane);
     {
-      const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(a.NHL));
+      const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(NHL));
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
@@ -893,61 +1033,86 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         store_tiles<F16, 1>(Ds, g0, p, q);
       }
       wave_lds_sync();
-      const int last = a.NHL - 1;
+      const int last = NHL - 1;
       {
         const unsigned char *Hl = Hs + last * hs_layer_bytes;
-        const int wo = s.w_off(a.NHL), bo = s.b_off(a.NHL);
+        if constexpr (REGDW) {
 #pragma unroll
-        for (int ut = 0; ut < HT; ++ut) {
-          const f32x4 acc = dw_tile<F16>(Ds, 0, Hl, 16 * ut, p, q);
-          const int u = 16 * ut + p;
+          for (int ut = 0; ut < HT; ++ut) R.wo[ut] = dw_tile<F16>(Ds, 0, Hl, 16 * ut, p, q, R.wo[ut]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 4 * q + r;
-            if (o < a.M && u < a.H) atomicAdd(dw + wo + u * a.M + o, acc[r] * a.inv_loss_scale);
-          }
-        }
+          for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float sv = 0.0f;
+            for (int nt = 0; nt < kNT; ++nt) R.bo[r] += g[0][nt][r];
+        } else {
+          const int wo = s.w_off(NHL), bo = s.b_off(NHL);
 #pragma unroll
-          for (int nt = 0; nt < kNT; ++nt) sv += g[0][nt][r];
-          sv = sum_over_p(sv);
-          const int o = 4 * q + r;
-          if (p == 0 && o < a.M) atomicAdd(dw + bo + o, sv * a.inv_loss_scale);
-        }
-      }
-      f32x4 dl[HT][kNT];
-      layer_mma<F16, OKT, HT>(smem + s.bwd_off(a.NHL), g, dl, lane);
-      relu_mask<F16, HT>(dl, Hs + last * hs_layer_bytes, p, q);
-
-      // ---- hidden layers nhl-1 .. 1
-      for (int k = a.NHL - 1; k >= 1; --k) {
-        wave_lds_sync();
-        store_tiles<F16, HT>(Ds, dl, p, q);
-        wave_lds_sync();
-        const unsigned char *Hin = Hs + (k - 1) * hs_layer_bytes;
-        const int wk = s.w_off(k), bk = s.b_off(k);
-#pragma unroll
-        for (int mt = 0; mt < HT; ++mt) {
-#pragma unroll
-          for (int it = 0; it < HT; ++it) {
-            const f32x4 acc = dw_tile<F16>(Ds, 16 * mt, Hin, 16 * it, p, q);
-            const int i = 16 * it + p;
+          for (int ut = 0; ut < HT; ++ut) {
+            const f32x4 acc = dw_tile<F16>(Ds, 0, Hl, 16 * ut, p, q);
+            const int u = 16 * ut + p;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int u = 16 * mt + 4 * q + r;
-              if (u < a.H && i < a.H) atomicAdd(dw + wk + i * a.H + u, acc[r] * a.inv_loss_scale);
+              const int o = 4 * q + r;
+              if (o < a.M && u < a.H) atomicAdd(dw + wo + u * a.M + o, acc[r] * a.inv_loss_scale);
             }
           }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float sv = 0.0f;
 #pragma unroll
-            for (int nt = 0; nt < kNT; ++nt) sv += dl[mt][nt][r];
+            for (int nt = 0; nt < kNT; ++nt) sv += g[0][nt][r];
             sv = sum_over_p(sv);
-            const int u = 16 * mt + 4 * q + r;
-            if (p == 0 && u < a.H) atomicAdd(dw + bk + u, sv * a.inv_loss_scale);
+            const int o = 4 * q + r;
+            if (p == 0 && o < a.M) atomicAdd(dw + bo + o, sv * a.inv_loss_scale);
+          }
+        }
+      }
+      f32x4 dl[HT][kNT];
+      layer_mma<F16, OKT, HT>(smem + s.bwd_off(NHL), g, dl, lane);
+      relu_mask<F16, HT>(dl, Hs + last * hs_layer_bytes, p, q);
+
+      // ---- hidden layers nhl-1 .. 1
+      auto hidden_bwd = [&](auto kc) {
+        constexpr int KC = decltype(kc)::value;  // compile-time layer (REGDW) or 0
+        const int k = KC > 0 ? KC : kc.runtime;
+        wave_lds_sync();
+        store_tiles<F16, HT>(Ds, dl, p, q);
+        wave_lds_sync();
+        const unsigned char *Hin = Hs + (k - 1) * hs_layer_bytes;
+        if constexpr (REGDW) {
+#pragma unroll
+          for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+            for (int it = 0; it < HT; ++it)
+              R.wh[KC - 1][mt][it] =
+                  dw_tile<F16>(Ds, 16 * mt, Hin, 16 * it, p, q, R.wh[KC - 1][mt][it]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+              for (int nt = 0; nt < kNT; ++nt) R.b[KC][mt][r] += dl[mt][nt][r];
+          }
+        } else {
+          const int wk = s.w_off(k), bk = s.b_off(k);
+#pragma unroll
+          for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+            for (int it = 0; it < HT; ++it) {
+              const f32x4 acc = dw_tile<F16>(Ds, 16 * mt, Hin, 16 * it, p, q);
+              const int i = 16 * it + p;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int u = 16 * mt + 4 * q + r;
+                if (u < a.H && i < a.H) atomicAdd(dw + wk + i * a.H + u, acc[r] * a.inv_loss_scale);
+              }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float sv = 0.0f;
+#pragma unroll
+              for (int nt = 0; nt < kNT; ++nt) sv += dl[mt][nt][r];
+              sv = sum_over_p(sv);
+              const int u = 16 * mt + 4 * q + r;
+              if (p == 0 && u < a.H) atomicAdd(dw + bk + u, sv * a.inv_loss_scale);
+            }
           }
         }
         f32x4 nd[HT][kNT];
@@ -957,13 +1122,29 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         for (int mt = 0; mt < HT; ++mt)
 #pragma unroll
           for (int nt = 0; nt < kNT; ++nt) dl[mt][nt] = nd[mt][nt];
+      };
+      if constexpr (NHLT > 0) {
+        static_for_desc<NHLT - 1>([&](auto kc) { hidden_bwd(kc); });
+      } else {
+        for (int k = NHL - 1; k >= 1; --k) hidden_bwd(RuntimeLayer{k});
       }
 
       // ---- layer 0: dW0, db0, input-feature gradient, hash scatter
       wave_lds_sync();
       store_tiles<F16, HT>(Ds, dl, p, q);
       wave_lds_sync();
-      {
+      if constexpr (REGDW) {
+#pragma unroll
+        for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+          for (int ft = 0; ft < KT0; ++ft)
+            R.w0[mt][ft] = dw_tile<F16>(Ds, 16 * mt, Xs, 16 * ft, p, q, R.w0[mt][ft]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) R.b[0][mt][r] += dl[mt][nt][r];
+        }
+      } else {
         const int w0 = s.w_off(0), b0 = s.b_off(0);
 #pragma unroll
         for (int mt = 0; mt < HT; ++mt) {
@@ -990,7 +1171,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       }
       f32x4 dx[KT0][kNT];
       layer_mma<F16, HT, KT0>(smem + s.bwd_off(0), dl, dx, lane);
-      scatter_tile<KT0>(a, res, q, P, valid, dx);
+      scatter_tile<KT0, DF>(a, res, q, P, valid, dx);
     }
   }
 
@@ -998,16 +1179,26 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
     float v = lane_loss;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
-    float *red = reinterpret_cast<float *>(smem + s.red_off);
-    if (lane == 0) red[wave] = v;
+    float *lred = reinterpret_cast<float *>(smem + s.red_off);
+    if (lane == 0) lred[wave] = v;
     __syncthreads();
     if (threadIdx.x == 0) {
       float t = 0.0f;
-      for (int w = 0; w < a.waves_per_block; ++w) t += red[w];
+      for (int w = 0; w < a.waves_per_block; ++w) t += lred[w];
       a.loss_partials[blockIdx.x] = t;
     }
-    if (!s.dw_global) {
-      float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+    float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+    if constexpr (REGDW) {
+      // every wave is past its tiles (barrier above): reduce the waves'
+      // register accumulators through LDS in wave order, then store the row
+      __syncthreads();
+      float *red = reinterpret_cast<float *>(smem);
+      for (int w = 0; w < a.waves_per_block; ++w) {
+        if (wave == w) dw_regs_to_lds<HT, KT0, NHLT>(R, a, s, red, p, q, w == 0, a.inv_loss_scale);
+        __syncthreads();
+      }
+      for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = red[e];
+    } else if (!s.dw_global) {
       for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = dw[e];
     }
   }
@@ -1015,15 +1206,15 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 
 // Training launches are LDS-bound to one 4-wave block per CU (one wave per
 // SIMD), so they may use the whole register file.
-template <int HP, int INP, bool F16>
+template <int HP, int INP, bool F16, int DF, int NHLT>
 __global__ void __launch_bounds__(kBlockThreads)
     __attribute__((amdgpu_waves_per_eu(1, 1))) field_train_kernel(FieldArgs a) {
-  field_body<HP, INP, F16, true>(a);
+  field_body<HP, INP, F16, true, DF, NHLT>(a);
 }
 
-template <int HP, int INP, bool F16>
+template <int HP, int INP, bool F16, int DF>
 __global__ void __launch_bounds__(kBlockThreads) field_forward_kernel(FieldArgs a) {
-  field_body<HP, INP, F16, false>(a);
+  field_body<HP, INP, F16, false, DF, 0>(a);
 }
 
 }  // namespace tmnn_hip

@@ -56,26 +56,46 @@ float baked6(float v) {
 
 using FieldKernel = void (*)(FieldArgs);
 
-template <int HP, int INP, bool F16, bool TRAIN>
-FieldKernel kernel_ptr() {
-  if constexpr (TRAIN)
-    return field_train_kernel<HP, INP, F16>;
-  else
-    return field_forward_kernel<HP, INP, F16>;
-}
+struct KernelChoice {
+  FieldKernel fn = nullptr;
+  bool reg_dw = false;  // dW accumulated in registers (compile-time layers)
+};
 
-FieldKernel select_kernel(int HP, int INP, bool f16, bool train) {
-#define TMNN_SEL(hp, inp)                                                   \
-  if (HP == hp && INP == inp) {                                             \
-    if (f16) return train ? kernel_ptr<hp, inp, true, true>() : kernel_ptr<hp, inp, true, false>(); \
-    return train ? kernel_ptr<hp, inp, false, true>() : kernel_ptr<hp, inp, false, false>(); \
+// Geometry-specialised kernels (compile-time D, F and hidden-layer count;
+// dW in registers) for the BASELINE shapes, else the generic kernels
+// (runtime geometry, dW accumulated in LDS).
+KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL) {
+  const int DF = D * 8 + F;
+#define TMNN_SPEC(hp, inp, df, nhl)                                                  \
+  if (HP == hp && INP == inp && DF == df && (!train || NHL == nhl)) {               \
+    if (train)                                                                      \
+      return {f16 ? field_train_kernel<hp, inp, true, df, nhl>                      \
+                  : field_train_kernel<hp, inp, false, df, nhl>,                    \
+              true};                                                                \
+    return {f16 ? field_forward_kernel<hp, inp, true, df>                           \
+                : field_forward_kernel<hp, inp, false, df>,                         \
+            false};                                                                 \
+  }
+  TMNN_SPEC(64, 32, 2 * 8 + 2, 2)  // image fit: 2D, 16x2 features, 64x2 MLP
+  TMNN_SPEC(64, 32, 3 * 8 + 2, 1)  // NeRF density: 3D, 16x2, 64x1
+  TMNN_SPEC(64, 64, 3 * 8 + 4, 3)  // SDF: 3D, 16x4, 64x3
+#undef TMNN_SPEC
+#define TMNN_SEL(hp, inp)                                                        \
+  if (HP == hp && INP == inp) {                                                  \
+    if (train)                                                                   \
+      return {f16 ? field_train_kernel<hp, inp, true, 0, 0>                      \
+                  : field_train_kernel<hp, inp, false, 0, 0>,                    \
+              false};                                                            \
+    return {f16 ? field_forward_kernel<hp, inp, true, 0>                         \
+                : field_forward_kernel<hp, inp, false, 0>,                       \
+            false};                                                              \
   }
   TMNN_SEL(32, 32)
   TMNN_SEL(32, 64)
   TMNN_SEL(64, 32)
   TMNN_SEL(64, 64)
 #undef TMNN_SEL
-  return nullptr;
+  return {};
 }
 
 struct DevBuf {
@@ -110,6 +130,7 @@ struct KernelPlan {
   int wpb = 0;          // waves per block
   int lds = 0;          // dynamic LDS bytes
   bool dw_global = false;  // dW accumulator outside LDS
+  bool reg_dw = false;     // dW accumulator in registers
   int max_blocks = 0;   // resident blocks on the whole device
 };
 
@@ -231,17 +252,20 @@ int prof_collect(tmnn_trainer *tr) {
 }
 
 int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
-  out.fn = select_kernel(tr->HP, tr->INP, f16, train);
+  const KernelChoice kc = select_kernel(tr->HP, tr->INP, f16, train, tr->d.spatial_dims,
+                                        tr->d.features_per_level, tr->d.num_hidden_layers);
+  out.fn = kc.fn;
+  out.reg_dw = kc.reg_dw;
   if (!out.fn) return fail(TMNN_ERR_UNSUPPORTED, "no kernel for this geometry");
   // Most waves per block whose LDS plan fits; failing that, move the dW
   // accumulator out of LDS (global float atomics into the block's row).
   int wpb = 0;
-  for (int dwg = 0; dwg <= (train ? 1 : 0) && wpb == 0; ++dwg) {
+  for (int dwg = 0; dwg <= (train && !kc.reg_dw ? 1 : 0) && wpb == 0; ++dwg) {
     for (int w = 4; w >= 1; --w) {
       const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
                                         tr->d.num_hidden_layers, tr->d.num_outputs,
                                         static_cast<int>(tr->mlp_count), f16, train, w,
-                                        dwg != 0);
+                                        dwg != 0, kc.reg_dw);
       if (s.total <= kMaxLdsBytes) {
         out.lds = s.total;
         out.dw_global = dwg != 0;
