@@ -256,6 +256,13 @@ int tmnn_debug_get_gradients(tmnn_trainer *tr, int32_t *grad_hash,
 int tmnn_debug_get_active_mask(tmnn_trainer *tr, uint32_t *words,
                                size_t word_count);
 
+/* The step's Morton sort of a batch (morton_sort_batch, morton_sort.h:
+ * 60-110): codes[i] = Morton code of positions[i] (2D: the x/y interleave of
+ * the lifted point, which orders identically), perm[j] = input row of the
+ * j-th point in sorted order (stable: ties keep input order). Host memory. */
+int tmnn_debug_morton_sort(tmnn_trainer *tr, const float *positions, int32_t n,
+                           uint32_t *codes, uint32_t *perm);
+
 /* Per-level resolution table used by every kernel (L floats). */
 int tmnn_debug_get_resolutions(tmnn_trainer *tr, float *out, int32_t count);
 

@@ -333,3 +333,36 @@ def test_set_initial_weights_size_mismatch():
     with make_trainer(d, m_out, enc, net) as tr:
         with pytest.raises(Exception, match="count mismatch"):
             tr.set_initial_weights(np.zeros(5, np.float32), None)
+
+
+# ------------------------------------------------------------ Morton sort --
+
+def _compact_2d(code3):
+    """x/y interleave of a lifted (x, y, 0) 3D Morton code (the z bits are the
+    same on every point, so dropping them keeps the order)."""
+    out = np.zeros_like(code3)
+    for b in range(10):
+        out |= ((code3 >> (3 * b)) & 1) << (2 * b)
+        out |= ((code3 >> (3 * b + 1)) & 1) << (2 * b + 1)
+    return out
+
+
+@pytest.mark.parametrize("d,n", [(2, 1), (2, 4097), (2, 70000), (3, 12345), (4, 9000)])
+def test_morton_sort_matches_oracle_codes_and_stable_order(oracle, d, n):
+    """morton_sort.h: same codes as the oracle (the reference's quantisation),
+    and the permutation is the stable argsort of those codes."""
+    _say(f"morton sort d={d} n={n}")
+    name = {2: "2d_f2", 3: "3d_f2", 4: "4d_f2"}[d]
+    _, enc, net, m_out = GEOMS[name]
+    rng = np.random.default_rng(n)
+    pos = rng.random((n, d), dtype=np.float32)
+    pos[: n // 4] = pos[0]  # ties
+    with make_trainer(d, m_out, enc, net, batch=1 << 20) as tr:
+        codes, perm = tr.debug_morton_sort(pos)
+    want = oracle.morton_codes(pos, d)
+    if d == 2:
+        # the lifted z = 0 quantises to 512 on every point: a constant bit 29
+        assert np.all(((want >> 2) & 0o1111111111) == (1 << 27))
+        want = _compact_2d(want)
+    assert np.array_equal(codes, want)
+    assert np.array_equal(perm, np.argsort(want, kind="stable").astype(np.uint32))

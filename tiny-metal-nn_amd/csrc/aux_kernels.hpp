@@ -29,10 +29,21 @@ __global__ void philox_uniform_kernel(float *out, uint32_t count, uint32_t k0,
   }
 }
 
-// Morton code per point (morton_sort.h:14-57); 2D points are lifted to
-// (x, y, 0) like the reference's callers. idx[i] = i for the sort payload.
+// Morton code per point (morton_sort.h:14-57): the reference's 10-bit (3D)
+// or 8-bit (4D) quantisation. 2D points are the reference's lifted
+// (x, y, 0); their z bits are all zero, so the code keeps only the x/y
+// interleave (20 bits), which sorts identically.
+__device__ __forceinline__ uint32_t expand_bits_2d(uint32_t v) {
+  v &= 0x3FFu;
+  v = (v | (v << 8)) & 0x00FF00FFu;
+  v = (v | (v << 4)) & 0x0F0F0F0Fu;
+  v = (v | (v << 2)) & 0x33333333u;
+  v = (v | (v << 1)) & 0x55555555u;
+  return v;
+}
+
 __global__ void morton_codes_kernel(const float *pos, int32_t n, int32_t dims,
-                                    uint32_t *codes, uint32_t *idx) {
+                                    uint32_t *codes) {
   const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const float *p = pos + static_cast<size_t>(i) * dims;
@@ -42,14 +53,15 @@ __global__ void morton_codes_kernel(const float *pos, int32_t n, int32_t dims,
         (expand_bits_4d(morton_quant(p[2], 256.0f, 255.0f)) << 2) |
         (expand_bits_4d(morton_quant(p[1], 256.0f, 255.0f)) << 1) |
         expand_bits_4d(morton_quant(p[0], 256.0f, 255.0f));
-  } else {
-    const float z = dims == 3 ? p[2] : 0.0f;
-    c = (expand_bits_3d(morton_quant(z, 1024.0f, 1023.0f)) << 2) |
+  } else if (dims == 3) {
+    c = (expand_bits_3d(morton_quant(p[2], 1024.0f, 1023.0f)) << 2) |
         (expand_bits_3d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
         expand_bits_3d(morton_quant(p[0], 1024.0f, 1023.0f));
+  } else {
+    c = (expand_bits_2d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
+        expand_bits_2d(morton_quant(p[0], 1024.0f, 1023.0f));
   }
   codes[i] = c;
-  idx[i] = static_cast<uint32_t>(i);
 }
 
 // dst_pos[i] = src_pos[perm[i]], dst_tgt[i] = src_tgt[perm[i]].
@@ -67,14 +79,33 @@ __global__ void gather_rows_kernel(const float *src_pos, const float *src_tgt,
       dst_tgt[static_cast<size_t>(i) * tgt_dims + d] = src_tgt[s * tgt_dims + d];
 }
 
-// grad_mlp[i] += sum over blocks b (ascending) of partials[b][i].
-__global__ void reduce_partials_kernel(const float *partials, int32_t blocks,
-                                       int32_t count, float *grad_mlp) {
-  const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
+// grad_mlp[i] += sum over the per-block partial rows partials[b][i].
+// Block = 64 columns x 16 row groups; row group g sums rows g, g+16, ...
+// in ascending order, then the 16 group sums are added in group order:
+// a fixed order, so the result is bit-reproducible.
+constexpr int kReduceCols = 64;
+constexpr int kReduceGroups = 16;
+__global__ void __launch_bounds__(kReduceCols * kReduceGroups)
+    reduce_partials_kernel(const float *partials, int32_t blocks, int32_t count,
+                           float *grad_mlp) {
+  __shared__ float red[kReduceGroups][kReduceCols + 1];
+  const int c = threadIdx.x % kReduceCols;
+  const int g = threadIdx.x / kReduceCols;
+  const int col = blockIdx.x * kReduceCols + c;
   float s = 0.0f;
-  for (int32_t b = 0; b < blocks; ++b) s += partials[static_cast<size_t>(b) * count + i];
-  grad_mlp[i] = grad_mlp[i] + s;
+  if (col < count) {
+#pragma unroll 4
+    for (int32_t b = g; b < blocks; b += kReduceGroups)
+      s += partials[static_cast<size_t>(b) * count + col];
+  }
+  red[g][c] = s;
+  __syncthreads();
+  if (g == 0 && col < count) {
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kReduceGroups; ++k) t += red[k][c];
+    grad_mlp[col] = grad_mlp[col] + t;
+  }
 }
 
 struct AdamArgs {
@@ -165,14 +196,16 @@ __global__ void zero_bytes_kernel(uint8_t *dst, size_t n) {
     dst[i] = 0;
 }
 
-// loss = (sum over block partials, ascending) / N, written to *out.
-__global__ void loss_reduce_kernel(const float *partials, int32_t blocks,
-                                   float inv_count_div, int32_t n, float *out) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// loss = (sum over block partials) / N, written to *out. One wave: lane l
+// sums partials l, l+64, ... ascending, then a fixed xor-tree across lanes.
+__global__ void loss_reduce_kernel(const float *partials, int32_t blocks, int32_t n,
+                                   float *out) {
+  const int lane = threadIdx.x;
   float t = 0.0f;
-  for (int32_t b = 0; b < blocks; ++b) t += partials[b];
-  (void)inv_count_div;
-  *out = n > 0 ? t / static_cast<float>(n) : 0.0f;
+  for (int32_t b = lane; b < blocks; b += 64) t += partials[b];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+  if (lane == 0) *out = n > 0 ? t / static_cast<float>(n) : 0.0f;
 }
 
 // Encode-only inspection kernel: thread per (point, level).

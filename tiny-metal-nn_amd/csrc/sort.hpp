@@ -9,10 +9,17 @@
 
 namespace tmnn_hip {
 
+// Scratch bytes morton_sort_pairs needs for n keys.
 hipError_t morton_sort_temp_bytes(int n, size_t *bytes);
 
-hipError_t morton_sort_pairs(void *tmp, size_t &tmp_bytes, const uint32_t *keys_in,
-                             uint32_t *keys_out, const uint32_t *vals_in,
-                             uint32_t *vals_out, int n, int end_bit, hipStream_t stream);
+// Sorts keys0[0..n) (bits [0, end_bit)) with the point index as payload.
+// keys0/keys1 and vals0/vals1 are ping-pong buffers of n elements; keys0 is
+// overwritten. The payload of the first pass is the identity (vals0 is not
+// read). On return *keys_sorted / *vals_sorted point at the buffers holding
+// the sorted keys and their original indices.
+hipError_t morton_sort_pairs(void *tmp, size_t tmp_bytes, uint32_t *keys0, uint32_t *keys1,
+                             uint32_t *vals0, uint32_t *vals1, int n, int end_bit,
+                             hipStream_t stream, const uint32_t **keys_sorted,
+                             const uint32_t **vals_sorted);
 
 }  // namespace tmnn_hip

@@ -364,20 +364,22 @@ int sort_batch(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
   }
   const int threads = 256, blocks = (n + threads - 1) / threads;
   hipLaunchKernelGGL(morton_codes_kernel, dim3(blocks), dim3(threads), 0, st, d_pos, n,
-                     tr->d.spatial_dims, tr->keys0.as<uint32_t>(), tr->vals0.as<uint32_t>());
+                     tr->d.spatial_dims, tr->keys0.as<uint32_t>());
   TMNN_HIP_TRY(hipGetLastError());
-  const int end_bit = tr->d.spatial_dims == 4 ? 32 : 30;
-  size_t tmp = tr->sort_tmp.bytes;
-  TMNN_HIP_TRY(morton_sort_pairs(tr->sort_tmp.ptr, tmp, tr->keys0.as<uint32_t>(),
+  // 2D codes interleave x and y only (the lifted z = 0 bits are all zero,
+  // which leaves the order unchanged): 20 bits; 3D 30 bits; 4D 32 bits.
+  const int end_bit = tr->d.spatial_dims == 2 ? 20 : (tr->d.spatial_dims == 3 ? 30 : 32);
+  const uint32_t *sorted_keys = nullptr, *perm = nullptr;
+  TMNN_HIP_TRY(morton_sort_pairs(tr->sort_tmp.ptr, tr->sort_tmp.bytes, tr->keys0.as<uint32_t>(),
                                  tr->keys1.as<uint32_t>(), tr->vals0.as<uint32_t>(),
-                                 tr->vals1.as<uint32_t>(), n, end_bit, st));
+                                 tr->vals1.as<uint32_t>(), n, end_bit, st, &sorted_keys, &perm));
   hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks), dim3(threads), 0, st, d_pos, d_tgt,
-                     tr->vals1.as<uint32_t>(), n, tr->d.spatial_dims, tgt_dims,
+                     perm, n, tr->d.spatial_dims, tgt_dims,
                      tr->s_pos.as<float>(), d_tgt ? tr->s_tgt.as<float>() : nullptr);
   TMNN_HIP_TRY(hipGetLastError());
   *pos_out = tr->s_pos.as<float>();
   *tgt_out = d_tgt ? tr->s_tgt.as<float>() : nullptr;
-  *perm_out = tr->vals1.as<uint32_t>();
+  *perm_out = perm;
   return TMNN_OK;
 }
 
@@ -406,7 +408,8 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   const int blocks = launch_field(tr, tr->train_plan, a, n);
   if (blocks < 0) return blocks;
   if ((rc = prof_mark(tr, 2)) != TMNN_OK) return rc;
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + 255) / 256), dim3(256), 0,
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + kReduceCols - 1) / kReduceCols),
+                     dim3(kReduceCols * kReduceGroups), 0,
                      tr->ctx->stream, tr->partials.as<float>(), blocks,
                      static_cast<int32_t>(tr->mlp_count), tr->grad_mlp.as<float>());
   TMNN_HIP_TRY(hipGetLastError());
@@ -470,7 +473,7 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
   const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false);
   if (blocks < 0) return blocks;
   hipLaunchKernelGGL(loss_reduce_kernel, dim3(1), dim3(64), 0, tr->ctx->stream,
-                     tr->loss_partials.as<float>(), blocks, 0.0f, n,
+                     tr->loss_partials.as<float>(), blocks, n,
                      d_loss ? d_loss : tr->loss_out.as<float>());
   TMNN_HIP_TRY(hipGetLastError());
   if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
@@ -1157,6 +1160,40 @@ int tmnn_debug_get_active_mask(tmnn_trainer *tr, uint32_t *words, size_t word_co
       words[bit >> 5] |= 1u << (bit & 31u);
     }
   }
+  return TMNN_OK;
+}
+
+int tmnn_debug_morton_sort(tmnn_trainer *tr, const float *positions, int32_t n, uint32_t *codes,
+                           uint32_t *perm) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "N must be non-negative");
+  if (n == 0) return TMNN_OK;
+  if (!positions || !codes || !perm) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  int rc = ensure_batch(tr, n);
+  if (rc != TMNN_OK) return rc;
+  const size_t D = tr->d.spatial_dims;
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, positions, n * D * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const int threads = 256, blocks = (n + threads - 1) / threads;
+  hipLaunchKernelGGL(morton_codes_kernel, dim3(blocks), dim3(threads), 0, st,
+                     tr->in_pos.as<float>(), n, tr->d.spatial_dims, tr->keys0.as<uint32_t>());
+  TMNN_HIP_TRY(hipGetLastError());
+  TMNN_HIP_TRY(hipMemcpyAsync(codes, tr->keys0.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                              st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  const float *sp = nullptr, *stg = nullptr;
+  const uint32_t *p = nullptr;
+  rc = sort_batch(tr, tr->in_pos.as<float>(), nullptr, 0, n, &sp, &stg, &p);
+  if (rc != TMNN_OK) return rc;
+  if (!p && n == 1) {
+    perm[0] = 0u;  // a single point is its own order
+    return TMNN_OK;
+  }
+  if (!p) return fail(TMNN_ERR_RUNTIME, "morton_sort is disabled for this trainer");
+  TMNN_HIP_TRY(hipMemcpyAsync(perm, p, n * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
   return TMNN_OK;
 }
 

@@ -332,6 +332,17 @@ class Trainer:
         _lib.check(self._lib.tmnn_debug_get_active_mask(self._h, _ptr(out), words))
         return out
 
+    def debug_morton_sort(self, positions) -> tuple[np.ndarray, np.ndarray]:
+        """(Morton codes, stable sort permutation) the step applies to a batch."""
+        x = _as_f32_2d(positions, "positions", self.n_input)
+        n = x.shape[0]
+        codes = np.empty(n, np.uint32)
+        perm = np.empty(n, np.uint32)
+        if n:
+            _lib.check(self._lib.tmnn_debug_morton_sort(self._h, _ptr(x), n, _ptr(codes),
+                                                        _ptr(perm)))
+        return codes, perm
+
     def debug_resolutions(self) -> np.ndarray:
         self._check_open()
         L = self.config["encoding"]["n_levels"]
