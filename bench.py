@@ -134,15 +134,19 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
 
 
 def traffic_from_profiles() -> float | None:
-    """HBM bytes per launch of the fused train kernel from the committed
-    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated)."""
-    f = REPO / "profiles" / "field_train_kernel_c2_traffic.json"
+    """HBM bytes per launch of the fused train kernel, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled
+    by the same counter's reading for a plain copy of known size)."""
+    f = REPO / "profiles" / "field_train_kernel_c2.md"
     if not f.exists():
         return None
-    try:
-        return float(json.loads(f.read_text())["bytes_per_launch"])
-    except (ValueError, KeyError):
-        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1])
+            except ValueError:
+                return None
+    return None
 
 
 def main() -> int:
@@ -152,7 +156,20 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 launches): the "
+                         "known-size reference for FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 5}))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one "
               "MI355X (the hot path runs on a single GPU; see the sharding design in "
