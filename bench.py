@@ -59,10 +59,10 @@ C2_CONFIG = {
 
 def alg_bytes_per_point(d: int, levels: int, feats: int, n_out: int) -> int:
     """Algorithmic HBM bytes of the fused train kernel per point: position and
-    target reads, the 2^D corner gathers of every level (fp32 features) and one
-    int32 atomic per corner feature of the hash-gradient scatter."""
+    target reads, the 2^D corner gathers of every level (fp32 features) and the
+    fp32 input-feature gradient it hands to the scatter kernel."""
     corners = 1 << d
-    return 4 * d + 4 * n_out + 2 * (corners * levels * feats * 4)
+    return 4 * d + 4 * n_out + corners * levels * feats * 4 + levels * feats * 4
 
 
 def make_image(torch, seed: int, device):
@@ -254,8 +254,8 @@ def main() -> int:
                 "kernel_avg_us": round(k_us, 2),
                 "alg_bytes_per_point": bpp}
     phases = {k: round(prof[k] / steps_prof, 2) for k in
-              ("gpu_sort_us", "gpu_fwd_bwd_us", "gpu_reduce_us", "gpu_adam_us",
-               "gpu_total_us")}
+              ("gpu_sort_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",
+               "gpu_adam_us", "gpu_total_us")}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 

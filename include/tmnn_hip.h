@@ -229,7 +229,8 @@ typedef struct tmnn_step_profile {
   uint32_t steps;             /* profiled steps summed below */
   uint32_t batch_size;        /* points of the last profiled step */
   double gpu_sort_us;         /* Morton codes + radix sort + gather */
-  double gpu_fwd_bwd_us;      /* the fused field kernel (encode..scatter) */
+  double gpu_fwd_bwd_us;      /* the fused field kernel (encode..dx) */
+  double gpu_scatter_us;      /* hash-grid backward scatter + visit flags */
   double gpu_reduce_us;       /* dW partial reduction + loss reduction */
   double gpu_adam_us;         /* fused Adam pass (+ mask/grad clearing) */
   double gpu_total_us;        /* first event to last event, summed */

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "device_common.hpp"
+#include "scatter_kernel.hpp"
 
 namespace tmnn_hip {
 
@@ -114,14 +115,17 @@ struct AdamArgs {
   float *v;
   int32_t *grad_hash;       // [hash] int32 fixed point
   float *grad_mlp;          // [mlp]
-  uint8_t *mask;            // per-entry visit flags
+  const uint8_t *mask;      // per-entry visit flags of this step
+  uint8_t *mask_next;       // the other flag buffer: zeroed here for the next step
+  uint32_t partner_xor;     // 2D: z = 1 entry = z = 0 entry ^ partner_xor (0: none)
+  uint32_t log2T;
   int32_t lazy;             // 1: update visited entries only; 0: every entry
   uint32_t hash_entries;    // L * T (hash floats = hash_entries * F)
   uint32_t mlp_count;
   float lr_hash, lr_mlp, beta1, beta2, eps, bc1, bc2;
   float l1_hash, l2_mlp, grad_clip, weight_decay;
   int32_t clear_grads;      // zero consumed gradients (fused step)
-  int32_t clear_mask;       // zero consumed visit flags
+  int32_t clear_mask;       // zero mask_next (the caller then swaps the buffers)
 };
 
 // One Adam element (adam_kernel_msl.h:67-108, :137-163, :183-202).
@@ -146,8 +150,8 @@ __device__ __forceinline__ void adam_update(float &w, float &mo, float &ve,
 }
 
 // One pass over [hash entries | mlp params]. Thread j < hash_entries owns
-// table entry j (its F floats); in lazy mode the entry is updated only if its
-// visit flag is set -- the lazy sparse semantics of
+// table entry j (its F floats); in lazy mode the entry is updated only if it
+// was visited (its flag, or for lifted 2D points its z = 0 partner's flag) -- the lazy sparse semantics of
 // neural_sdf_adam_hash_sparse (adam_kernel_msl.h:120-164) without the host
 // compaction (default_trainer.cpp:1882-1960). Threads past the table own one
 // MLP parameter each (neural_sdf_adam_mlp_dense, adam_kernel_msl.h:166-203).
@@ -157,13 +161,22 @@ __global__ void adam_kernel(AdamArgs a) {
   const uint32_t stride = gridDim.x * blockDim.x;
   for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < total; j += stride) {
     if (j < a.hash_entries) {
-      const bool visited = a.mask[j] != 0;
-      if (visited && a.clear_mask) a.mask[j] = 0;
+      bool visited = a.mask[j] != 0;
+      if (a.partner_xor) {  // lifted 2D: also visited as some corner's z = 1 partner
+        const uint32_t tmask = (1u << a.log2T) - 1u;
+        visited = visited || a.mask[(j & ~tmask) | ((j & tmask) ^ a.partner_xor)] != 0;
+      }
+      if (a.clear_mask) a.mask_next[j] = 0;
       if (a.lazy && !visited) continue;
+      int32_t gi[F];
+#pragma unroll
+      for (int f = 0; f < F; ++f) gi[f] = a.grad_hash[static_cast<size_t>(j) * F + f];
+      // F == 2 entries accumulate as one packed 64-bit sum (scatter_kernel.hpp)
+      if constexpr (F == 2) gi[1] = unpack_hi(gi[0], gi[1]);
 #pragma unroll
       for (int f = 0; f < F; ++f) {
         const size_t i = static_cast<size_t>(j) * F + f;
-        const float g = static_cast<float>(a.grad_hash[i]) * (1.0f / 65536.0f);
+        const float g = static_cast<float>(gi[f]) * (1.0f / 65536.0f);
         float w = a.params[i], mo = a.m[i], ve = a.v[i];
         adam_update(w, mo, ve, g, a.lr_hash, a, false);
         a.params[i] = w;

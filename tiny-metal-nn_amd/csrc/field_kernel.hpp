@@ -4,8 +4,10 @@
 //   hash-grid encode (gathers straight into MFMA B-operand registers)
 //   -> MLP forward on MFMA (weights resident in LDS as A-operand fragments)
 //   -> loss + output gradient                          [training modes]
-//   -> MLP backward on MFMA, dW reduced per block in LDS [training modes]
-//   -> input-feature gradient -> int32 fixed-point hash scatter + lazy mask
+//   -> MLP backward on MFMA, dW accumulated per wave    [training modes]
+//   -> input-feature gradient dx, stored per point      [training modes]
+// and hash_scatter_kernel then turns dx into the int32 fixed-point hash
+// gradients and lazy-Adam visit flags, one thread per (point, level).
 //
 // Reference semantics (paths relative to the reference checkout):
 //   encode      mlp_kernel_emitter.cpp:205-360 (emitHashEncodeUnified)
@@ -54,7 +56,6 @@ struct FieldArgs {
   float inv_n;              // fl(1/N) of the loss (emitScalarTrainKernelImpl)
   float loss_scale;         // power of two applied to d_out in the fp16 path
   float inv_loss_scale;
-  int32_t lift2d_mask;      // mark the lifted z=1 corners of 2D points
   int32_t dw_global;        // dW accumulator in grad_partials (LDS too small)
   int32_t mlp_count;
   float res[kMaxLevels];    // per-level resolution table
@@ -62,10 +63,10 @@ struct FieldArgs {
   const float *target;      // [n][M] target (TrainLoss) or d_out (TrainExtGrad)
   const float *table;       // [L][T][F] fp32
   const float *mlp;         // fp32 master MLP params (reference layout)
+  const unsigned char *image; // packed LDS head (pack_image_kernel), s.dw_off bytes
   float *out;               // [n][M] (Forward)
   const uint32_t *out_index;// nullable: row of out[] for point i
-  int32_t *grad_hash;       // [L][T][F] int32 fixed point
-  uint8_t *mask;            // lazy-Adam visit flags, one byte per table entry
+  float *dx_out;            // [n][IN] input-feature gradients (training)
   float *grad_partials;     // [gridDim.x][mlp_count]
   float *loss_partials;     // [gridDim.x]
 };
@@ -137,6 +138,7 @@ __host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
   off += (NHL * HP + 16) * 4;
   s.res_off = off;
   off += kMaxLevels * 4;
+  off = round_up(off, 16);  // end of the packed image (copied in 16-byte units)
   s.dw_off = off;
   s.dw_global = dw_global ? 1 : 0;
   if (train && !dw_global && !reg_dw) off += round_up(mlp_count, 4) * 4;
@@ -484,206 +486,217 @@ __device__ __forceinline__ void encode_tile(const FieldArgs &a, const float *res
   }
 }
 
-// Visit flag of one table entry: a plain byte store. Every writer stores the
-// same value, so concurrent marks need no atomics (the reference's bit-mask
-// atomic_fetch_or, mlp_kernel_emitter.cpp:48-71, marks the same set: all F
-// floats of every visited corner, zero-weight corners included).
-__device__ __forceinline__ void mark_entry(uint8_t *mask, size_t entry) {
-  mask[entry] = 1;
-}
+// ----------------------------------------------- software-pipelined encode --
+//
+// The geometry-specialised kernels split the encode of a wave tile in two:
+// gather_issue computes the corners and issues every table load of the tile
+// into registers; gather_finish (one tile later in program order, after the
+// previous tile's backward) applies the corner weights. The loads of tile i+1
+// are in flight while tile i runs its MLP backward.
 
-// Gradient scatter of one level: int32((d * w) * 65536) per corner and
-// feature on the reference's float2 path (F == 2, 2D/3D), else
-// int32(d * wx * wy * wz (* wt) * 65536); every visited corner sets its
-// entry's lazy-Adam visit flag.
-template <int D, int F>
-__device__ __forceinline__ void scatter_level(const FieldArgs &a, int l,
-                                              const float *p, float res,
-                                              const float *d) {
-  const Cell<D> c = cell_of<D>(p, res);
-  const uint32_t tmask = (1u << a.log2T) - 1u;
-  const size_t lbase = static_cast<size_t>(l) << a.log2T;
-  constexpr bool kVec2 = (F == 2 && D <= 3);
-#pragma unroll
-  for (int k = 0; k < (1 << D); ++k) {
-    int co[D];
-    float wc[D];
-    corner_of<D>(c, k, co, wc);
-    const size_t entry = lbase + hash_corner<D>(co, tmask);
-    const float w = corner_weight<D>(wc);
-#pragma unroll
-    for (int f = 0; f < F; ++f) {
-      float v;
-      if constexpr (kVec2) {
-        v = d[f] * w;
-      } else {
-        v = d[f] * wc[0];
-        v = v * wc[1];
-        if constexpr (D >= 3) v = v * wc[2];
-        if constexpr (D == 4) v = v * wc[3];
-      }
-      const int32_t ci = f2i_trunc(v * kGradScale);
-      if (ci != 0) atomicAdd(a.grad_hash + entry * F + f, ci);
-    }
-    mark_entry(a.mask, entry);
-    if constexpr (D == 2) {
-      if (a.lift2d_mask) mark_entry(a.mask, lbase + hash_corner_lift_z1(co, tmask));
-    }
-  }
-}
-
-template <int D, int F>
-__device__ __forceinline__ void scatter_quad_t(const FieldArgs &a,
-                                               const float *res, int fb,
-                                               const float *p, f32x4 dq) {
-  if constexpr (F == 1) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int l = fb + r;
-      if (l < a.L) {
-        const float d[1] = {dq[r]};
-        scatter_level<D, 1>(a, l, p, res[l], d);
-      }
-    }
-  } else if constexpr (F == 2) {
-#pragma unroll
-    for (int lv = 0; lv < 2; ++lv) {
-      const int l = fb / 2 + lv;
-      if (l < a.L) {
-        const float d[2] = {dq[2 * lv], dq[2 * lv + 1]};
-        scatter_level<D, 2>(a, l, p, res[l], d);
-      }
-    }
-  } else {
-    const int l = fb / 4;
-    if (l < a.L) {
-      const float d[4] = {dq[0], dq[1], dq[2], dq[3]};
-      scatter_level<D, 4>(a, l, p, res[l], d);
-    }
-  }
-}
-
-// Scatter every input-feature gradient quad of the wave tile for one (D, F).
 template <int D, int F, int KT0>
-__device__ __forceinline__ void scatter_tile_t(const FieldArgs &a,
-                                               const float *res, int q,
-                                               const float (&P)[kNT][4],
-                                               const bool (&valid)[kNT],
-                                               const f32x4 (&dx)[KT0][kNT]) {
+struct Gathered {
+  static constexpr int LPQ = 4 / F;  // levels per feature quad
+  static constexpr int C = 1 << D;   // corners per level
+  float v[kNT][KT0][LPQ][C][F];
+};
+
+template <int D, int F, int KT0>
+__device__ __forceinline__ void gather_issue(const FieldArgs &a, const float *res, int q,
+                                             const float (&P)[kNT][4],
+                                             Gathered<D, F, KT0> &g) {
+  constexpr int LPQ = Gathered<D, F, KT0>::LPQ;
+  const uint32_t tmask = (1u << a.log2T) - 1u;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    if (!valid[nt]) continue;
-    const float pp[4] = {P[nt][0], P[nt][1], P[nt][2], P[nt][3]};
-#pragma unroll 1
-    for (int kt = 0; kt < KT0; ++kt) {
-      f32x4 dq = {0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-      for (int j = 0; j < KT0; ++j)
-        if (j == kt) dq = dx[j][nt];
+    for (int kt = 0; kt < KT0; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dq[r] = dq[r] * a.inv_loss_scale;
-      scatter_quad_t<D, F>(a, res, 16 * kt + 4 * q, pp, dq);
-    }
-  }
+      for (int lv = 0; lv < LPQ; ++lv) {
+        const int l = (16 * kt + 4 * q) / F + lv;
+        const bool on = l < a.L;
+        const Cell<D> c = cell_of<D>(P[nt], res[on ? l : 0]);
+#pragma unroll
+        for (int k = 0; k < (1 << D); ++k) {
+          int co[D];
+          float wc[D];
+          corner_of<D>(c, k, co, wc);
+          const uint32_t h = hash_corner<D>(co, tmask);
+          const float *e = a.table + ((static_cast<size_t>(on ? l : 0) << a.log2T) + h) * F;
+          if constexpr (F == 1) {
+            g.v[nt][kt][lv][k][0] = on ? e[0] : 0.0f;
+          } else if constexpr (F == 2) {
+            const f32x2 t = on ? *reinterpret_cast<const f32x2 *>(e) : f32x2{0.f, 0.f};
+            g.v[nt][kt][lv][k][0] = t[0];
+            g.v[nt][kt][lv][k][1] = t[1];
+          } else {
+            const f32x4 t = on ? *reinterpret_cast<const f32x4 *>(e) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int f = 0; f < 4; ++f) g.v[nt][kt][lv][k][f] = t[f];
+          }
+        }
+      }
 }
 
-template <int KT0, int DF>
-__device__ __forceinline__ void scatter_tile(const FieldArgs &a, const float *res,
-                                             int q, const float (&P)[kNT][4],
-                                             const bool (&valid)[kNT],
-                                             const f32x4 (&dx)[KT0][kNT]) {
-  if constexpr (DF != 0) {
-    scatter_tile_t<DF / 8, DF % 8, KT0>(a, res, q, P, valid, dx);
-    return;
-  }
-  switch (a.D * 8 + a.F) {
-    case 2 * 8 + 1: scatter_tile_t<2, 1, KT0>(a, res, q, P, valid, dx); break;
-    case 2 * 8 + 2: scatter_tile_t<2, 2, KT0>(a, res, q, P, valid, dx); break;
-    case 2 * 8 + 4: scatter_tile_t<2, 4, KT0>(a, res, q, P, valid, dx); break;
-    case 3 * 8 + 1: scatter_tile_t<3, 1, KT0>(a, res, q, P, valid, dx); break;
-    case 3 * 8 + 2: scatter_tile_t<3, 2, KT0>(a, res, q, P, valid, dx); break;
-    case 3 * 8 + 4: scatter_tile_t<3, 4, KT0>(a, res, q, P, valid, dx); break;
-    case 4 * 8 + 1: scatter_tile_t<4, 1, KT0>(a, res, q, P, valid, dx); break;
-    case 4 * 8 + 2: scatter_tile_t<4, 2, KT0>(a, res, q, P, valid, dx); break;
-    default: scatter_tile_t<4, 4, KT0>(a, res, q, P, valid, dx); break;
-  }
+// Interpolation of gathered corners in the reference's order (features start
+// at 0, corners z, y, x ascending, weight ((wx * wy) * wz)(* wt)).
+template <int D, int F, int KT0>
+__device__ __forceinline__ void gather_finish(const FieldArgs &a, const float *res, int q,
+                                              const float (&P)[kNT][4],
+                                              const Gathered<D, F, KT0> &g,
+                                              f32x4 (&X)[KT0][kNT]) {
+  constexpr int LPQ = Gathered<D, F, KT0>::LPQ;
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+    for (int kt = 0; kt < KT0; ++kt) {
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int lv = 0; lv < LPQ; ++lv) {
+        const int l = (16 * kt + 4 * q) / F + lv;
+        const Cell<D> c = cell_of<D>(P[nt], res[l < a.L ? l : 0]);
+        float feat[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) feat[f] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < (1 << D); ++k) {
+          int co[D];
+          float wc[D];
+          corner_of<D>(c, k, co, wc);
+          const float w = corner_weight<D>(wc);
+#pragma unroll
+          for (int f = 0; f < F; ++f) feat[f] = feat[f] + w * g.v[nt][kt][lv][k][f];
+        }
+#pragma unroll
+        for (int f = 0; f < F; ++f) o[lv * F + f] = l < a.L ? feat[f] : 0.0f;
+      }
+      X[kt][nt] = o;
+    }
 }
 
 // ------------------------------------------------------------ LDS staging --
 
+
+// ----------------------------------------------------- weight image packing --
+//
+// The head of the kernel's LDS plan -- [fwd A fragments (hi) | fwd lo
+// fragments (fp16) | bwd A fragments | fp32 biases | resolution table] -- is
+// the same for every block, so it is built once per weight update by
+// pack_image_kernel (one thread per element) and each block copies it into
+// LDS with 16-byte loads.
+
+enum : int32_t { kSecFwd = 0, kSecBwd = 1, kSecBias = 2, kSecRes = 3 };
+constexpr int kMaxSections = 3 * kMaxLayers + 1;
+
+struct PackArgs {
+  FieldLayout s;
+  int32_t f16;
+  int32_t L;
+  int32_t nsec;
+  int32_t sec_start[kMaxSections + 1];  // element prefix over the sections
+  int32_t sec_kind[kMaxSections];
+  int32_t sec_layer[kMaxSections];
+  float res[kMaxLevels];
+  const float *mlp;                      // fp32 master MLP params (reference layout)
+  unsigned char *image;                  // s.dw_off bytes
+};
+
 // K-slot order of one fp16 A fragment: slot (q, j) of K step ks covers unit
 // 32*ks + 4*q + j (j < 4) or 32*ks + 16 + 4*q + (j - 4) (j >= 4), matching
 // pack8() of two D-layout tiles.
-__device__ __forceinline__ int kslot_f16(int ks, int q, int j) {
+__host__ __device__ inline int kslot_f16(int ks, int q, int j) {
   return 32 * ks + (j < 4 ? 4 * q + j : 16 + 4 * q + (j - 4));
 }
 
-template <int HP, int INP, bool F16, bool TRAIN, bool REGDW>
-__device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLayout &s,
-                              unsigned char *smem) {
-  const int tid = threadIdx.x;
-  const int nthr = blockDim.x;
-  for (int k = 0; k <= a.NHL; ++k) {
-    const int kin = k == 0 ? INP : HP;
-    const int kreal = k == 0 ? a.IN : a.H;
-    const int mout = k == a.NHL ? 16 : HP;
-    const int mreal = k == a.NHL ? a.M : a.H;
-    const float *W = a.mlp + s.w_off(k);
-    // forward: A = W_k^T, rows = output units, K = input units
-    const int nf = kin * mout;
-    for (int e = tid; e < nf; e += nthr) {
-      int i, o;
-      if constexpr (F16) {
-        const int j = e & 7, lane = (e >> 3) & 63, f = e >> 9;
-        const int ks_n = kin / 32, mt = f / ks_n, ks = f % ks_n;
-        i = kslot_f16(ks, lane >> 4, j);
-        o = 16 * mt + (lane & 15);
-      } else {
-        const int r = e & 3, lane = (e >> 2) & 63, f = e >> 8;
-        const int kt_n = kin / 16, mt = f / kt_n, kt = f % kt_n;
-        i = 16 * kt + 4 * (lane >> 4) + r;
-        o = 16 * mt + (lane & 15);
-      }
-      const float v = (i < kreal && o < mreal) ? W[i * mreal + o] : 0.0f;
-      if constexpr (F16) {
+// Value of element e of layer k's forward (A = W_k^T) or backward (A = W_k)
+// fragments: the fragment slot -> (input unit i, output unit o) mapping.
+__host__ __device__ inline float frag_value(const PackArgs &a, int k, bool bwd, int e) {
+  const FieldLayout &s = a.s;
+  const int kin = k == 0 ? s.INP : s.HP;
+  const int kreal = k == 0 ? s.IN : s.H;
+  const int mout = k == s.NHL ? 16 : s.HP;
+  const int mreal = k == s.NHL ? s.M : s.H;
+  int i, o;
+  if (a.f16) {
+    const int j = e & 7, lane = (e >> 3) & 63, f = e >> 9;
+    if (!bwd) {
+      const int ks_n = kin / 32, mt = f / ks_n, ks = f % ks_n;
+      i = kslot_f16(ks, lane >> 4, j);
+      o = 16 * mt + (lane & 15);
+    } else {
+      const int ko = round_up(mout, 32);
+      const int ks_n = ko / 32, mt = f / ks_n, ks = f % ks_n;
+      i = 16 * mt + (lane & 15);
+      o = kslot_f16(ks, lane >> 4, j);
+    }
+  } else {
+    const int r = e & 3, lane = (e >> 2) & 63, f = e >> 8;
+    if (!bwd) {
+      const int kt_n = kin / 16, mt = f / kt_n, kt = f % kt_n;
+      i = 16 * kt + 4 * (lane >> 4) + r;
+      o = 16 * mt + (lane & 15);
+    } else {
+      const int kt_n = mout / 16, mt = f / kt_n, kt = f % kt_n;
+      i = 16 * mt + (lane & 15);
+      o = 16 * kt + 4 * (lane >> 4) + r;
+    }
+  }
+  return (i < kreal && o < mreal) ? a.mlp[s.w_off(k) + i * mreal + o] : 0.0f;
+}
+
+__global__ void pack_image_kernel(PackArgs a) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= a.sec_start[a.nsec]) return;
+  int sec = 0;
+  while (g >= a.sec_start[sec + 1]) ++sec;
+  const int e = g - a.sec_start[sec];
+  const int k = a.sec_layer[sec];
+  const FieldLayout &s = a.s;
+  switch (a.sec_kind[sec]) {
+    case kSecFwd: {
+      const float v = frag_value(a, k, false, e);
+      if (a.f16) {
         const _Float16 hi = static_cast<_Float16>(v);
-        reinterpret_cast<_Float16 *>(smem + s.fwd_off(k))[e] = hi;
-        reinterpret_cast<_Float16 *>(smem + s.fwd_lo_off(k))[e] =
+        reinterpret_cast<_Float16 *>(a.image + s.fwd_off(k))[e] = hi;
+        reinterpret_cast<_Float16 *>(a.image + s.fwd_lo_off(k))[e] =
             static_cast<_Float16>(v - static_cast<float>(hi));
       } else {
-        reinterpret_cast<float *>(smem + s.fwd_off(k))[e] = v;
+        reinterpret_cast<float *>(a.image + s.fwd_off(k))[e] = v;
       }
+      break;
     }
-    if constexpr (TRAIN) {
-      // backward: A = W_k, rows = input units, K = output units
-      const int ko = F16 ? round_up(mout, 32) : mout;
-      const int nb = kin * ko;
-      for (int e = tid; e < nb; e += nthr) {
-        int i, o;
-        if constexpr (F16) {
-          const int j = e & 7, lane = (e >> 3) & 63, f = e >> 9;
-          const int ks_n = ko / 32, mt = f / ks_n, ks = f % ks_n;
-          i = 16 * mt + (lane & 15);
-          o = kslot_f16(ks, lane >> 4, j);
-        } else {
-          const int r = e & 3, lane = (e >> 2) & 63, f = e >> 8;
-          const int kt_n = ko / 16, mt = f / kt_n, kt = f % kt_n;
-          i = 16 * mt + (lane & 15);
-          o = 16 * kt + 4 * (lane >> 4) + r;
-        }
-        const float v = (i < kreal && o < mreal) ? W[i * mreal + o] : 0.0f;
-        if constexpr (F16)
-          reinterpret_cast<_Float16 *>(smem + s.bwd_off(k))[e] = static_cast<_Float16>(v);
-        else
-          reinterpret_cast<float *>(smem + s.bwd_off(k))[e] = v;
-      }
+    case kSecBwd: {
+      const float v = frag_value(a, k, true, e);
+      if (a.f16)
+        reinterpret_cast<_Float16 *>(a.image + s.bwd_off(k))[e] = static_cast<_Float16>(v);
+      else
+        reinterpret_cast<float *>(a.image + s.bwd_off(k))[e] = v;
+      break;
     }
-    for (int e = tid; e < mout; e += nthr)
-      reinterpret_cast<float *>(smem + s.bias_off(k))[e] =
+    case kSecBias: {
+      const int mreal = k == s.NHL ? s.M : s.H;
+      reinterpret_cast<float *>(a.image + s.bias_off(k))[e] =
           e < mreal ? a.mlp[s.b_off(k) + e] : 0.0f;
+      break;
+    }
+    default:
+      reinterpret_cast<float *>(a.image + s.res_off)[e] = e < a.L ? a.res[e] : 0.0f;
+      break;
   }
-  for (int e = tid; e < kMaxLevels; e += nthr)
-    reinterpret_cast<float *>(smem + s.res_off)[e] = e < a.L ? a.res[e] : 0.0f;
+}
+
+// Block-wide copy of the packed image into LDS (+ zeroing of an LDS or
+// global dW accumulator for the generic kernels).
+template <bool TRAIN, bool REGDW>
+__device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLayout &s,
+                                              unsigned char *smem) {
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int n16 = s.dw_off / 16;
+  const uint4 *src = reinterpret_cast<const uint4 *>(a.image);
+  uint4 *dst = reinterpret_cast<uint4 *>(smem);
+#pragma unroll 4
+  for (int e = tid; e < n16; e += nthr) dst[e] = src[e];
   if constexpr (TRAIN && !REGDW) {
     if (s.dw_global) {
       float *dwg = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
@@ -841,7 +854,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   const FieldLayout s = make_layout(INP, HP, a.IN, a.H, NHL, a.M,
                                     a.mlp_count, F16, TRAIN, a.waves_per_block,
                                     a.dw_global != 0, REGDW);
-  stage_weights<HP, INP, F16, TRAIN, REGDW>(a, s, smem);
+  stage_weights<TRAIN, REGDW>(a, s, smem);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -881,23 +894,56 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
     for (int r = 0; r < 4; ++r) R.bo[r] = 0.0f;
   }
 
-  for (int tile = blockIdx.x * a.waves_per_block + wave; tile < a.n_tiles;
-       tile += gridDim.x * a.waves_per_block) {
+  // Positions of a tile (zero past the batch).
+  auto load_pos = [&](int t, float (&Pt)[kNT][4]) {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const int i = t * kTilePts + 16 * nt + p;
+      const bool ok = t < a.n_tiles && i < a.n;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        Pt[nt][d] = (ok && d < a.D) ? a.pos[static_cast<size_t>(i) * a.D + d] : 0.0f;
+    }
+  };
+  // Specialised kernels pipeline the gathers when the in-flight corner values
+  // fit in registers (<= 128 floats per lane; e.g. not for 3D x 4 features).
+  constexpr bool kPipe =
+      DF != 0 && kNT * KT0 * (DF ? (4 / (DF % 8)) * (1 << (DF / 8)) * (DF % 8) : 0) <= 128;
+  const int tile_stride = gridDim.x * a.waves_per_block;
+  int tile = blockIdx.x * a.waves_per_block + wave;
+  float P[kNT][4];
+  load_pos(tile, P);
+  Gathered<(DF ? DF / 8 : 2), (DF ? DF % 8 : 2), KT0> G;
+  if constexpr (kPipe) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, P, G);
+
+  for (; tile < a.n_tiles; tile += tile_stride) {
+    const int next = tile + tile_stride;
     int pt[kNT];
     bool valid[kNT];
-    float P[kNT][4];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       pt[nt] = tile * kTilePts + 16 * nt + p;
       valid[nt] = pt[nt] < a.n;
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        P[nt][d] = (valid[nt] && d < a.D) ? a.pos[static_cast<size_t>(pt[nt]) * a.D + d] : 0.0f;
     }
 
     // ---- encode: input features 16*kt + 4*q + r of point 16*nt + p
     f32x4 X[KT0][kNT];
-    encode_tile<KT0, DF>(a, res, q, P, X);
+    if constexpr (kPipe)
+      gather_finish<DF / 8, DF % 8, KT0>(a, res, q, P, G, X);
+    else
+      encode_tile<KT0, DF>(a, res, q, P, X);
+    // prefetch: the next tile's positions and this tile's targets / d_out
+    float Pn[kNT][4];
+    load_pos(next, Pn);
+    float Tv[kNT][4];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        Tv[nt][r] = (TRAIN && valid[nt] && o < a.M)
+                        ? a.target[static_cast<size_t>(pt[nt]) * a.M + o] : 0.0f;
+      }
     if constexpr (TRAIN) store_tiles<F16, KT0>(Xs, X, p, q);
 
     // ---- MLP forward
@@ -939,6 +985,13 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[0][nt][r] = y[0][nt][r] + bias[4 * q + r];
     }
+    // the next tile's gathers fly while this tile finishes
+    if constexpr (kPipe)
+      if (next < a.n_tiles) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, Pn, G);
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) P[nt][d] = Pn[nt][d];
 
     if constexpr (!TRAIN) {
 #pragma unroll
@@ -965,8 +1018,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int o = 4 * q + r;
-            if (valid[nt] && o < a.M)
-              g[0][nt][r] = a.target[static_cast<size_t>(pt[nt]) * a.M + o] * a.loss_scale;
+            if (valid[nt] && o < a.M) g[0][nt][r] = Tv[nt][r] * a.loss_scale;
           }
       } else if (a.loss_kind == kLossCosine) {
         // emitLoss cosine branch (mlp_kernel_emitter.cpp:643-662)
@@ -978,7 +1030,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
           for (int r = 0; r < 4; ++r) {
             const int o = 4 * q + r;
             const bool ok = valid[nt] && o < a.M;
-            tv[r] = ok ? a.target[static_cast<size_t>(pt[nt]) * a.M + o] : 0.0f;
+            tv[r] = ok ? Tv[nt][r] : 0.0f;
             const float yv = ok ? y[0][nt][r] : 0.0f;
             dot = dot + yv * tv[r];
             pn = pn + yv * yv;
@@ -1016,9 +1068,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
             const int o = 4 * q + r;
             if (valid[nt] && o < a.M) {
               float d;
-              lane_loss += elem_loss(a.loss_kind, y[0][nt][r],
-                                     a.target[static_cast<size_t>(pt[nt]) * a.M + o],
-                                     a.huber_delta, a.inv_n, &d);
+              lane_loss += elem_loss(a.loss_kind, y[0][nt][r], Tv[nt][r], a.huber_delta,
+                                     a.inv_n, &d);
               g[0][nt][r] = d * a.loss_scale;
             }
           }
@@ -1171,7 +1222,26 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       }
       f32x4 dx[KT0][kNT];
       layer_mma<F16, HT, KT0>(smem + s.bwd_off(0), dl, dx, lane);
-      scatter_tile<KT0, DF>(a, res, q, P, valid, dx);
+      // dx (D layout: feature 16*kt + 4*q + r of point 16*nt + p) -> [n][IN]
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        if (!valid[nt]) continue;
+        float *row = a.dx_out + static_cast<size_t>(pt[nt]) * a.IN;
+#pragma unroll
+        for (int kt = 0; kt < KT0; ++kt) {
+          const int f0 = 16 * kt + 4 * q;
+          f32x4 v = dx[kt][nt];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = v[r] * a.inv_loss_scale;
+          if (f0 + 3 < a.IN && (a.IN & 3) == 0) {
+            *reinterpret_cast<f32x4 *>(row + f0) = v;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (f0 + r < a.IN) row[f0 + r] = v[r];
+          }
+        }
+      }
     }
   }
 

@@ -1,0 +1,156 @@
+// scatter_kernel.hpp -- hash-grid backward: input-feature gradients dx of a
+// batch -> int32 fixed-point table gradients + lazy-Adam visit flags.
+//
+// One thread per (point, level); the grid is level-major (blockIdx.y =
+// level), so at any moment the resident blocks hit one level's slice of the
+// table and Morton-sorted neighbours share cache lines. Few registers and no
+// LDS: many waves per SIMD hide the atomic latency.
+//
+// Reference semantics (emitHashScatter, mlp_kernel_emitter.cpp:672-901;
+// mask :48-71): per corner and feature, int32(trunc(d * w * 65536)) with
+// w = ((wx * wy) * wz) on the float2 path (F == 2, 2D/3D), else
+// ((d * wx) * wy) * wz (* wt); every visited corner (zero weight included)
+// is marked; for the reference's lifted 2D points the z = 1 corners count as
+// visited too, which Adam reads off the z = 0 partner's flag (the z = 1 entry
+// of a corner is its z = 0 entry XOR (805459861 mod T) within the level).
+//
+// Lanes of a wave hold consecutive Morton-sorted points of one level; runs of
+// lanes that hit the same entry are summed across lanes first and issue one
+// atomic (and one flag store) per run.
+//
+// F == 2 packs both features of an entry into one 64-bit atomic:
+//   S += (int64)c1 * 2^32 + (int64)c0   (c0 sign-extended)
+// The low word is then exactly the int32 (wrapping) sum of c0, the high word
+// the sum of c1 minus one when that low sum is negative. Readers restore
+// feature 1 as hi + (lo < 0), exact whenever the true sum of c0 stays in
+// int32 range (|gradient| < 32768), as the reference's own sum must.
+#pragma once
+
+#include "device_common.hpp"
+
+namespace tmnn_hip {
+
+struct ScatterArgs {
+  int32_t n;                 // points
+  int32_t IN;                // L * F (row stride of dx)
+  uint32_t log2T;
+  float res[kMaxLevels];     // per-level resolution table
+  const float *pos;          // [n][D], the order dx was produced in
+  const float *dx;           // [n][IN]
+  int32_t *grad_hash;        // [L][T][F]
+  uint8_t *mask;             // [L][T] visit flags
+};
+
+constexpr int kScatterThreads = 256;
+
+// Visit flag of one table entry: a plain byte store. Every writer stores the
+// same value, so concurrent marks need no atomics (the reference's bit-mask
+// atomic_fetch_or marks the same set: all F floats of a visited corner).
+__device__ __forceinline__ void mark_entry(uint8_t *mask, size_t entry) { mask[entry] = 1; }
+
+// feature 1 of a packed F == 2 gradient entry (see the file comment)
+__host__ __device__ inline int32_t unpack_hi(int32_t lo, int32_t hi) {
+  return static_cast<int32_t>(static_cast<uint32_t>(hi) + (lo < 0 ? 1u : 0u));
+}
+
+// Sum of v over the run of equal keys that ends at this lane (runs are
+// maximal sequences of equal keys in lane order); is_tail is set on the last
+// lane of each run, which then owns the run's total. Integer sums are exact
+// in any order, so merging lanes leaves the table gradients bit-identical.
+__device__ __forceinline__ int64_t run_sum(uint32_t key, int64_t v, int lane, bool *is_tail) {
+  const uint32_t prev = __shfl_up(key, 1);
+  const bool head = lane == 0 || prev != key;
+  const uint64_t heads = __ballot(head);
+  if (heads == ~0ull) {  // no two neighbours share an entry
+    *is_tail = true;
+    return v;
+  }
+  const uint64_t le = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+  const int start = 63 - __clzll(heads & le);  // first lane of this lane's run
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t up = __shfl_up(v, off);
+    if (lane - off >= start) v += up;
+  }
+  *is_tail = lane == 63 || ((heads >> (lane + 1)) & 1ull);
+  return v;
+}
+
+template <int D, int F>
+__global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterArgs a) {
+  const int l = blockIdx.y;
+  const int i = blockIdx.x * kScatterThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  // lanes past the batch take part in the wave's run merging with a key no
+  // point can have and nothing to add
+  const bool valid = i < a.n;
+  const int ii = valid ? i : a.n - 1;
+  float p[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(ii) * D + k];
+  float d[F];
+  const float *src = a.dx + static_cast<size_t>(ii) * a.IN + l * F;
+  if constexpr (F == 2) {
+    const f32x2 v = *reinterpret_cast<const f32x2 *>(src);
+    d[0] = v[0];
+    d[1] = v[1];
+  } else if constexpr (F == 4) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(src);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) d[f] = v[f];
+  } else {
+    d[0] = src[0];
+  }
+  const Cell<D> c = cell_of<D>(p, a.res[l]);
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+  constexpr bool kVec2 = (F == 2 && D <= 3);
+#pragma unroll
+  for (int k = 0; k < (1 << D); ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const uint32_t local = valid ? hash_corner<D>(co, tmask) : 0xFFFFFFFFu;
+    const size_t entry = lbase + local;
+    int32_t ci[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      float v;
+      if constexpr (kVec2) {
+        v = d[f] * corner_weight<D>(wc);
+      } else {
+        v = d[f] * wc[0];
+        v = v * wc[1];
+        if constexpr (D >= 3) v = v * wc[2];
+        if constexpr (D == 4) v = v * wc[3];
+      }
+      ci[f] = valid ? f2i_trunc(v * kGradScale) : 0;
+    }
+    bool tail = true;
+    if constexpr (F == 2) {
+      // packed pair (see the file comment); merged over runs of equal entries
+      int64_t v64 = static_cast<int64_t>(
+          (static_cast<uint64_t>(static_cast<uint32_t>(ci[1])) << 32) +
+          static_cast<uint64_t>(static_cast<int64_t>(ci[0])));
+      v64 = run_sum(local, v64, lane, &tail);
+      if (valid && tail) {
+        if (v64 != 0)
+          atomicAdd(reinterpret_cast<unsigned long long *>(a.grad_hash + entry * 2),
+                    static_cast<unsigned long long>(v64));
+        mark_entry(a.mask, entry);
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < F; ++f) {
+        bool t;
+        const int64_t sum = run_sum(local, ci[f], lane, &t);
+        tail = t;
+        if (valid && t && sum != 0)
+          atomicAdd(a.grad_hash + entry * F + f, static_cast<int32_t>(sum));
+      }
+      if (valid && tail) mark_entry(a.mask, entry);
+    }
+  }
+}
+
+}  // namespace tmnn_hip

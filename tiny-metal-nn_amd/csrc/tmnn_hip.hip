@@ -23,6 +23,7 @@
 #include "tmnn_hip.h"
 #include "aux_kernels.hpp"
 #include "field_kernel.hpp"
+#include "scatter_kernel.hpp"
 #include "sort.hpp"
 
 using namespace tmnn_hip;
@@ -127,6 +128,10 @@ struct DevBuf {
 
 struct KernelPlan {
   FieldKernel fn = nullptr;
+  bool f16 = false, train = false;
+  uint64_t packed_version = ~0ull;  // weights version of the packed LDS image
+  void *image = nullptr;            // device copy of the LDS head (weights, biases, res)
+  size_t image_bytes = 0;
   int wpb = 0;          // waves per block
   int lds = 0;          // dynamic LDS bytes
   bool dw_global = false;  // dW accumulator outside LDS
@@ -155,16 +160,20 @@ struct tmnn_trainer {
   uint32_t step = 0;
   float lr_enc = 0.f, lr_net = 0.f;
 
-  DevBuf params, m, v, grad_hash, grad_mlp, mask;
+  DevBuf params, m, v, grad_hash, grad_mlp;
+  DevBuf mask[2];  // visit flags, double-buffered: Adam reads one, zeroes the other
+  int mask_cur = 0;
   DevBuf partials, loss_partials, loss_out;
   DevBuf in_pos, in_tgt, s_pos, s_tgt, keys0, keys1, vals0, vals1, sort_tmp, out_buf;
+  DevBuf dx;  // [batch][IN] input-feature gradients between the two train kernels
   DevBuf dbg_a, dbg_b, dbg_c;
 
   KernelPlan train_plan, fwd_plan, infer_plan;
+  uint64_t weights_version = 0;  // bumped whenever the parameters change
 
   // Step profiling: one set of phase events per profiled step, summed and
   // recycled when the profile is read.
-  static constexpr int kProfEvents = 5;  // sort | fwd/bwd | reduce | adam |
+  static constexpr int kProfEvents = 6;  // sort | fwd/bwd | scatter | reduce | adam |
   bool profiling = false;
   std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
   size_t prof_used = 0;
@@ -172,6 +181,8 @@ struct tmnn_trainer {
   tmnn_step_profile prof_acc{};
 
   ~tmnn_trainer() {
+    for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan})
+      if (p->image) (void)hipFree(p->image);
     for (auto &set : prof_events)
       for (hipEvent_t e : set)
         if (e) (void)hipEventDestroy(e);
@@ -242,9 +253,10 @@ int prof_collect(tmnn_trainer *tr) {
       TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[k], e[k + 1]));
     tr->prof_acc.gpu_sort_us += 1e3 * ms[0];
     tr->prof_acc.gpu_fwd_bwd_us += 1e3 * ms[1];
-    tr->prof_acc.gpu_reduce_us += 1e3 * ms[2];
-    tr->prof_acc.gpu_adam_us += 1e3 * ms[3];
-    tr->prof_acc.gpu_total_us += 1e3 * (ms[0] + ms[1] + ms[2] + ms[3]);
+    tr->prof_acc.gpu_scatter_us += 1e3 * ms[2];
+    tr->prof_acc.gpu_reduce_us += 1e3 * ms[3];
+    tr->prof_acc.gpu_adam_us += 1e3 * ms[4];
+    tr->prof_acc.gpu_total_us += 1e3 * (ms[0] + ms[1] + ms[2] + ms[3] + ms[4]);
     tr->prof_acc.steps += 1;
   }
   tr->prof_used = 0;
@@ -276,6 +288,15 @@ int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
   }
   if (wpb < 1) return fail(TMNN_ERR_UNSUPPORTED, "model does not fit in LDS");
   out.wpb = wpb;
+  out.f16 = f16;
+  out.train = train;
+  {
+    const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
+                                      tr->d.num_hidden_layers, tr->d.num_outputs,
+                                      static_cast<int>(tr->mlp_count), f16, train, 1);
+    out.image_bytes = static_cast<size_t>(s.dw_off);
+    TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
+  }
   TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                    out.lds));
@@ -301,17 +322,53 @@ FieldArgs base_args(const tmnn_trainer *tr) {
   a.huber_delta = baked6(tr->d.huber_delta);
   a.loss_scale = 1.0f;
   a.inv_loss_scale = 1.0f;
-  a.lift2d_mask = tr->d.spatial_dims == 2 ? 1 : 0;
   a.mlp_count = static_cast<int32_t>(tr->mlp_count);
   for (int l = 0; l < kMaxLevels; ++l) a.res[l] = tr->res[l];
   a.table = tr->params.as<float>();
   a.mlp = tr->params.as<float>() + tr->hash_count;
-  a.grad_hash = tr->grad_hash.as<int32_t>();
-  a.mask = tr->mask.as<uint8_t>();
   return a;
 }
 
-int launch_field(tmnn_trainer *tr, const KernelPlan &plan, FieldArgs a, int n) {
+// Rebuild a plan's packed LDS image if the weights changed since it was made.
+int ensure_image(tmnn_trainer *tr, KernelPlan &plan) {
+  if (plan.packed_version == tr->weights_version) return TMNN_OK;
+  PackArgs p{};
+  p.s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim, tr->d.num_hidden_layers,
+                    tr->d.num_outputs, static_cast<int>(tr->mlp_count), plan.f16, plan.train, 1);
+  p.f16 = plan.f16 ? 1 : 0;
+  p.L = tr->d.num_levels;
+  for (int l = 0; l < kMaxLevels; ++l) p.res[l] = tr->res[l];
+  p.mlp = tr->params.as<float>() + tr->hash_count;
+  p.image = static_cast<unsigned char *>(plan.image);
+  int n = 0, total = 0;
+  auto add = [&](int kind, int layer, int count) {
+    p.sec_kind[n] = kind;
+    p.sec_layer[n] = layer;
+    p.sec_start[n] = total;
+    total += count;
+    ++n;
+  };
+  const int NHL = tr->d.num_hidden_layers;
+  for (int k = 0; k <= NHL; ++k) {
+    const int kin = k == 0 ? tr->INP : tr->HP;
+    const int mout = k == NHL ? 16 : tr->HP;
+    add(kSecFwd, k, kin * mout);
+    if (plan.train) add(kSecBwd, k, kin * (plan.f16 ? round_up(mout, 32) : mout));
+    add(kSecBias, k, mout);
+  }
+  add(kSecRes, 0, kMaxLevels);
+  p.nsec = n;
+  p.sec_start[n] = total;
+  hipLaunchKernelGGL(pack_image_kernel, dim3((total + 255) / 256), dim3(256), 0, tr->ctx->stream, p);
+  TMNN_HIP_TRY(hipGetLastError());
+  plan.packed_version = tr->weights_version;
+  return TMNN_OK;
+}
+
+int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n) {
+  const int rc = ensure_image(tr, plan);
+  if (rc != TMNN_OK) return rc;
+  a.image = static_cast<const unsigned char *>(plan.image);
   a.n = n;
   a.n_tiles = (n + kTilePts - 1) / kTilePts;
   a.waves_per_block = plan.wpb;
@@ -347,6 +404,7 @@ int ensure_batch(tmnn_trainer *tr, int n) {
   size_t tmp = 0;
   TMNN_HIP_TRY(morton_sort_temp_bytes(n, &tmp));
   TMNN_HIP_TRY(tr->sort_tmp.ensure(std::max<size_t>(tmp, 256)));
+  TMNN_HIP_TRY(tr->dx.ensure(static_cast<size_t>(n) * tr->IN * sizeof(float)));
   return TMNN_OK;
 }
 
@@ -383,6 +441,35 @@ int sort_batch(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
   return TMNN_OK;
 }
 
+// Hash-grid backward of the dx the train kernel left in tr->dx for the n
+// points at pos (same order): table gradients + visit flags.
+int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
+  ScatterArgs s{};
+  s.n = n;
+  s.IN = tr->IN;
+  s.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
+  for (int l = 0; l < kMaxLevels; ++l) s.res[l] = tr->res[l];
+  s.pos = pos;
+  s.dx = tr->dx.as<float>();
+  s.grad_hash = tr->grad_hash.as<int32_t>();
+  s.mask = tr->mask[tr->mask_cur].as<uint8_t>();
+  const dim3 grid((n + kScatterThreads - 1) / kScatterThreads, tr->d.num_levels);
+  hipStream_t st = tr->ctx->stream;
+  switch (tr->d.spatial_dims * 8 + tr->d.features_per_level) {
+    case 2 * 8 + 1: hipLaunchKernelGGL((hash_scatter_kernel<2, 1>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 2 * 8 + 2: hipLaunchKernelGGL((hash_scatter_kernel<2, 2>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 2 * 8 + 4: hipLaunchKernelGGL((hash_scatter_kernel<2, 4>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 3 * 8 + 1: hipLaunchKernelGGL((hash_scatter_kernel<3, 1>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 3 * 8 + 2: hipLaunchKernelGGL((hash_scatter_kernel<3, 2>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 3 * 8 + 4: hipLaunchKernelGGL((hash_scatter_kernel<3, 4>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 4 * 8 + 1: hipLaunchKernelGGL((hash_scatter_kernel<4, 1>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 4 * 8 + 2: hipLaunchKernelGGL((hash_scatter_kernel<4, 2>), grid, dim3(kScatterThreads), 0, st, s); break;
+    default: hipLaunchKernelGGL((hash_scatter_kernel<4, 4>), grid, dim3(kScatterThreads), 0, st, s); break;
+  }
+  TMNN_HIP_TRY(hipGetLastError());
+  return TMNN_OK;
+}
+
 // Fused forward/backward over n device-resident points, gradients
 // accumulated into grad_hash / grad_mlp / mask. Returns the block count used
 // (for the loss reduction) or a negative status.
@@ -405,9 +492,12 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   a.target = tgt;
   a.grad_partials = tr->partials.as<float>();
   a.loss_partials = tr->loss_partials.as<float>();
+  a.dx_out = tr->dx.as<float>();
   const int blocks = launch_field(tr, tr->train_plan, a, n);
   if (blocks < 0) return blocks;
   if ((rc = prof_mark(tr, 2)) != TMNN_OK) return rc;
+  if ((rc = launch_scatter(tr, pos, n)) != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + kReduceCols - 1) / kReduceCols),
                      dim3(kReduceCols * kReduceGroups), 0,
                      tr->ctx->stream, tr->partials.as<float>(), blocks,
@@ -425,7 +515,10 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
   a.grad_mlp = tr->grad_mlp.as<float>();
   // Sparse hash Adam needs l1_reg == 0 (default_trainer.cpp:1868-1876).
   a.lazy = (tr->d.hash_adam_mode == TMNN_HASH_ADAM_LAZY && tr->d.l1_reg == 0.0f) ? 1 : 0;
-  a.mask = tr->mask.as<uint8_t>();
+  a.mask = tr->mask[tr->mask_cur].as<uint8_t>();
+  a.mask_next = tr->mask[tr->mask_cur ^ 1].as<uint8_t>();
+  a.partner_xor = tr->d.spatial_dims == 2 ? (kPrimeZ & ((1u << tr->d.log2_hashmap_size) - 1u)) : 0u;
+  a.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
   a.hash_entries = tr->hash_entries;
   a.mlp_count = tr->mlp_count;
   a.lr_hash = tr->lr_enc;
@@ -452,6 +545,8 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
     default: hipLaunchKernelGGL(adam_kernel<4>, dim3(blocks), dim3(256), 0, tr->ctx->stream, a); break;
   }
   TMNN_HIP_TRY(hipGetLastError());
+  if (clear_mask) tr->mask_cur ^= 1;  // the zeroed buffer collects the next step
+  ++tr->weights_version;
   return TMNN_OK;
 }
 
@@ -476,9 +571,9 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
                      tr->loss_partials.as<float>(), blocks, n,
                      d_loss ? d_loss : tr->loss_out.as<float>());
   TMNN_HIP_TRY(hipGetLastError());
-  if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
-  if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
+  if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 5)) != TMNN_OK) return rc;
   if (tr->prof_cur >= 0) tr->prof_acc.batch_size = static_cast<uint32_t>(n);
   tr->prof_cur = -1;
   ++tr->step;
@@ -488,7 +583,8 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
 int zero_training_state(tmnn_trainer *tr) {
   int rc = zero_device(tr, tr->grad_hash.ptr, tr->hash_count * sizeof(int32_t));
   if (rc == TMNN_OK) rc = zero_device(tr, tr->grad_mlp.ptr, tr->mlp_count * sizeof(float));
-  if (rc == TMNN_OK) rc = zero_device(tr, tr->mask.ptr, tr->hash_entries);
+  if (rc == TMNN_OK) rc = zero_device(tr, tr->mask[0].ptr, tr->hash_entries);
+  if (rc == TMNN_OK) rc = zero_device(tr, tr->mask[1].ptr, tr->hash_entries);
   return rc;
 }
 
@@ -541,6 +637,7 @@ int init_weights(tmnn_trainer *tr) {
     ctr += static_cast<uint32_t>((s.bc + 3) / 4);
     dst += s.bc;
   }
+  ++tr->weights_version;
   return TMNN_OK;
 }
 
@@ -701,7 +798,8 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
   TMNN_HIP_TRY(tr->v.ensure(total * sizeof(float)));
   TMNN_HIP_TRY(tr->grad_hash.ensure(tr->hash_count * sizeof(int32_t)));
   TMNN_HIP_TRY(tr->grad_mlp.ensure(tr->mlp_count * sizeof(float)));
-  TMNN_HIP_TRY(tr->mask.ensure(tr->hash_entries));
+  TMNN_HIP_TRY(tr->mask[0].ensure(tr->hash_entries));
+  TMNN_HIP_TRY(tr->mask[1].ensure(tr->hash_entries));
   TMNN_HIP_TRY(tr->partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
                                    tr->mlp_count * sizeof(float)));
   TMNN_HIP_TRY(tr->loss_partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
@@ -958,6 +1056,7 @@ int tmnn_set_initial_weights(tmnn_trainer *tr, const float *hash, size_t hash_co
   if (mlp && mlp_count)
     TMNN_HIP_TRY(hipMemcpyAsync(tr->params.as<float>() + tr->hash_count, mlp,
                                 mlp_count * sizeof(float), hipMemcpyHostToDevice, st));
+  ++tr->weights_version;
   int rc = reset_moments(tr);
   if (rc != TMNN_OK) return rc;
   rc = zero_training_state(tr);
@@ -1137,6 +1236,10 @@ int tmnn_debug_get_gradients(tmnn_trainer *tr, int32_t *grad_hash, size_t hash_c
     TMNN_HIP_TRY(hipMemcpyAsync(grad_mlp, tr->grad_mlp.ptr, mlp_count * sizeof(float),
                                 hipMemcpyDeviceToHost, st));
   TMNN_HIP_TRY(hipStreamSynchronize(st));
+  // F == 2 entries hold one packed 64-bit sum; restore feature 1
+  if (grad_hash && tr->d.features_per_level == 2)
+    for (size_t e = 0; e + 1 < hash_count; e += 2)
+      grad_hash[e + 1] = unpack_hi(grad_hash[e], grad_hash[e + 1]);
   return TMNN_OK;
 }
 
@@ -1145,16 +1248,20 @@ int tmnn_debug_get_active_mask(tmnn_trainer *tr, uint32_t *words, size_t word_co
   if (word_count != tr->mask_words) return fail(TMNN_ERR_INVALID_ARGUMENT, "word count mismatch");
   TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
   std::vector<uint8_t> flags(tr->hash_entries);
-  TMNN_HIP_TRY(hipMemcpyAsync(flags.data(), tr->mask.ptr, flags.size(), hipMemcpyDeviceToHost,
-                              tr->ctx->stream));
+  TMNN_HIP_TRY(hipMemcpyAsync(flags.data(), tr->mask[tr->mask_cur].ptr, flags.size(),
+                              hipMemcpyDeviceToHost, tr->ctx->stream));
   TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
   // Reference layout (mlp_kernel_emitter.cpp:48-71): bit per entry (F == 2),
-  // else bit per float, all F floats of a visited entry set.
+  // else bit per float, all F floats of a visited entry set; lifted 2D points
+  // also set their z = 1 corners, the partners of the flagged z = 0 entries.
   std::memset(words, 0, word_count * sizeof(uint32_t));
   const uint32_t F = static_cast<uint32_t>(tr->d.features_per_level);
   const uint32_t per = F == 2 ? 1u : F;
+  const uint32_t tmask = (1u << tr->d.log2_hashmap_size) - 1u;
+  const uint32_t pxor = tr->d.spatial_dims == 2 ? (kPrimeZ & tmask) : 0u;
   for (uint32_t e = 0; e < tr->hash_entries; ++e) {
-    if (!flags[e]) continue;
+    const bool z1 = pxor != 0 && flags[(e & ~tmask) | ((e & tmask) ^ pxor)];
+    if (!flags[e] && !z1) continue;
     for (uint32_t f = 0; f < per; ++f) {
       const uint32_t bit = e * per + f;
       words[bit >> 5] |= 1u << (bit & 31u);

@@ -89,6 +89,7 @@ class StepProfile(ctypes.Structure):
         ("batch_size", ctypes.c_uint32),
         ("gpu_sort_us", ctypes.c_double),
         ("gpu_fwd_bwd_us", ctypes.c_double),
+        ("gpu_scatter_us", ctypes.c_double),
         ("gpu_reduce_us", ctypes.c_double),
         ("gpu_adam_us", ctypes.c_double),
         ("gpu_total_us", ctypes.c_double),
