@@ -167,6 +167,13 @@ int tmnn_inference(tmnn_trainer *tr, const float *positions, float *output,
 int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions,
                           float *d_output, int32_t n);
 
+/* FieldEvaluator::evaluate_with_gradient (evaluator.h:41-50;
+ * default_trainer.cpp:467-620): outputs [N][num_outputs] and the Jacobian
+ * gradients [N][num_outputs][spatial_dims] (d output / d position, row-major,
+ * evaluator.h:10-12), fp32, unsorted, no batch cap. Host memory. */
+int tmnn_evaluate_with_gradient(tmnn_trainer *tr, const float *positions,
+                                float *output, float *gradients, int32_t n);
+
 /* ITrainerRuntime::forward_for_training (trainer.h:145-150;
  * default_trainer.cpp:1047-1127): forward in the training precision, output
  * in the caller's point order. *written = min(N, batch_size) * num_outputs. */

@@ -385,6 +385,59 @@ void backward_point(const Geo &g, const Offsets &o, const float *res,
   for (int j = 0; j < g.H; ++j) gW[o.b[0] + j] += static_cast<double>(d0[j]);
 }
 
+// d(feature f of level l)/d(cell fraction) at one point: the 3D lerp form of
+// trilinear_feature_grad (mlp_kernel_emitter.cpp:1677-1704; lifted 2D points
+// use it with fz = 0) and the 4D loops of the gradient kernel (:2034-2056).
+void level_frac_grad(const Geo &g, const float *table, const Level &lv, int l, int f,
+                     float *dv) {
+  const size_t base = static_cast<size_t>(l) * g.T * g.F;
+  auto at = [&](int dx, int dy, int dz, int dw) {
+    int c[4] = {lv.bc[0] + dx, lv.bc[1] + dy, lv.bc[2] + dz, lv.bc[3] + dw};
+    return table[base + static_cast<size_t>(hash_idx(c, g.D, g.T)) * g.F + f];
+  };
+  const float fx = lv.fr[0], fy = lv.fr[1], fz = lv.fr[2], fw = lv.fr[3];
+  if (g.D == 3) {
+    const float c000 = at(0, 0, 0, 0), c001 = at(0, 0, 1, 0), c010 = at(0, 1, 0, 0),
+                c011 = at(0, 1, 1, 0), c100 = at(1, 0, 0, 0), c101 = at(1, 0, 1, 0),
+                c110 = at(1, 1, 0, 0), c111 = at(1, 1, 1, 0);
+    dv[0] = (1.0f - fz) * ((1.0f - fy) * (c100 - c000) + fy * (c110 - c010)) +
+            fz * ((1.0f - fy) * (c101 - c001) + fy * (c111 - c011));
+    dv[1] = (1.0f - fz) * ((1.0f - fx) * (c010 - c000) + fx * (c110 - c100)) +
+            fz * ((1.0f - fx) * (c011 - c001) + fx * (c111 - c101));
+    dv[2] = (1.0f - fy) * ((1.0f - fx) * (c001 - c000) + fx * (c101 - c100)) +
+            fy * ((1.0f - fx) * (c011 - c010) + fx * (c111 - c110));
+    dv[3] = 0.0f;
+    return;
+  }
+  float c[2][2][2][2];
+  for (int dw = 0; dw < 2; ++dw)
+    for (int dz = 0; dz < 2; ++dz)
+      for (int dy = 0; dy < 2; ++dy)
+        for (int dx = 0; dx < 2; ++dx) c[dw][dz][dy][dx] = at(dx, dy, dz, dw);
+  auto w = [](int d, float fr) { return d == 0 ? (1.0f - fr) : fr; };
+  float gx = 0.0f, gy = 0.0f, gz = 0.0f, gt = 0.0f;
+  for (int dw = 0; dw < 2; ++dw)
+    for (int dz = 0; dz < 2; ++dz)
+      for (int dy = 0; dy < 2; ++dy)
+        gx += w(dy, fy) * w(dz, fz) * w(dw, fw) * (c[dw][dz][dy][1] - c[dw][dz][dy][0]);
+  for (int dw = 0; dw < 2; ++dw)
+    for (int dz = 0; dz < 2; ++dz)
+      for (int dx = 0; dx < 2; ++dx)
+        gy += w(dx, fx) * w(dz, fz) * w(dw, fw) * (c[dw][dz][1][dx] - c[dw][dz][0][dx]);
+  for (int dw = 0; dw < 2; ++dw)
+    for (int dy = 0; dy < 2; ++dy)
+      for (int dx = 0; dx < 2; ++dx)
+        gz += w(dx, fx) * w(dy, fy) * w(dw, fw) * (c[dw][1][dy][dx] - c[dw][0][dy][dx]);
+  for (int dz = 0; dz < 2; ++dz)
+    for (int dy = 0; dy < 2; ++dy)
+      for (int dx = 0; dx < 2; ++dx)
+        gt += w(dx, fx) * w(dy, fy) * w(dz, fz) * (c[1][dz][dy][dx] - c[0][dz][dy][dx]);
+  dv[0] = gx;
+  dv[1] = gy;
+  dv[2] = gz;
+  dv[3] = gt;
+}
+
 // Philox-4x32-10 (metal_context.cpp:735-752; Salmon et al., SC'11).
 inline void philox(uint32_t ctr_in, uint32_t k0, uint32_t k1, uint32_t out[4]) {
   uint32_t c0 = ctr_in, c1 = 0, c2 = 0, c3 = 0;
@@ -685,6 +738,59 @@ float orc_training_step(const orc_model *m, const orc_adam *a,
   orc_adam_step(m, a, logical_step, params, mom1, mom2, gh.data(), gmf.data(),
                 dense ? nullptr : mask.data(), n_threads);
   return n > 0 ? static_cast<float>(loss / static_cast<double>(n)) : 0.0f;
+}
+
+// FieldEvaluator::evaluate_with_gradient (neural_sdf_analytical_eval_gradient_
+// points, mlp_kernel_emitter.cpp:1865-2090; host default_trainer.cpp:467-620):
+// out[N][M] as orc_forward, grads[N][M][D] = d out_m / d pos. Per output m
+// the backward starts from d out_m = 1: g_last[j] = WO[j][m] * [h_last > 0],
+// g_prev[i] = (sum_j g[j] * W[i][j]) * [h_prev > 0] (:1966-1990); then
+// grad_feat = sum_j g0[j] * W0[feat][j] and grad_pos += (grad_feat * r_l) *
+// d(feat)/d(frac) over levels and features (:1995-2060). 2D points are the
+// lifted (x, y, 0); their z component is dropped.
+void orc_evaluate_with_gradient(const orc_model *m, const float *table, const float *mlp,
+                                const float *pos, int32_t n, float *out, float *grads) {
+  const Geo g = geo_of(m);
+  const Offsets o = offsets_of(g);
+  std::vector<float> res(g.L);
+  resolutions(m, res.data());
+#pragma omp parallel for schedule(static)
+  for (int32_t i = 0; i < n; ++i) {
+    const float *p = pos + static_cast<size_t>(i) * g.in_D;
+    std::vector<float> acts(static_cast<size_t>(g.NHL) * g.H);
+    forward_point(g, o, res.data(), table, mlp, p, acts.data(),
+                  out + static_cast<size_t>(i) * g.M);
+    std::vector<float> cur(g.H), nxt(g.H);
+    for (int mm = 0; mm < g.M; ++mm) {
+      const float *last = acts.data() + (g.NHL - 1) * g.H;
+      for (int j = 0; j < g.H; ++j)
+        cur[j] = mlp[o.w[g.NHL] + j * g.M + mm] * (last[j] > 0.0f ? 1.0f : 0.0f);
+      for (int k = g.NHL - 1; k >= 1; --k) {
+        const float *hp = acts.data() + (k - 1) * g.H;
+        for (int ii = 0; ii < g.H; ++ii) {
+          float acc = 0.0f;
+          for (int j = 0; j < g.H; ++j) acc = acc + cur[j] * mlp[o.w[k] + ii * g.H + j];
+          nxt[ii] = acc * (hp[ii] > 0.0f ? 1.0f : 0.0f);
+        }
+        std::swap(cur, nxt);
+      }
+      float gp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int l = 0; l < g.L; ++l) {
+        const Level lv = level_of(g, p, res[l]);
+        for (int f = 0; f < g.F; ++f) {
+          const int row = o.w[0] + (l * g.F + f) * g.H;
+          float gf = 0.0f;
+          for (int j = 0; j < g.H; ++j) gf = gf + cur[j] * mlp[row + j];
+          float dv[4];
+          level_frac_grad(g, table, lv, l, f, dv);
+          const float s = gf * res[l];
+          for (int a = 0; a < g.D; ++a) gp[a] = gp[a] + s * dv[a];
+        }
+      }
+      for (int a = 0; a < g.in_D; ++a)
+        grads[(static_cast<size_t>(i) * g.M + mm) * g.in_D + a] = gp[a];
+    }
+  }
 }
 
 }  // extern "C"

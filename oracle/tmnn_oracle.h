@@ -110,6 +110,12 @@ void orc_adam_step(const orc_model *m, const orc_adam *a, uint32_t logical_step,
 /* Morton code of one point set: codes[N]. dims 2 is lifted to (x, y, 0). */
 void orc_morton_codes(const float *pos, int32_t n, int32_t dims, uint32_t *codes);
 
+/* FieldEvaluator::evaluate_with_gradient: out [N][num_outputs] and the
+ * Jacobian grads [N][num_outputs][spatial_dims] (d out / d position). */
+void orc_evaluate_with_gradient(const orc_model *m, const float *table,
+                                const float *mlp, const float *pos, int32_t n,
+                                float *out, float *grads);
+
 /* One full reference training step: forward/backward with internal loss,
  * lazy hash Adam + dense MLP Adam (dense hash when dense_hash != 0 or
  * l1_reg != 0), grads and mask consumed. Returns the reported loss

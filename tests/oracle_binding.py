@@ -71,6 +71,7 @@ class Oracle:
             "orc_adam_step": (None, [M, A, ctypes.c_uint32, _V, _V, _V, _V, _V, _V,
                                      ctypes.c_int32]),
             "orc_morton_codes": (None, [_V, ctypes.c_int32, ctypes.c_int32, _V]),
+            "orc_evaluate_with_gradient": (None, [M, _V, _V, _V, ctypes.c_int32, _V, _V]),
             "orc_training_step": (ctypes.c_float, [M, A, ctypes.c_uint32, _V, _V, _V, _V, _V,
                                                    ctypes.c_int32, ctypes.c_int32,
                                                    ctypes.c_int32]),
@@ -135,6 +136,16 @@ class Oracle:
         out = np.empty((pos.shape[0], m.num_outputs), np.float32)
         self.lib.orc_forward(m, _p(table), _p(mlp), _p(pos), pos.shape[0], _p(out))
         return out
+
+    def evaluate_with_gradient(self, m, table, mlp, pos):
+        """(out [N][M], Jacobian [N][M][D]) of the evaluator's gradient kernel."""
+        pos = np.ascontiguousarray(pos, np.float32)
+        n = pos.shape[0]
+        out = np.empty((n, m.num_outputs), np.float32)
+        grads = np.empty((n, m.num_outputs, m.spatial_dims), np.float32)
+        self.lib.orc_evaluate_with_gradient(m, _p(table), _p(mlp), _p(pos), n, _p(out),
+                                            _p(grads))
+        return out, grads
 
     def forward_backward(self, m, table, mlp, pos, target=None, d_out=None, threads=8):
         """Returns (grad_hash int32, grad_mlp float64, mask uint32, loss_sum, outputs)."""

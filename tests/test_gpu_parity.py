@@ -366,3 +366,26 @@ def test_morton_sort_matches_oracle_codes_and_stable_order(oracle, d, n):
         want = _compact_2d(want)
     assert np.array_equal(codes, want)
     assert np.array_equal(perm, np.argsort(want, kind="stable").astype(np.uint32))
+
+
+# ------------------------------------------------- evaluate_with_gradient --
+
+@pytest.mark.parametrize("name", list(GEOMS))
+def test_evaluate_with_gradient_matches_oracle(oracle, name):
+    """FieldEvaluator::evaluate_with_gradient: outputs and the position
+    Jacobian [N][M][D] against the oracle's restatement of the reference's
+    analytic gradient kernel (fp32, same tolerance as outputs)."""
+    _say(f"evaluate_with_gradient {name}")
+    d, enc, net, m_out = GEOMS[name]
+    rng = np.random.default_rng(31)
+    with make_trainer(d, m_out, enc, net, hash_range=0.5, precision="fp16") as tr:
+        hw, mw = tr.get_weights()
+        pos = rng.random((777, d), dtype=np.float32)
+        out, jac = tr.evaluate_with_gradient(pos)
+        oout, ojac = oracle.evaluate_with_gradient(omodel(oracle, tr), hw, mw, pos)
+        assert jac.shape == (777, m_out, d)
+        for got, ref in ((out, oout), (jac, ojac)):
+            tol = 1e-5 * (np.abs(ref) + np.sqrt((ref.astype(np.float64) ** 2).mean()))
+            assert np.all(np.abs(got - ref) <= tol), float(np.abs(got - ref).max())
+        e_out, e_jac = tr.evaluate_with_gradient(np.zeros((0, d), np.float32))
+        assert e_out.shape == (0, m_out) and e_jac.shape == (0, m_out, d)

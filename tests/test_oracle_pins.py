@@ -387,3 +387,39 @@ def test_training_step_reports_sum_over_outputs_over_n(oracle):
     tgt = np.zeros((100, 3), np.float32)
     loss = oracle.training_step(m, oracle.adam(), 0, params, m1, m2, pos, tgt)
     assert loss == pytest.approx(0.25 + 0.0625 + 0.25, rel=1e-6)
+
+
+@pytest.mark.parametrize("d,f,nhl,m_out", [(3, 2, 2, 1), (2, 2, 1, 3), (4, 2, 1, 2), (3, 4, 1, 1),
+                                           (3, 1, 2, 2)])
+def test_position_gradient_matches_finite_differences(oracle, d, f, nhl, m_out):
+    """evaluate_with_gradient (mlp_kernel_emitter.cpp:1865-2090): the analytic
+    Jacobian equals central differences of the oracle's own forward, and its
+    output equals orc_forward exactly. Points are kept away from cell faces so
+    the +-eps steps stay in one cell at every level (ReLU kinks may still lie
+    inside a step)."""
+    m = oracle.model(d, 4, f, 12, 4.0, 2.0, 16, nhl, m_out, "L2")
+    h, w = oracle.init_params(m, 5, 0.5)
+    rng = np.random.default_rng(d * 10 + f)
+    res = oracle.resolutions(m).astype(np.float64)
+    pts = []
+    while len(pts) < 24:
+        p = rng.random(d) * 0.8 + 0.1
+        fr = (p[None, :] * res[:, None]) % 1.0
+        if np.all((fr > 0.05) & (fr < 0.95)):
+            pts.append(p)
+    pos = np.array(pts, np.float32)
+    out, jac = oracle.evaluate_with_gradient(m, h, w, pos)
+    assert np.array_equal(out, oracle.forward(m, h, w, pos))
+    eps = 1e-4
+    for a in range(d):
+        pp, pm = pos.astype(np.float64).copy(), pos.astype(np.float64).copy()
+        pp[:, a] += eps
+        pm[:, a] -= eps
+        fd = (oracle.forward(m, h, w, pp.astype(np.float32)).astype(np.float64)
+              - oracle.forward(m, h, w, pm.astype(np.float32)).astype(np.float64))
+        fd /= (pp[:, a].astype(np.float32).astype(np.float64)
+               - pm[:, a].astype(np.float32).astype(np.float64))[:, None]
+        # a ReLU kink inside +-eps spoils the difference at a few points;
+        # a wrong term or sign would spoil nearly all of them
+        err = np.abs(jac[:, :, a] - fd) / np.abs(jac).max()
+        assert (err <= 2e-3).mean() >= 0.85, (a, np.sort(err.ravel())[-5:])

@@ -29,7 +29,9 @@
 
 namespace tmnn_hip {
 
-enum : int32_t { kModeForward = 0, kModeTrainLoss = 1, kModeTrainExtGrad = 2 };
+// kModeInputGrad: forward + backward from d out_m = 1 for output grad_output,
+// storing only dx (the evaluator's position gradient); no weight gradients.
+enum : int32_t { kModeForward = 0, kModeTrainLoss = 1, kModeTrainExtGrad = 2, kModeInputGrad = 3 };
 enum : int32_t {
   kLossL2 = 0,
   kLossL1 = 1,
@@ -51,6 +53,7 @@ struct FieldArgs {
   int32_t n_tiles;          // ceil(n / kTilePts)
   int32_t waves_per_block;
   int32_t mode;             // kMode*
+  int32_t grad_output;      // kModeInputGrad: the output row of the Jacobian
   int32_t loss_kind;        // kLoss*
   float huber_delta;
   float inv_n;              // fl(1/N) of the loss (emitScalarTrainKernelImpl)
@@ -941,7 +944,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int o = 4 * q + r;
-        Tv[nt][r] = (TRAIN && valid[nt] && o < a.M)
+        Tv[nt][r] = (TRAIN && a.mode != kModeInputGrad && valid[nt] && o < a.M)
                         ? a.target[static_cast<size_t>(pt[nt]) * a.M + o] : 0.0f;
       }
     if constexpr (TRAIN) store_tiles<F16, KT0>(Xs, X, p, q);
@@ -1012,7 +1015,20 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       for (int t = 0; t < OKT; ++t)
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt) g[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (a.mode == kModeTrainExtGrad) {
+      const bool wgrads = a.mode != kModeInputGrad;  // accumulate dW / loss
+      if (!wgrads) {
+        // evaluator gradient pass: outputs once, then d out_m = 1
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+          if (!valid[nt]) continue;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 4 * q + r;
+            if (a.out && o < a.M) a.out[static_cast<size_t>(pt[nt]) * a.M + o] = y[0][nt][r];
+            if (o == a.grad_output) g[0][nt][r] = 1.0f;
+          }
+        }
+      } else if (a.mode == kModeTrainExtGrad) {
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
@@ -1087,7 +1103,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       const int last = NHL - 1;
       {
         const unsigned char *Hl = Hs + last * hs_layer_bytes;
-        if constexpr (REGDW) {
+        if (!wgrads) {
+        } else if constexpr (REGDW) {
 #pragma unroll
           for (int ut = 0; ut < HT; ++ut) R.wo[ut] = dw_tile<F16>(Ds, 0, Hl, 16 * ut, p, q, R.wo[ut]);
 #pragma unroll
@@ -1129,7 +1146,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         store_tiles<F16, HT>(Ds, dl, p, q);
         wave_lds_sync();
         const unsigned char *Hin = Hs + (k - 1) * hs_layer_bytes;
-        if constexpr (REGDW) {
+        if (!wgrads) {
+        } else if constexpr (REGDW) {
 #pragma unroll
           for (int mt = 0; mt < HT; ++mt) {
 #pragma unroll
@@ -1184,7 +1202,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       wave_lds_sync();
       store_tiles<F16, HT>(Ds, dl, p, q);
       wave_lds_sync();
-      if constexpr (REGDW) {
+      if (!wgrads) {
+      } else if constexpr (REGDW) {
 #pragma unroll
         for (int mt = 0; mt < HT; ++mt) {
 #pragma unroll
@@ -1246,6 +1265,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   }
 
   if constexpr (TRAIN) {
+    if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
     float v = lane_loss;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);

@@ -23,6 +23,7 @@
 #include "tmnn_hip.h"
 #include "aux_kernels.hpp"
 #include "field_kernel.hpp"
+#include "grad_kernel.hpp"
 #include "scatter_kernel.hpp"
 #include "sort.hpp"
 
@@ -169,6 +170,9 @@ struct tmnn_trainer {
   DevBuf dbg_a, dbg_b, dbg_c;
 
   KernelPlan train_plan, fwd_plan, infer_plan;
+  KernelPlan grad_plan;          // fp32 backward for evaluate_with_gradient (lazy)
+  bool grad_planned = false;
+  DevBuf grad_out;               // [n][M][D] Jacobian of evaluate_with_gradient
   uint64_t weights_version = 0;  // bumped whenever the parameters change
 
   // Step profiling: one set of phase events per profiled step, summed and
@@ -181,7 +185,7 @@ struct tmnn_trainer {
   tmnn_step_profile prof_acc{};
 
   ~tmnn_trainer() {
-    for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan})
+    for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan, &grad_plan})
       if (p->image) (void)hipFree(p->image);
     for (auto &set : prof_events)
       for (hipEvent_t e : set)
@@ -921,6 +925,73 @@ int tmnn_inference(tmnn_trainer *tr, const float *positions, float *output, int3
   const int rc = tmnn_inference_device(tr, tr->in_pos.as<float>(), tr->out_buf.as<float>(), n);
   if (rc != TMNN_OK) return rc;
   TMNN_HIP_TRY(hipMemcpyAsync(output, tr->out_buf.ptr, n * M * sizeof(float),
+                              hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+int tmnn_evaluate_with_gradient(tmnn_trainer *tr, const float *positions, float *output,
+                                float *gradients, int32_t n) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n < 0)
+    return fail(TMNN_ERR_INVALID_ARGUMENT,
+                "FieldEvaluator::evaluate_with_gradient: N must be non-negative");
+  if (n == 0) return TMNN_OK;
+  if (!positions || !output || !gradients)
+    return fail(TMNN_ERR_INVALID_ARGUMENT,
+                "positions, output, and gradients must be non-null when N > 0");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  int rc;
+  if (!tr->grad_planned) {  // the evaluator's gradient kernel is fp32 (default_trainer.cpp:497-507)
+    if ((rc = plan_kernel(tr, false, true, tr->grad_plan)) != TMNN_OK) return rc;
+    TMNN_HIP_TRY(tr->partials.ensure(static_cast<size_t>(tr->grad_plan.max_blocks) *
+                                     tr->mlp_count * sizeof(float)));
+    TMNN_HIP_TRY(tr->loss_partials.ensure(static_cast<size_t>(tr->grad_plan.max_blocks) *
+                                          sizeof(float)));
+    tr->grad_planned = true;
+  }
+  hipStream_t st = tr->ctx->stream;
+  const size_t D = tr->d.spatial_dims, M = tr->d.num_outputs;
+  if ((rc = ensure_batch(tr, n)) != TMNN_OK) return rc;
+  TMNN_HIP_TRY(tr->out_buf.ensure(n * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->grad_out.ensure(n * M * D * sizeof(float)));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, positions, n * D * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  PosGradArgs g{};
+  g.n = n;
+  g.L = tr->d.num_levels;
+  g.F = tr->d.features_per_level;
+  g.M = static_cast<int32_t>(M);
+  g.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
+  for (int l = 0; l < kMaxLevels; ++l) g.res[l] = tr->res[l];
+  g.pos = tr->in_pos.as<float>();
+  g.table = tr->params.as<float>();
+  g.dx = tr->dx.as<float>();
+  g.grads = tr->grad_out.as<float>();
+  for (int m = 0; m < static_cast<int>(M); ++m) {
+    // d out_m / d features for every point, then the position gradient
+    FieldArgs a = base_args(tr);
+    a.mode = kModeInputGrad;
+    a.grad_output = m;
+    a.pos = tr->in_pos.as<float>();
+    a.out = m == 0 ? tr->out_buf.as<float>() : nullptr;
+    a.dx_out = tr->dx.as<float>();
+    a.grad_partials = tr->partials.as<float>();
+    a.loss_partials = tr->loss_partials.as<float>();
+    const int blocks = launch_field(tr, tr->grad_plan, a, n);
+    if (blocks < 0) return blocks;
+    g.m = m;
+    const dim3 grid((n + 255) / 256);
+    switch (tr->d.spatial_dims) {
+      case 2: hipLaunchKernelGGL(pos_grad_kernel<2>, grid, dim3(256), 0, st, g); break;
+      case 3: hipLaunchKernelGGL(pos_grad_kernel<3>, grid, dim3(256), 0, st, g); break;
+      default: hipLaunchKernelGGL(pos_grad_kernel<4>, grid, dim3(256), 0, st, g); break;
+    }
+    TMNN_HIP_TRY(hipGetLastError());
+  }
+  TMNN_HIP_TRY(hipMemcpyAsync(output, tr->out_buf.ptr, n * M * sizeof(float),
+                              hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipMemcpyAsync(gradients, tr->grad_out.ptr, n * M * D * sizeof(float),
                               hipMemcpyDeviceToHost, st));
   TMNN_HIP_TRY(hipStreamSynchronize(st));
   return TMNN_OK;

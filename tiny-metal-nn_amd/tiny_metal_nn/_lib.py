@@ -120,6 +120,7 @@ SIGNATURES = {
     "tmnn_training_step_device": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
     "tmnn_inference": (ctypes.c_int, [_V, _V, _V, _I32]),
     "tmnn_inference_device": (ctypes.c_int, [_V, _V, _V, _I32]),
+    "tmnn_evaluate_with_gradient": (ctypes.c_int, [_V, _V, _V, _V, _I32]),
     "tmnn_forward_for_training": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(_U32)]),
     "tmnn_zero_gradients": (ctypes.c_int, [_V]),
     "tmnn_backward_accumulate": (ctypes.c_int, [_V, _V, _V, _I32]),

@@ -206,6 +206,18 @@ class Trainer:
 
     evaluate = inference
 
+    def evaluate_with_gradient(self, input) -> tuple[np.ndarray, np.ndarray]:
+        """(outputs (N, n_output), Jacobian (N, n_output, n_input)) in fp32."""
+        x = _as_f32_2d(input, "input", self.n_input)
+        n = x.shape[0]
+        out = np.empty((n, self.n_output), np.float32)
+        jac = np.empty((n, self.n_output, self.n_input), np.float32)
+        with self._enter("evaluate_with_gradient"):
+            if n:
+                _lib.check(self._lib.tmnn_evaluate_with_gradient(self._h, _ptr(x), _ptr(out),
+                                                                 _ptr(jac), n))
+        return out, jac
+
     def inference_device(self, input_ptr: int, output_ptr: int, n: int) -> None:
         self._check_open()
         _lib.check(self._lib.tmnn_inference_device(
