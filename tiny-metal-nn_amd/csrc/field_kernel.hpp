@@ -70,6 +70,8 @@ struct FieldArgs {
   float *out;               // [n][M] (Forward)
   const uint32_t *out_index;// nullable: row of out[] for point i
   float *dx_out;            // [n][IN] input-feature gradients (training)
+  uint64_t *wide_mask;      // wide kernel: ReLU bits of hidden layers [NHL-1][n_tiles][64 lanes]
+  _Float16 *wide_act;       // wide kernel: hidden activations [NHL-1][n_tiles][128][32] (fp16 training)
   float *grad_partials;     // [gridDim.x][mlp_count]
   float *loss_partials;     // [gridDim.x]
 };
@@ -744,6 +746,95 @@ __device__ __forceinline__ float elem_loss(int kind, float y, float t,
   }
 }
 
+// Loss term and output gradient of one wave tile (emitLoss,
+// mlp_kernel_emitter.cpp:562-670) in D layout: output 4*q + r of point
+// 16*nt + p. kModeInputGrad instead writes the outputs and seeds
+// d out_{grad_output} = 1; kModeTrainExtGrad takes d_out from Tv.
+template <int OKT>
+__device__ __forceinline__ void output_grad(const FieldArgs &a, const f32x4 (&y)[1][kNT],
+                                            const float (&Tv)[kNT][4], const bool (&valid)[kNT],
+                                            const int (&pt)[kNT], int q, float &lane_loss,
+                                            f32x4 (&g)[OKT][kNT]) {
+#pragma unroll
+  for (int t = 0; t < OKT; ++t)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) g[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (a.mode == kModeInputGrad) {
+    // evaluator gradient pass: outputs once, then d out_m = 1
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      if (!valid[nt]) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        if (a.out && o < a.M) a.out[static_cast<size_t>(pt[nt]) * a.M + o] = y[0][nt][r];
+        if (o == a.grad_output) g[0][nt][r] = 1.0f;
+      }
+    }
+  } else if (a.mode == kModeTrainExtGrad) {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        if (valid[nt] && o < a.M) g[0][nt][r] = Tv[nt][r] * a.loss_scale;
+      }
+  } else if (a.loss_kind == kLossCosine) {
+    // emitLoss cosine branch (mlp_kernel_emitter.cpp:643-662)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      float tv[4];
+      float dot = 0.0f, pn = 0.0f, tn = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        const bool ok = valid[nt] && o < a.M;
+        tv[r] = ok ? Tv[nt][r] : 0.0f;
+        const float yv = ok ? y[0][nt][r] : 0.0f;
+        dot = dot + yv * tv[r];
+        pn = pn + yv * yv;
+        tn = tn + tv[r] * tv[r];
+      }
+      dot += __shfl_xor(dot, 16);
+      dot += __shfl_xor(dot, 32);
+      pn += __shfl_xor(pn, 16);
+      pn += __shfl_xor(pn, 32);
+      tn += __shfl_xor(tn, 16);
+      tn += __shfl_xor(tn, 32);
+      const float pnorm = sqrtf(pn + 1e-8f);
+      const float tnorm = sqrtf(tn + 1e-8f);
+      const float denom = pnorm * tnorm;
+      const float cosine = dot / denom;
+      const float pdenom = pn + 1e-8f;
+      if (valid[nt]) {
+        if (q == 0) lane_loss += 1.0f - cosine;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 4 * q + r;
+          if (o < a.M) {
+            const float t1 = (cosine * y[0][nt][r]) / pdenom;
+            const float t2 = tv[r] / denom;
+            g[0][nt][r] = ((t1 - t2) * a.inv_n) * a.loss_scale;
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        if (valid[nt] && o < a.M) {
+          float d;
+          lane_loss += elem_loss(a.loss_kind, y[0][nt][r], Tv[nt][r], a.huber_delta,
+                                 a.inv_n, &d);
+          g[0][nt][r] = d * a.loss_scale;
+        }
+      }
+  }
+}
+
 // ---------------------------------------------------------------- kernel ----
 
 // Compile-time layer index for the unrolled backward (value > 0) and the
@@ -1009,87 +1100,10 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       }
       continue;
     } else {
-      // ---- loss / output gradient (D layout: output 4*q + r of point 16*nt + p)
-      f32x4 g[OKT][kNT];
-#pragma unroll
-      for (int t = 0; t < OKT; ++t)
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) g[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // ---- loss / output gradient
       const bool wgrads = a.mode != kModeInputGrad;  // accumulate dW / loss
-      if (!wgrads) {
-        // evaluator gradient pass: outputs once, then d out_m = 1
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-          if (!valid[nt]) continue;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 4 * q + r;
-            if (a.out && o < a.M) a.out[static_cast<size_t>(pt[nt]) * a.M + o] = y[0][nt][r];
-            if (o == a.grad_output) g[0][nt][r] = 1.0f;
-          }
-        }
-      } else if (a.mode == kModeTrainExtGrad) {
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 4 * q + r;
-            if (valid[nt] && o < a.M) g[0][nt][r] = Tv[nt][r] * a.loss_scale;
-          }
-      } else if (a.loss_kind == kLossCosine) {
-        // emitLoss cosine branch (mlp_kernel_emitter.cpp:643-662)
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-          float tv[4];
-          float dot = 0.0f, pn = 0.0f, tn = 0.0f;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 4 * q + r;
-            const bool ok = valid[nt] && o < a.M;
-            tv[r] = ok ? Tv[nt][r] : 0.0f;
-            const float yv = ok ? y[0][nt][r] : 0.0f;
-            dot = dot + yv * tv[r];
-            pn = pn + yv * yv;
-            tn = tn + tv[r] * tv[r];
-          }
-          dot += __shfl_xor(dot, 16);
-          dot += __shfl_xor(dot, 32);
-          pn += __shfl_xor(pn, 16);
-          pn += __shfl_xor(pn, 32);
-          tn += __shfl_xor(tn, 16);
-          tn += __shfl_xor(tn, 32);
-          const float pnorm = sqrtf(pn + 1e-8f);
-          const float tnorm = sqrtf(tn + 1e-8f);
-          const float denom = pnorm * tnorm;
-          const float cosine = dot / denom;
-          const float pdenom = pn + 1e-8f;
-          if (valid[nt]) {
-            if (q == 0) lane_loss += 1.0f - cosine;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int o = 4 * q + r;
-              if (o < a.M) {
-                const float t1 = (cosine * y[0][nt][r]) / pdenom;
-                const float t2 = tv[r] / denom;
-                g[0][nt][r] = ((t1 - t2) * a.inv_n) * a.loss_scale;
-              }
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 4 * q + r;
-            if (valid[nt] && o < a.M) {
-              float d;
-              lane_loss += elem_loss(a.loss_kind, y[0][nt][r], Tv[nt][r], a.huber_delta,
-                                     a.inv_n, &d);
-              g[0][nt][r] = d * a.loss_scale;
-            }
-          }
-      }
+      f32x4 g[OKT][kNT];
+      output_grad<OKT>(a, y, Tv, valid, pt, q, lane_loss, g);
 
       // ---- output layer backward
       wave_lds_sync();

@@ -26,6 +26,7 @@
 #include "grad_kernel.hpp"
 #include "scatter_kernel.hpp"
 #include "sort.hpp"
+#include "wide_kernel.hpp"
 
 using namespace tmnn_hip;
 
@@ -61,12 +62,30 @@ using FieldKernel = void (*)(FieldArgs);
 struct KernelChoice {
   FieldKernel fn = nullptr;
   bool reg_dw = false;  // dW accumulated in registers (compile-time layers)
+  bool wide = false;    // hidden width 128: the block-cooperative wide kernel
 };
+
+// Hidden width 128 (wide_kernel.hpp): instantiated for the BASELINE 4D shape
+// (16 levels x 2 features, 4 hidden layers) and a 3D two-layer shape.
+KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
+#define TMNN_WIDE(d, f, nhl)                                                         \
+  if (D == d && F == f && NHL == nhl) {                                              \
+    if (train) return {f16 ? wide_kernel<d, f, nhl, true, true>                      \
+                           : wide_kernel<d, f, nhl, false, true>, false, true};      \
+    return {f16 ? wide_kernel<d, f, nhl, true, false>                                \
+                : wide_kernel<d, f, nhl, false, false>, false, true};                \
+  }
+  TMNN_WIDE(4, 2, 4)
+  TMNN_WIDE(3, 2, 2)
+#undef TMNN_WIDE
+  return {};
+}
 
 // Geometry-specialised kernels (compile-time D, F and hidden-layer count;
 // dW in registers) for the BASELINE shapes, else the generic kernels
 // (runtime geometry, dW accumulated in LDS).
 KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL) {
+  if (HP == kWideHP) return INP == 32 ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
   const int DF = D * 8 + F;
 #define TMNN_SPEC(hp, inp, df, nhl)                                                  \
   if (HP == hp && INP == inp && DF == df && (!train || NHL == nhl)) {               \
@@ -137,6 +156,7 @@ struct KernelPlan {
   int lds = 0;          // dynamic LDS bytes
   bool dw_global = false;  // dW accumulator outside LDS
   bool reg_dw = false;     // dW accumulator in registers
+  bool wide = false;       // block-cooperative hidden-128 kernel (4 waves, 128-point block tiles)
   int max_blocks = 0;   // resident blocks on the whole device
 };
 
@@ -167,6 +187,7 @@ struct tmnn_trainer {
   DevBuf partials, loss_partials, loss_out;
   DevBuf in_pos, in_tgt, s_pos, s_tgt, keys0, keys1, vals0, vals1, sort_tmp, out_buf;
   DevBuf dx;  // [batch][IN] input-feature gradients between the two train kernels
+  DevBuf wide_mask, wide_act;  // hidden-128 kernel: per-tile ReLU bits and fp16 activations
   DevBuf dbg_a, dbg_b, dbg_c;
 
   KernelPlan train_plan, fwd_plan, infer_plan;
@@ -272,7 +293,28 @@ int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
                                         tr->d.features_per_level, tr->d.num_hidden_layers);
   out.fn = kc.fn;
   out.reg_dw = kc.reg_dw;
+  out.wide = kc.wide;
   if (!out.fn) return fail(TMNN_ERR_UNSUPPORTED, "no kernel for this geometry");
+  if (out.wide) {
+    const FieldLayout fl = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
+                                       tr->d.num_hidden_layers, tr->d.num_outputs,
+                                       static_cast<int>(tr->mlp_count), f16, train, 1);
+    const WideLayout wl = make_wide_layout(fl, f16, train);
+    out.wpb = kWideWaves;
+    out.lds = wl.total;
+    out.f16 = f16;
+    out.train = train;
+    out.image_bytes = static_cast<size_t>(fl.dw_off);
+    TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
+    TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, out.lds));
+    int per_cu = 0;
+    TMNN_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<const void *>(out.fn), 64 * kWideWaves, out.lds));
+    if (per_cu < 1) return fail(TMNN_ERR_UNSUPPORTED, "wide field kernel cannot be resident");
+    out.max_blocks = per_cu * tr->ctx->cu_count;
+    return TMNN_OK;
+  }
   // Most waves per block whose LDS plan fits; failing that, move the dW
   // accumulator out of LDS (global float atomics into the block's row).
   int wpb = 0;
@@ -377,6 +419,10 @@ int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n) {
   a.n_tiles = (n + kTilePts - 1) / kTilePts;
   a.waves_per_block = plan.wpb;
   a.dw_global = plan.dw_global ? 1 : 0;
+  if (plan.wide) {
+    a.wide_mask = tr->wide_mask.as<uint64_t>();
+    a.wide_act = tr->wide_act.as<_Float16>();
+  }
   const int need = (a.n_tiles + plan.wpb - 1) / plan.wpb;
   const int blocks = std::max(1, std::min(need, plan.max_blocks));
   hipLaunchKernelGGL(plan.fn, dim3(blocks), dim3(64 * plan.wpb), plan.lds,
@@ -409,6 +455,12 @@ int ensure_batch(tmnn_trainer *tr, int n) {
   TMNN_HIP_TRY(morton_sort_temp_bytes(n, &tmp));
   TMNN_HIP_TRY(tr->sort_tmp.ensure(std::max<size_t>(tmp, 256)));
   TMNN_HIP_TRY(tr->dx.ensure(static_cast<size_t>(n) * tr->IN * sizeof(float)));
+  if (tr->HP == kWideHP && tr->d.num_hidden_layers > 1) {
+    const size_t tiles = static_cast<size_t>((n + kTilePts - 1) / kTilePts);
+    const size_t layers = static_cast<size_t>(tr->d.num_hidden_layers - 1);
+    TMNN_HIP_TRY(tr->wide_mask.ensure(layers * tiles * 64 * sizeof(uint64_t)));
+    TMNN_HIP_TRY(tr->wide_act.ensure(layers * tiles * kWideHP * kTilePts * 2));
+  }
   return TMNN_OK;
 }
 
@@ -747,8 +799,14 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
     return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_model_desc.struct_size mismatch");
   std::string why;
   if (!desc_ok(desc, why)) return fail(TMNN_ERR_INVALID_ARGUMENT, "KernelSpec: " + why);
-  if (desc->hidden_dim > 64)
-    return fail(TMNN_ERR_UNSUPPORTED, "hidden_dim > 64 is not built in this library");
+  if (desc->hidden_dim > 128)
+    return fail(TMNN_ERR_UNSUPPORTED, "hidden_dim > 128 is not built in this library");
+  if (desc->hidden_dim > 64 && desc->num_levels * desc->features_per_level > 32)
+    return fail(TMNN_ERR_UNSUPPORTED,
+                "hidden_dim > 64 needs num_levels * features_per_level <= 32 in this library");
+  if (desc->hidden_dim > 64 && desc->precision != TMNN_PRECISION_FP16)
+    return fail(TMNN_ERR_UNSUPPORTED,
+                "hidden_dim > 64 trains with precision fp16 only in this library");
   if (desc->num_outputs > 16)
     return fail(TMNN_ERR_UNSUPPORTED, "num_outputs > 16 is not built in this library");
   const int IN = desc->num_levels * desc->features_per_level;
@@ -762,7 +820,7 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
   tr->d = *desc;
   tr->IN = IN;
   tr->INP = IN <= 32 ? 32 : 64;
-  tr->HP = desc->hidden_dim <= 32 ? 32 : 64;
+  tr->HP = desc->hidden_dim <= 32 ? 32 : (desc->hidden_dim <= 64 ? 64 : kWideHP);
   tr->lr_enc = desc->lr_encoding;
   tr->lr_net = desc->lr_network;
   tr->hash_count = static_cast<uint32_t>(desc->num_levels) *
