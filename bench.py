@@ -254,7 +254,7 @@ def main() -> int:
                 "kernel_avg_us": round(k_us, 2),
                 "alg_bytes_per_point": bpp}
     phases = {k: round(prof[k] / steps_prof, 2) for k in
-              ("gpu_sort_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",
+              ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",
                "gpu_adam_us", "gpu_total_us")}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)

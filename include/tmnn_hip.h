@@ -236,11 +236,12 @@ typedef struct tmnn_step_profile {
   uint32_t steps;             /* profiled steps summed below */
   uint32_t batch_size;        /* points of the last profiled step */
   double gpu_sort_us;         /* Morton codes + radix sort + gather */
-  double gpu_fwd_bwd_us;      /* the fused field kernel (encode..dx) */
+  double gpu_fwd_bwd_us;      /* the MLP kernel: forward, loss, backward to dx */
   double gpu_scatter_us;      /* hash-grid backward scatter + visit flags */
   double gpu_reduce_us;       /* dW partial reduction + loss reduction */
   double gpu_adam_us;         /* fused Adam pass (+ mask/grad clearing) */
   double gpu_total_us;        /* first event to last event, summed */
+  double gpu_encode_us;       /* hash-grid encode forward (features of the batch) */
 } tmnn_step_profile;
 
 int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled);

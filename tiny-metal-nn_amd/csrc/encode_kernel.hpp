@@ -1,0 +1,122 @@
+// encode_kernel.hpp -- hash-grid encode forward as its own kernel, writing the
+// input features of every point straight into the MFMA register layout the
+// MLP kernels consume.
+//
+// The encode is a gather problem: 2^D corners x L levels per point, each an
+// F-float load from a table that may not fit in L2. A launch of one thread
+// per point, few registers and many waves per SIMD keeps enough loads in
+// flight to run at the chip's gather rate; inside an MLP kernel (one wave per
+// SIMD, the register file taken by weight-gradient accumulators) the same
+// gathers are latency-bound. Each thread issues the loads of a group of
+// feature quads (<= 128 floats) before it interpolates any of them.
+//
+// Arithmetic: as encode_level (the reference's corner order z, y, x
+// ascending, weight ((wx * wy) * wz)(* wt), features summed from 0;
+// emitHashEncodeUnified, mlp_kernel_emitter.cpp:205-360) -- bit-identical
+// features.
+//
+// Layout of the feature buffer ("X tiles"): point i = 32 t + 16 nt + p and
+// feature f = 16 kt + 4 q + r sit at float offset
+//   ((((t * KT0 + kt) * kNT + nt) * 64 + p + 16 q) * 4 + r,
+// i.e. one f32x4 per lane of a wave tile, in the order the MLP kernels hold
+// X[kt][nt] in registers: a wave loads its tile with 16-byte coalesced loads.
+// Padding features (IN <= f < 16 KT0) and padding points (n <= i < 32 t_max)
+// are zero.
+#pragma once
+
+#include "device_common.hpp"
+
+namespace tmnn_hip {
+
+struct EncodeArgs {
+  int32_t n;       // points
+  int32_t n_pad;   // n rounded up to whole 32-point tiles
+  int32_t L;       // levels
+  int32_t KT0;     // input K tiles (16 features each)
+  uint32_t log2T;
+  float res[kMaxLevels];
+  const float *pos;    // [n][D]
+  const float *table;  // [L][T][F]
+  float *xfeat;        // X tiles, n_pad * 16 * KT0 floats
+};
+
+constexpr int kEncodeThreads = 256;
+
+// float offset of feature quad fq (features 4 fq .. 4 fq + 3) of point i
+__host__ __device__ inline size_t xtile_offset(int i, int fq, int KT0) {
+  const int t = i >> 5, nt = (i >> 4) & 1, p = i & 15;
+  const int kt = fq >> 2, q = fq & 3;
+  return ((((static_cast<size_t>(t) * KT0 + kt) * 2 + nt) * 64) + p + 16 * q) * 4;
+}
+
+template <int D, int F>
+__global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeArgs a) {
+  constexpr int C = 1 << D;        // corners per level
+  constexpr int LPQ = 4 / F;       // levels per feature quad
+  constexpr int QG = C >= 32 ? 1 : 32 / C;  // quads per group: QG * 4 * C floats in flight
+  const int i = blockIdx.x * kEncodeThreads + threadIdx.x;
+  if (i >= a.n_pad) return;
+  const bool valid = i < a.n;
+  float p[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = valid ? a.pos[static_cast<size_t>(i) * D + k] : 0.0f;
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  const int nquads = 4 * a.KT0;
+  for (int q0 = 0; q0 < nquads; q0 += QG) {
+    float v[QG][LPQ][C][F];
+#pragma unroll
+    for (int g = 0; g < QG; ++g)
+#pragma unroll
+      for (int lv = 0; lv < LPQ; ++lv) {
+        const int l = (q0 + g) * LPQ + lv;
+        const bool on = valid && q0 + g < nquads && l < a.L;
+        const Cell<D> c = cell_of<D>(p, a.res[on ? l : 0]);
+        const size_t lbase = static_cast<size_t>(on ? l : 0) << a.log2T;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          int co[D];
+          float wc[D];
+          corner_of<D>(c, k, co, wc);
+          const float *e = a.table + (lbase + hash_corner<D>(co, tmask)) * F;
+          if constexpr (F == 1) {
+            v[g][lv][k][0] = on ? e[0] : 0.0f;
+          } else if constexpr (F == 2) {
+            const f32x2 t = on ? *reinterpret_cast<const f32x2 *>(e) : f32x2{0.f, 0.f};
+            v[g][lv][k][0] = t[0];
+            v[g][lv][k][1] = t[1];
+          } else {
+            const f32x4 t = on ? *reinterpret_cast<const f32x4 *>(e) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int f = 0; f < 4; ++f) v[g][lv][k][f] = t[f];
+          }
+        }
+      }
+#pragma unroll
+    for (int g = 0; g < QG; ++g) {
+      if (q0 + g >= nquads) break;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int lv = 0; lv < LPQ; ++lv) {
+        const int l = (q0 + g) * LPQ + lv;
+        const Cell<D> c = cell_of<D>(p, a.res[l < a.L ? l : 0]);
+        float feat[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) feat[f] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          int co[D];
+          float wc[D];
+          corner_of<D>(c, k, co, wc);
+          const float w = corner_weight<D>(wc);
+#pragma unroll
+          for (int f = 0; f < F; ++f) feat[f] = feat[f] + w * v[g][lv][k][f];
+        }
+#pragma unroll
+        for (int f = 0; f < F; ++f) o[lv * F + f] = (valid && l < a.L) ? feat[f] : 0.0f;
+      }
+      *reinterpret_cast<f32x4 *>(a.xfeat + xtile_offset(i, q0 + g, a.KT0)) = o;
+    }
+  }
+}
+
+}  // namespace tmnn_hip

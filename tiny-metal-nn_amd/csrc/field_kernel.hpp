@@ -63,6 +63,7 @@ struct FieldArgs {
   int32_t mlp_count;
   float res[kMaxLevels];    // per-level resolution table
   const float *pos;         // [n][D]
+  const float *xfeat;       // input features as X tiles (encode_kernel.hpp), XMEM kernels
   const float *target;      // [n][M] target (TrainLoss) or d_out (TrainExtGrad)
   const float *table;       // [L][T][F] fp32
   const float *mlp;         // fp32 master MLP params (reference layout)
@@ -934,8 +935,9 @@ __device__ __forceinline__ void dw_regs_to_lds(const DwRegs<HT, KT0, NHLT> &R, c
 // input width INP (MFMA tiles), fp16 (split-fp16 forward, fp16 backward) or
 // fp32 MFMA, training or forward only, DF = D * 8 + F (0: runtime geometry),
 // NHLT = hidden-layer count (0: runtime count, dW accumulated in LDS;
-// > 0: dW accumulated in registers across tiles).
-template <int HP, int INP, bool F16, bool TRAIN, int DF, int NHLT>
+// > 0: dW accumulated in registers across tiles), XMEM: input features read
+// from a.xfeat (written by encode_features_kernel) instead of encoded here.
+template <int HP, int INP, bool F16, bool TRAIN, int DF, int NHLT, bool XMEM = false>
 __device__ __forceinline__ void field_body(const FieldArgs &a) {
   constexpr int HT = HP / 16;
   constexpr int KT0 = INP / 16;
@@ -1003,12 +1005,28 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   // fit in registers (<= 128 floats per lane; e.g. not for 3D x 4 features).
   constexpr bool kPipe =
       DF != 0 && kNT * KT0 * (DF ? (4 / (DF % 8)) * (1 << (DF / 8)) * (DF % 8) : 0) <= 128;
+  // X tile of wave tile t: one 16-byte load per (kt, nt), zero past the batch
+  const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
+  auto load_x = [&](int t, f32x4 (&Xt)[KT0][kNT]) {
+#pragma unroll
+    for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+        Xt[kt][nt] = t < a.n_tiles
+                         ? xt[((static_cast<size_t>(t) * KT0 + kt) * kNT + nt) * 64 + lane]
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
   const int tile_stride = gridDim.x * a.waves_per_block;
   int tile = blockIdx.x * a.waves_per_block + wave;
   float P[kNT][4];
-  load_pos(tile, P);
   Gathered<(DF ? DF / 8 : 2), (DF ? DF % 8 : 2), KT0> G;
-  if constexpr (kPipe) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, P, G);
+  f32x4 Xn[KT0][kNT];  // XMEM: features of the next tile, in flight
+  if constexpr (XMEM) {
+    if constexpr (KT0 <= 2) load_x(tile, Xn);
+  } else {
+    load_pos(tile, P);
+    if constexpr (kPipe) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, P, G);
+  }
 
   for (; tile < a.n_tiles; tile += tile_stride) {
     const int next = tile + tile_stride;
@@ -1022,13 +1040,24 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 
     // ---- encode: input features 16*kt + 4*q + r of point 16*nt + p
     f32x4 X[KT0][kNT];
-    if constexpr (kPipe)
-      gather_finish<DF / 8, DF % 8, KT0>(a, res, q, P, G, X);
-    else
-      encode_tile<KT0, DF>(a, res, q, P, X);
-    // prefetch: the next tile's positions and this tile's targets / d_out
     float Pn[kNT][4];
-    load_pos(next, Pn);
+    if constexpr (XMEM) {
+      if constexpr (KT0 > 2) load_x(tile, Xn);
+#pragma unroll
+      for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) X[kt][nt] = Xn[kt][nt];
+      // one tile ahead when the prefetch registers are cheap (32 features)
+      if constexpr (KT0 <= 2) load_x(next, Xn);
+    } else {
+      if constexpr (kPipe)
+        gather_finish<DF / 8, DF % 8, KT0>(a, res, q, P, G, X);
+      else
+        encode_tile<KT0, DF>(a, res, q, P, X);
+      // prefetch: the next tile's positions
+      load_pos(next, Pn);
+    }
+    // this tile's targets / d_out
     float Tv[kNT][4];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt)
@@ -1080,12 +1109,14 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         for (int r = 0; r < 4; ++r) y[0][nt][r] = y[0][nt][r] + bias[4 * q + r];
     }
     // the next tile's gathers fly while this tile finishes
-    if constexpr (kPipe)
-      if (next < a.n_tiles) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, Pn, G);
+    if constexpr (!XMEM) {
+      if constexpr (kPipe)
+        if (next < a.n_tiles) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, Pn, G);
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
+      for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-      for (int d = 0; d < 4; ++d) P[nt][d] = Pn[nt][d];
+        for (int d = 0; d < 4; ++d) P[nt][d] = Pn[nt][d];
+    }
 
     if constexpr (!TRAIN) {
 #pragma unroll
@@ -1309,11 +1340,12 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 }
 
 // Training launches are LDS-bound to one 4-wave block per CU (one wave per
-// SIMD), so they may use the whole register file.
-template <int HP, int INP, bool F16, int DF, int NHLT>
+// SIMD), so they may use the whole register file. Their input features come
+// from encode_features_kernel (XMEM).
+template <int HP, int INP, bool F16, int NHLT>
 __global__ void __launch_bounds__(kBlockThreads)
     __attribute__((amdgpu_waves_per_eu(1, 1))) field_train_kernel(FieldArgs a) {
-  field_body<HP, INP, F16, true, DF, NHLT>(a);
+  field_body<HP, INP, F16, true, 0, NHLT, true>(a);
 }
 
 template <int HP, int INP, bool F16, int DF>

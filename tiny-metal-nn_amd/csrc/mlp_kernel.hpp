@@ -1,0 +1,510 @@
+// mlp_kernel.hpp -- fp16 training kernel of the 64-wide MLP with no LDS
+// staging of activations or deltas.
+//
+// The weight gradients dW_k = sum over points of h_{k-1} delta_k^T contract
+// over the points of a tile, so their MFMA operands need the points along K:
+// each lane must hold consecutive points of one unit. Layer products leave
+// the opposite arrangement in registers (the "D layout": a lane holds four
+// consecutive units of one point). Instead of a round trip through LDS, this
+// kernel transposes on the matrix cores: an MFMA with the packed fp16 tile
+// set as A and a constant 0/1 selection fragment as B returns the transposed
+// 16x16 tile exactly (every product is x * 1 or x * 0 in an fp32
+// accumulator). Those transposed fp16 tiles are precisely the values the LDS
+// path fed to the dW MFMAs (fp16(h), fp16(delta)), so the arithmetic of the
+// weight gradients is unchanged.
+//
+// Occupancy and weight gradients: eight waves per block, two per SIMD (256
+// registers each), so one wave's MFMA / LDS latencies hide behind the other's
+// work. The block walks its tiles in rounds of eight (one per wave); each
+// wave parks the transposed operands of its tile in LDS (lane-private 16-byte
+// slots), and after a barrier every wave accumulates the dW tiles it OWNS over
+// all eight waves' points, in wave order, in registers that live across all
+// rounds. Each dW element has exactly one owner (deterministic sums, no
+// cross-wave reduction); the owners write the block's partial row at the end.
+// Parking slots are reused as layers die: the output gradient, then delta_k
+// in the slots of h_k once dW_{k+1} (the last reader of h_k) is done.
+//
+// Everything else follows field_body in the fp16 training configuration:
+// split-fp16 forward (hi/lo operands, three MFMAs per product), fp16 backward
+// with a power-of-two loss scale, input features read as X tiles from
+// encode_features_kernel. Two details differ and are of fp16 size: the ReLU
+// derivative is taken from the fp16 activation (a positive activation below
+// 2^-25 rounds to 0 and masks its delta), and the bias gradients sum the
+// fp16 deltas on the matrix cores (an all-ones A operand against the
+// transposed delta tiles).
+#pragma once
+
+#include "field_kernel.hpp"
+
+namespace tmnn_hip {
+
+constexpr int kMlpWaves = 8;
+
+// LDS plan of mlp_train_kernel (bytes): the packed weight image, the per-wave
+// loss slots, then per wave its parking slots (16 bytes per lane each):
+// [0, KT0) input features, KT0 + k * HT + t hidden layer k (then delta_k),
+// KT0 + NHL * HT the output gradient.
+struct MlpLds {
+  int32_t loss, park, park_bytes, total;
+};
+
+__host__ __device__ inline MlpLds mlp_lds(const FieldLayout &s) {
+  MlpLds m;
+  m.loss = s.dw_off;
+  m.park = m.loss + 16 * 4;
+  m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + 1) * 64 * 16;
+  m.total = m.park + kMlpWaves * m.park_bytes;
+  return m;
+}
+
+// Lane-private 16-byte LDS slots (slot-major, lane-minor: conflict-free).
+__device__ __forceinline__ void park(unsigned char *base, int slot, int lane, half8 v) {
+  *reinterpret_cast<half8 *>(base + (slot * 64 + lane) * 16) = v;
+}
+__device__ __forceinline__ half8 unpark(const unsigned char *base, int slot, int lane) {
+  return *reinterpret_cast<const half8 *>(base + (slot * 64 + lane) * 16);
+}
+
+// B-operand selection fragments of the transpose MFMA: with a packed tile
+// pair (t0 | t1) as A, sel_lo picks t0 and sel_hi picks t1 (lane p + 16 q,
+// K slot j: t0 unit 4q + j for j < 4, t1 unit 4q + j - 4 for j >= 4).
+__device__ __forceinline__ void selection_fragments(int p, int q, half8 &sel_lo, half8 &sel_hi) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    sel_lo[j] = (j < 4 && 4 * q + j == p) ? static_cast<_Float16>(1.0f) : static_cast<_Float16>(0.0f);
+    sel_hi[j] = (j >= 4 && 4 * q + j - 4 == p) ? static_cast<_Float16>(1.0f) : static_cast<_Float16>(0.0f);
+  }
+}
+
+// Transposed fp16 tiles of a packed D-layout tile set b[KS][nt] (units along
+// K, 32 points): T[u] for unit tile u = 2 ks + t holds, in lane p + 16 q,
+// slot j, the value of unit 16 u + p at point 4 q + j (j < 4) or
+// 16 + 4 q + j - 4 (j >= 4) -- the A/B operand of a dW MFMA over the tile's
+// 32 points.
+template <int KS>
+__device__ __forceinline__ void transpose_tiles(const half8 (&b)[KS][kNT], half8 sel_lo,
+                                                half8 sel_hi, half8 (&T)[2 * KS]) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const f32x4 a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[ks][0], sel_lo, z, 0, 0, 0);
+    const f32x4 a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[ks][1], sel_lo, z, 0, 0, 0);
+    const f32x4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[ks][0], sel_hi, z, 0, 0, 0);
+    const f32x4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[ks][1], sel_hi, z, 0, 0, 0);
+    T[2 * ks] = pack8(a0, a1);
+    T[2 * ks + 1] = pack8(c0, c1);
+  }
+}
+
+// out[MT][nt] = A(frag) x B for a packed B operand (fp16, K step 32).
+template <int KS, int MT>
+__device__ __forceinline__ void mma_packed(const unsigned char *frag, const half8 (&b)[KS][kNT],
+                                           f32x4 (&out)[MT][kNT], int lane) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4 acc[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const half8 av = *reinterpret_cast<const half8 *>(frag + ((mt * KS + ks) * 64 + lane) * 16);
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[ks][nt], acc[nt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
+  }
+}
+
+// Split-fp16 forward product (as layer_mma_split) on prepacked operands.
+template <int KS, int MT>
+__device__ __forceinline__ void mma_split_packed(const unsigned char *frag_hi,
+                                                 const unsigned char *frag_lo,
+                                                 const half8 (&bh)[KS][kNT],
+                                                 const half8 (&bl)[KS][kNT],
+                                                 f32x4 (&out)[MT][kNT], int lane) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4 acc[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = ((mt * KS + ks) * 64 + lane) * 16;
+      const half8 ah = *reinterpret_cast<const half8 *>(frag_hi + off);
+      const half8 al = *reinterpret_cast<const half8 *>(frag_lo + off);
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[ks][nt], acc[nt], 0, 0, 0);
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[ks][nt], acc[nt], 0, 0, 0);
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[ks][nt], acc[nt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
+  }
+}
+
+template <int KT>
+__device__ __forceinline__ void pack_split_tiles(const f32x4 (&t)[KT][kNT], half8 (&bh)[KT / 2][kNT],
+                                                 half8 (&bl)[KT / 2][kNT]) {
+#pragma unroll
+  for (int ks = 0; ks < KT / 2; ++ks)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) pack8_split(t[2 * ks][nt], t[2 * ks + 1][nt], bh[ks][nt], bl[ks][nt]);
+}
+
+template <int KT>
+__device__ __forceinline__ void pack_tiles(const f32x4 (&t)[KT][kNT], half8 (&b)[KT / 2][kNT]) {
+#pragma unroll
+  for (int ks = 0; ks < KT / 2; ++ks)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = pack8(t[2 * ks][nt], t[2 * ks + 1][nt]);
+}
+
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// ReLU' of a packed fp16 activation tile pair as a 16-bit lane mask
+// (0xFFFF where the activation is > 0): |bits| != 0, since the activations
+// are max(v, 0) (the sign bit masks out a -0).
+__device__ __forceinline__ u16x8 relu_mask_words(half8 h) {
+  const u16x8 b = __builtin_bit_cast(u16x8, h) & static_cast<uint16_t>(0x7fff);
+  const u16x8 one = static_cast<uint16_t>(1);
+  const u16x8 m = b < one ? b : one;  // 1 where nonzero
+  const u16x8 zero = static_cast<uint16_t>(0);
+  return zero - m;                    // 0xFFFF or 0
+}
+
+__device__ __forceinline__ half8 apply_mask(half8 v, u16x8 m) {
+  return __builtin_bit_cast(half8, __builtin_bit_cast(u16x8, v) & m);
+}
+
+template <int HP, int INP, int NHL>
+__global__ void __launch_bounds__(kMlpWaves * 64)
+    __attribute__((amdgpu_waves_per_eu(2, 2))) mlp_train_kernel(FieldArgs a) {
+  constexpr int HT = HP / 16;    // unit tiles of a hidden layer
+  constexpr int HS = HT / 2;     // K steps over a hidden layer
+  constexpr int KT0 = INP / 16;  // input feature tiles
+  constexpr int XS = KT0 / 2;    // K steps over the input
+  constexpr int W = kMlpWaves;
+  static_assert(HT % 2 == 0 && KT0 % 2 == 0 && NHL >= 1, "shape");
+  // owned jobs (dW tiles + bias tiles) per phase, wave w owns jobs w + W j
+  constexpr int kJobsOut = HT + 1;        // dW_out tiles (units x outputs) + b_out
+  constexpr int kJobsHid = HT * HT + HT;  // dW_k tiles + b_k tiles
+  constexpr int kJobs0 = KT0 * HT + HT;   // dW_0 tiles + b_0 tiles
+  constexpr int kSlotsOut = (kJobsOut + W - 1) / W;
+  constexpr int kSlotsHid = (kJobsHid + W - 1) / W;
+  constexpr int kSlots0 = (kJobs0 + W - 1) / W;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const FieldLayout s = make_layout(INP, HP, a.IN, a.H, NHL, a.M, a.mlp_count, true, true, W,
+                                    false, true);
+  const MlpLds ml = mlp_lds(s);
+  stage_weights<true, true>(a, s, smem);
+  // parked operands of absent tiles must be finite (they meet zero deltas)
+  for (int e = threadIdx.x; e < W * ml.park_bytes / 16; e += blockDim.x)
+    reinterpret_cast<uint4 *>(smem + ml.park)[e] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int p = lane & 15;
+  const int q = lane >> 4;
+  const bool wgrads = a.mode != kModeInputGrad;
+  unsigned char *park0 = smem + ml.park;
+  unsigned char *pk = park0 + wave * ml.park_bytes;
+  auto hslot = [](int k, int it) { return KT0 + k * HT + it; };
+  constexpr int kGSlot = KT0 + NHL * HT;
+  // operand of wave w's slot
+  auto opnd = [&](int w, int slot) {
+    return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
+  };
+  half8 sel_lo, sel_hi, ones;
+  selection_fragments(p, q, sel_lo, sel_hi);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = static_cast<_Float16>(1.0f);
+
+  f32x4 accO[kSlotsOut];
+  f32x4 accH[NHL > 1 ? NHL - 1 : 1][kSlotsHid];
+  f32x4 acc0[kSlots0];
+#pragma unroll
+  for (int j = 0; j < kSlotsOut; ++j) accO[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < (NHL > 1 ? NHL - 1 : 1); ++k)
+#pragma unroll
+    for (int j = 0; j < kSlotsHid; ++j) accH[k][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kSlots0; ++j) acc0[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float lane_loss = 0.0f;
+  const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
+  const bool has_target = a.mode != kModeInputGrad && a.target != nullptr;
+  const bool dx_vec = (a.IN & 3) == 0;
+  const int n_rounds = (a.n_tiles + W - 1) / W;
+
+  for (int round = blockIdx.x; round < n_rounds; round += gridDim.x) {
+    const int tile = round * W + wave;
+    const bool have = tile < a.n_tiles;  // waves past the batch park zero deltas
+    int pt[kNT];
+    bool valid[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      pt[nt] = tile * kTilePts + 16 * nt + p;
+      valid[nt] = have && pt[nt] < a.n;
+    }
+    f32x4 X[KT0][kNT];
+#pragma unroll
+    for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+        X[kt][nt] = have ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+    float Tv[kNT][4];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tv[nt][r] = 0.0f;
+    if (has_target) {
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        const size_t row = static_cast<size_t>(valid[nt] ? pt[nt] : 0) * a.M;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 4 * q + r;
+          const float v = a.target[row + (o < a.M ? o : a.M - 1)];
+          Tv[nt][r] = (valid[nt] && o < a.M) ? v : 0.0f;
+        }
+      }
+    }
+
+    // ---- forward; transposed fp16 layer inputs parked, ReLU masks kept
+    f32x4 act[HT][kNT];
+    u16x8 mask[NHL][HS][kNT];
+    {
+      half8 bh[XS][kNT], bl[XS][kNT];
+      pack_split_tiles<KT0>(X, bh, bl);
+      half8 xT[KT0];
+      transpose_tiles<XS>(bh, sel_lo, sel_hi, xT);
+#pragma unroll
+      for (int ft = 0; ft < KT0; ++ft) park(pk, ft, lane, xT[ft]);
+      mma_split_packed<XS, HT>(smem + s.fwd_off(0), smem + s.fwd_lo_off(0), bh, bl, act, lane);
+    }
+    auto bias_relu = [&](int k) {
+      const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(k));
+#pragma unroll
+      for (int mt = 0; mt < HT; ++mt) {
+        const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + 16 * mt + 4 * q);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) act[mt][nt][r] = __builtin_fmaxf(act[mt][nt][r] + bv[r], 0.0f);
+      }
+    };
+    auto pack_hidden = [&](int k, half8 (&bh)[HS][kNT], half8 (&bl)[HS][kNT]) {
+      pack_split_tiles<HT>(act, bh, bl);
+#pragma unroll
+      for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) mask[k][ks][nt] = relu_mask_words(bh[ks][nt]);
+      half8 hT[HT];
+      transpose_tiles<HS>(bh, sel_lo, sel_hi, hT);
+#pragma unroll
+      for (int it = 0; it < HT; ++it) park(pk, hslot(k, it), lane, hT[it]);
+    };
+    bias_relu(0);
+#pragma unroll
+    for (int k = 1; k < NHL; ++k) {
+      half8 bh[HS][kNT], bl[HS][kNT];
+      pack_hidden(k - 1, bh, bl);
+      mma_split_packed<HS, HT>(smem + s.fwd_off(k), smem + s.fwd_lo_off(k), bh, bl, act, lane);
+      bias_relu(k);
+    }
+    f32x4 y[1][kNT];
+    {
+      half8 bh[HS][kNT], bl[HS][kNT];
+      pack_hidden(NHL - 1, bh, bl);
+      mma_split_packed<HS, 1>(smem + s.fwd_off(NHL), smem + s.fwd_lo_off(NHL), bh, bl, y, lane);
+      const f32x4 bv = *reinterpret_cast<const f32x4 *>(
+          reinterpret_cast<const float *>(smem + s.bias_off(NHL)) + 4 * q);
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[0][nt][r] = y[0][nt][r] + bv[r];
+    }
+
+    // ---- loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
+    f32x4 g[2][kNT];
+    output_grad<2>(a, y, Tv, valid, pt, q, lane_loss, g);
+    half8 gb[1][kNT];
+    pack_tiles<2>(g, gb);
+    {
+      half8 gT[2];
+      transpose_tiles<1>(gb, sel_lo, sel_hi, gT);
+      park(pk, kGSlot, lane, gT[0]);
+    }
+    f32x4 dl[HT][kNT];
+    mma_packed<1, HT>(smem + s.bwd_off(NHL), gb, dl, lane);
+
+    // ---- owners: dW_out (units x outputs) and b_out over the round's points
+    __syncthreads();
+    if (wgrads) {
+#pragma unroll
+      for (int j = 0; j < kSlotsOut; ++j) {
+        const int job = wave + W * j;
+        if (job < kJobsOut) {
+          f32x4 acc = accO[j];
+#pragma unroll
+          for (int w = 0; w < W; ++w)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                job < HT ? opnd(w, hslot(NHL - 1, job)) : ones, opnd(w, kGSlot), acc, 0, 0, 0);
+          accO[j] = acc;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- hidden layers NHL-1 .. 0: delta_k (masked, fp16) parked over h_k,
+    // owners add dW_k / b_k, then delta_{k-1} (or the input-feature gradient)
+#pragma unroll
+    for (int k = NHL - 1; k >= 0; --k) {
+      half8 b[HS][kNT];
+      pack_tiles<HT>(dl, b);
+#pragma unroll
+      for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = apply_mask(b[ks][nt], mask[k][ks][nt]);
+      {
+        half8 dT[HT];
+        transpose_tiles<HS>(b, sel_lo, sel_hi, dT);
+#pragma unroll
+        for (int ut = 0; ut < HT; ++ut) park(pk, hslot(k, ut), lane, dT[ut]);
+      }
+      if (k > 0) {
+        mma_packed<HS, HT>(smem + s.bwd_off(k), b, dl, lane);
+      } else {
+        f32x4 dx[KT0][kNT];
+        mma_packed<HS, KT0>(smem + s.bwd_off(0), b, dx, lane);
+        if (have) {
+          // rows past the batch exist (the buffer is padded to whole tiles)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) {
+            float *row = a.dx_out + static_cast<size_t>(pt[nt]) * a.IN;
+#pragma unroll
+            for (int kt = 0; kt < KT0; ++kt) {
+              const int f0 = 16 * kt + 4 * q;
+              f32x4 v = dx[kt][nt];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) v[r] = v[r] * a.inv_loss_scale;
+              if (dx_vec) {
+                if (f0 < a.IN) *reinterpret_cast<f32x4 *>(row + f0) = v;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  if (f0 + r < a.IN) row[f0 + r] = v[r];
+              }
+            }
+          }
+        }
+      }
+      __syncthreads();
+      if (wgrads) {
+        if (k > 0) {
+#pragma unroll
+          for (int j = 0; j < kSlotsHid; ++j) {
+            const int job = wave + W * j;
+            if (job < kJobsHid) {
+              // job < HT*HT: dW tile (it, ut) = (job / HT, job % HT); else bias tile
+              const int it = job / HT, ut = job < HT * HT ? job % HT : job - HT * HT;
+              f32x4 acc = accH[k - 1][j];
+#pragma unroll
+              for (int w = 0; w < W; ++w)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    job < HT * HT ? opnd(w, hslot(k - 1, it)) : ones, opnd(w, hslot(k, ut)), acc, 0, 0, 0);
+              accH[k - 1][j] = acc;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < kSlots0; ++j) {
+            const int job = wave + W * j;
+            if (job < kJobs0) {
+              const int ft = job / HT, ut = job < KT0 * HT ? job % HT : job - KT0 * HT;
+              f32x4 acc = acc0[j];
+#pragma unroll
+              for (int w = 0; w < W; ++w)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    job < KT0 * HT ? opnd(w, ft) : ones, opnd(w, hslot(0, ut)), acc, 0, 0, 0);
+              acc0[j] = acc;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
+  // ---- loss partial of the block (wave order)
+  float v = lane_loss;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  float *lred = reinterpret_cast<float *>(smem + ml.loss);
+  if (lane == 0) lred[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.0f;
+    for (int w = 0; w < W; ++w) t += lred[w];
+    a.loss_partials[blockIdx.x] = t;
+  }
+  // ---- owners write their tiles of the block's partial row (reference layout)
+  float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+  const float sc = a.inv_loss_scale;
+  const int H = a.H, IN = a.IN, M = a.M;
+#pragma unroll
+  for (int j = 0; j < kSlotsOut; ++j) {
+    const int job = wave + W * j;
+    if (job < HT) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int u = 16 * job + 4 * q + r;
+        if (u < H && p < M) dst[s.w_off(NHL) + u * M + p] = accO[j][r] * sc;
+      }
+    } else if (job == HT && q == 0 && p < M) {
+      dst[s.b_off(NHL) + p] = accO[j][0] * sc;
+    }
+  }
+#pragma unroll
+  for (int k = 1; k < NHL; ++k)
+#pragma unroll
+    for (int j = 0; j < kSlotsHid; ++j) {
+      const int job = wave + W * j;
+      if (job < HT * HT) {
+        const int it = job / HT, ut = job % HT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * it + 4 * q + r, u = 16 * ut + p;
+          if (i < H && u < H) dst[s.w_off(k) + i * H + u] = accH[k - 1][j][r] * sc;
+        }
+      } else if (job < kJobsHid && q == 0) {
+        const int u = 16 * (job - HT * HT) + p;
+        if (u < H) dst[s.b_off(k) + u] = accH[k - 1][j][0] * sc;
+      }
+    }
+#pragma unroll
+  for (int j = 0; j < kSlots0; ++j) {
+    const int job = wave + W * j;
+    if (job < KT0 * HT) {
+      const int ft = job / HT, ut = job % HT;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int f = 16 * ft + 4 * q + r, u = 16 * ut + p;
+        if (f < IN && u < H) dst[s.w_off(0) + f * H + u] = acc0[j][r] * sc;
+      }
+    } else if (job < kJobs0 && q == 0) {
+      const int u = 16 * (job - KT0 * HT) + p;
+      if (u < H) dst[s.b_off(0) + u] = acc0[j][0] * sc;
+    }
+  }
+}
+
+}  // namespace tmnn_hip

@@ -22,8 +22,10 @@
 
 #include "tmnn_hip.h"
 #include "aux_kernels.hpp"
+#include "encode_kernel.hpp"
 #include "field_kernel.hpp"
 #include "grad_kernel.hpp"
+#include "mlp_kernel.hpp"
 #include "scatter_kernel.hpp"
 #include "sort.hpp"
 #include "wide_kernel.hpp"
@@ -63,6 +65,8 @@ struct KernelChoice {
   FieldKernel fn = nullptr;
   bool reg_dw = false;  // dW accumulated in registers (compile-time layers)
   bool wide = false;    // hidden width 128: the block-cooperative wide kernel
+  bool xmem = false;    // input features from encode_features_kernel
+  bool mlp = false;     // mlp_train_kernel (no activation staging in LDS)
 };
 
 // Hidden width 128 (wide_kernel.hpp): instantiated for the BASELINE 4D shape
@@ -70,10 +74,10 @@ struct KernelChoice {
 KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
 #define TMNN_WIDE(d, f, nhl)                                                         \
   if (D == d && F == f && NHL == nhl) {                                              \
-    if (train) return {f16 ? wide_kernel<d, f, nhl, true, true>                      \
-                           : wide_kernel<d, f, nhl, false, true>, false, true};      \
-    return {f16 ? wide_kernel<d, f, nhl, true, false>                                \
-                : wide_kernel<d, f, nhl, false, false>, false, true};                \
+    if (train) return {f16 ? wide_kernel<d, f, nhl, true, true, true>                \
+                           : wide_kernel<d, f, nhl, false, true, true>, false, true, true}; \
+    return {f16 ? wide_kernel<d, f, nhl, true, false, false>                         \
+                : wide_kernel<d, f, nhl, false, false, false>, false, true, false};  \
   }
   TMNN_WIDE(4, 2, 4)
   TMNN_WIDE(3, 2, 2)
@@ -81,32 +85,45 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
   return {};
 }
 
-// Geometry-specialised kernels (compile-time D, F and hidden-layer count;
-// dW in registers) for the BASELINE shapes, else the generic kernels
-// (runtime geometry, dW accumulated in LDS).
+// Training kernels read their features from encode_features_kernel; the
+// BASELINE MLP shapes (compile-time hidden-layer count) keep dW in registers,
+// the rest accumulate it in LDS. Forward kernels encode inline, specialised
+// on the BASELINE geometries (compile-time D, F) or on the runtime geometry.
 KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL) {
   if (HP == kWideHP) return INP == 32 ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
   const int DF = D * 8 + F;
-#define TMNN_SPEC(hp, inp, df, nhl)                                                  \
-  if (HP == hp && INP == inp && DF == df && (!train || NHL == nhl)) {               \
-    if (train)                                                                      \
-      return {f16 ? field_train_kernel<hp, inp, true, df, nhl>                      \
-                  : field_train_kernel<hp, inp, false, df, nhl>,                    \
-              true};                                                                \
-    return {f16 ? field_forward_kernel<hp, inp, true, df>                           \
-                : field_forward_kernel<hp, inp, false, df>,                         \
-            false};                                                                 \
+  // fp16 training of the 64-wide, 32-feature shapes: transposes on the matrix
+  // cores instead of LDS staging (mlp_kernel.hpp)
+  if (train && f16 && HP == 64 && INP == 32 && NHL == 2)
+    return {mlp_train_kernel<64, 32, 2>, true, false, true, true};
+  if (train && f16 && HP == 64 && INP == 32 && NHL == 1)
+    return {mlp_train_kernel<64, 32, 1>, true, false, true, true};
+  if (train) {
+#define TMNN_TRAIN_SPEC(hp, inp, nhl)                                              \
+  if (HP == hp && INP == inp && NHL == nhl)                                        \
+    return {f16 ? field_train_kernel<hp, inp, true, nhl>                           \
+                : field_train_kernel<hp, inp, false, nhl>,                         \
+            true, false, true};
+    TMNN_TRAIN_SPEC(64, 32, 2)  // image fit: 16x2 features, 64x2 MLP
+    TMNN_TRAIN_SPEC(64, 32, 1)  // NeRF density: 16x2, 64x1
+    TMNN_TRAIN_SPEC(64, 64, 3)  // SDF: 16x4, 64x3
+#undef TMNN_TRAIN_SPEC
   }
-  TMNN_SPEC(64, 32, 2 * 8 + 2, 2)  // image fit: 2D, 16x2 features, 64x2 MLP
-  TMNN_SPEC(64, 32, 3 * 8 + 2, 1)  // NeRF density: 3D, 16x2, 64x1
-  TMNN_SPEC(64, 64, 3 * 8 + 4, 3)  // SDF: 3D, 16x4, 64x3
+#define TMNN_SPEC(hp, inp, df)                                                       \
+  if (!train && HP == hp && INP == inp && DF == df)                                  \
+    return {f16 ? field_forward_kernel<hp, inp, true, df>                            \
+                : field_forward_kernel<hp, inp, false, df>,                          \
+            false};
+  TMNN_SPEC(64, 32, 2 * 8 + 2)  // image fit: 2D, 16x2 features
+  TMNN_SPEC(64, 32, 3 * 8 + 2)  // NeRF density: 3D, 16x2
+  TMNN_SPEC(64, 64, 3 * 8 + 4)  // SDF: 3D, 16x4
 #undef TMNN_SPEC
 #define TMNN_SEL(hp, inp)                                                        \
   if (HP == hp && INP == inp) {                                                  \
     if (train)                                                                   \
-      return {f16 ? field_train_kernel<hp, inp, true, 0, 0>                      \
-                  : field_train_kernel<hp, inp, false, 0, 0>,                    \
-              false};                                                            \
+      return {f16 ? field_train_kernel<hp, inp, true, 0>                         \
+                  : field_train_kernel<hp, inp, false, 0>,                       \
+              false, false, true};                                               \
     return {f16 ? field_forward_kernel<hp, inp, true, 0>                         \
                 : field_forward_kernel<hp, inp, false, 0>,                       \
             false};                                                              \
@@ -157,6 +174,8 @@ struct KernelPlan {
   bool dw_global = false;  // dW accumulator outside LDS
   bool reg_dw = false;     // dW accumulator in registers
   bool wide = false;       // block-cooperative hidden-128 kernel (4 waves, 128-point block tiles)
+  bool xmem = false;       // features from encode_features_kernel (X tiles in xfeat)
+  bool mlp = false;        // mlp_train_kernel
   int max_blocks = 0;   // resident blocks on the whole device
 };
 
@@ -187,6 +206,7 @@ struct tmnn_trainer {
   DevBuf partials, loss_partials, loss_out;
   DevBuf in_pos, in_tgt, s_pos, s_tgt, keys0, keys1, vals0, vals1, sort_tmp, out_buf;
   DevBuf dx;  // [batch][IN] input-feature gradients between the two train kernels
+  DevBuf xfeat;  // input features of the batch as X tiles (encode_kernel.hpp)
   DevBuf wide_mask, wide_act;  // hidden-128 kernel: per-tile ReLU bits and fp16 activations
   DevBuf dbg_a, dbg_b, dbg_c;
 
@@ -198,7 +218,7 @@ struct tmnn_trainer {
 
   // Step profiling: one set of phase events per profiled step, summed and
   // recycled when the profile is read.
-  static constexpr int kProfEvents = 6;  // sort | fwd/bwd | scatter | reduce | adam |
+  static constexpr int kProfEvents = 7;  // sort | encode | fwd/bwd | scatter | reduce | adam |
   bool profiling = false;
   std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
   size_t prof_used = 0;
@@ -277,11 +297,12 @@ int prof_collect(tmnn_trainer *tr) {
     for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k)
       TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[k], e[k + 1]));
     tr->prof_acc.gpu_sort_us += 1e3 * ms[0];
-    tr->prof_acc.gpu_fwd_bwd_us += 1e3 * ms[1];
-    tr->prof_acc.gpu_scatter_us += 1e3 * ms[2];
-    tr->prof_acc.gpu_reduce_us += 1e3 * ms[3];
-    tr->prof_acc.gpu_adam_us += 1e3 * ms[4];
-    tr->prof_acc.gpu_total_us += 1e3 * (ms[0] + ms[1] + ms[2] + ms[3] + ms[4]);
+    tr->prof_acc.gpu_encode_us += 1e3 * ms[1];
+    tr->prof_acc.gpu_fwd_bwd_us += 1e3 * ms[2];
+    tr->prof_acc.gpu_scatter_us += 1e3 * ms[3];
+    tr->prof_acc.gpu_reduce_us += 1e3 * ms[4];
+    tr->prof_acc.gpu_adam_us += 1e3 * ms[5];
+    tr->prof_acc.gpu_total_us += 1e3 * (ms[0] + ms[1] + ms[2] + ms[3] + ms[4] + ms[5]);
     tr->prof_acc.steps += 1;
   }
   tr->prof_used = 0;
@@ -294,7 +315,30 @@ int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
   out.fn = kc.fn;
   out.reg_dw = kc.reg_dw;
   out.wide = kc.wide;
+  out.xmem = kc.xmem;
+  out.mlp = kc.mlp;
   if (!out.fn) return fail(TMNN_ERR_UNSUPPORTED, "no kernel for this geometry");
+  if (out.mlp) {
+    const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
+                                      tr->d.num_hidden_layers, tr->d.num_outputs,
+                                      static_cast<int>(tr->mlp_count), true, true, kMlpWaves,
+                                      false, true);
+    out.wpb = kMlpWaves;
+    out.lds = mlp_lds(s).total;
+    if (out.lds > kMaxLdsBytes) return fail(TMNN_ERR_UNSUPPORTED, "MLP train kernel LDS plan too large");
+    out.f16 = f16;
+    out.train = train;
+    out.image_bytes = static_cast<size_t>(s.dw_off);
+    TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
+    TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, out.lds));
+    int per_cu = 0;
+    TMNN_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<const void *>(out.fn), 64 * out.wpb, out.lds));
+    if (per_cu < 1) return fail(TMNN_ERR_UNSUPPORTED, "MLP train kernel cannot be resident");
+    out.max_blocks = per_cu * tr->ctx->cu_count;
+    return TMNN_OK;
+  }
   if (out.wide) {
     const FieldLayout fl = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
                                        tr->d.num_hidden_layers, tr->d.num_outputs,
@@ -411,9 +455,47 @@ int ensure_image(tmnn_trainer *tr, KernelPlan &plan) {
   return TMNN_OK;
 }
 
-int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n) {
-  const int rc = ensure_image(tr, plan);
+// Input features of n points at pos as X tiles in tr->xfeat.
+int launch_encode(tmnn_trainer *tr, const float *pos, int n) {
+  EncodeArgs e{};
+  e.n = n;
+  e.n_pad = (n + kTilePts - 1) / kTilePts * kTilePts;
+  e.L = tr->d.num_levels;
+  e.KT0 = tr->INP / 16;
+  e.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
+  for (int l = 0; l < kMaxLevels; ++l) e.res[l] = tr->res[l];
+  e.pos = pos;
+  e.table = tr->params.as<float>();
+  e.xfeat = tr->xfeat.as<float>();
+  const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads);
+  hipStream_t st = tr->ctx->stream;
+  switch (tr->d.spatial_dims * 8 + tr->d.features_per_level) {
+    case 2 * 8 + 1: hipLaunchKernelGGL((encode_features_kernel<2, 1>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 2 * 8 + 2: hipLaunchKernelGGL((encode_features_kernel<2, 2>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 2 * 8 + 4: hipLaunchKernelGGL((encode_features_kernel<2, 4>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 3 * 8 + 1: hipLaunchKernelGGL((encode_features_kernel<3, 1>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 3 * 8 + 2: hipLaunchKernelGGL((encode_features_kernel<3, 2>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 3 * 8 + 4: hipLaunchKernelGGL((encode_features_kernel<3, 4>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 4 * 8 + 1: hipLaunchKernelGGL((encode_features_kernel<4, 1>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 4 * 8 + 2: hipLaunchKernelGGL((encode_features_kernel<4, 2>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    default: hipLaunchKernelGGL((encode_features_kernel<4, 4>), grid, dim3(kEncodeThreads), 0, st, e); break;
+  }
+  TMNN_HIP_TRY(hipGetLastError());
+  return TMNN_OK;
+}
+
+// Launches a plan's field kernel over n points; XMEM plans first encode a.pos
+// into tr->xfeat (unless reuse_x: the features of these points are there
+// already), with profile mark prof_after_encode (if >= 0) in between.
+int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
+                 int prof_after_encode = -1, bool reuse_x = false) {
+  int rc = ensure_image(tr, plan);
   if (rc != TMNN_OK) return rc;
+  if (plan.xmem) {
+    if (!reuse_x && (rc = launch_encode(tr, a.pos, n)) != TMNN_OK) return rc;
+    a.xfeat = tr->xfeat.as<float>();
+  }
+  if (prof_after_encode >= 0 && (rc = prof_mark(tr, prof_after_encode)) != TMNN_OK) return rc;
   a.image = static_cast<const unsigned char *>(plan.image);
   a.n = n;
   a.n_tiles = (n + kTilePts - 1) / kTilePts;
@@ -454,7 +536,11 @@ int ensure_batch(tmnn_trainer *tr, int n) {
   size_t tmp = 0;
   TMNN_HIP_TRY(morton_sort_temp_bytes(n, &tmp));
   TMNN_HIP_TRY(tr->sort_tmp.ensure(std::max<size_t>(tmp, 256)));
-  TMNN_HIP_TRY(tr->dx.ensure(static_cast<size_t>(n) * tr->IN * sizeof(float)));
+  // dx rows for the whole last tile: the MLP train kernel stores unconditionally
+  TMNN_HIP_TRY(tr->dx.ensure(static_cast<size_t>((n + kTilePts - 1) / kTilePts) * kTilePts *
+                             tr->IN * sizeof(float)));
+  TMNN_HIP_TRY(tr->xfeat.ensure(static_cast<size_t>((n + kTilePts - 1) / kTilePts) * kTilePts *
+                                tr->INP * sizeof(float)));
   if (tr->HP == kWideHP && tr->d.num_hidden_layers > 1) {
     const size_t tiles = static_cast<size_t>((n + kTilePts - 1) / kTilePts);
     const size_t layers = static_cast<size_t>(tr->d.num_hidden_layers - 1);
@@ -549,11 +635,11 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   a.grad_partials = tr->partials.as<float>();
   a.loss_partials = tr->loss_partials.as<float>();
   a.dx_out = tr->dx.as<float>();
-  const int blocks = launch_field(tr, tr->train_plan, a, n);
+  const int blocks = launch_field(tr, tr->train_plan, a, n, 2);
   if (blocks < 0) return blocks;
-  if ((rc = prof_mark(tr, 2)) != TMNN_OK) return rc;
-  if ((rc = launch_scatter(tr, pos, n)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
+  if ((rc = launch_scatter(tr, pos, n)) != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + kReduceCols - 1) / kReduceCols),
                      dim3(kReduceCols * kReduceGroups), 0,
                      tr->ctx->stream, tr->partials.as<float>(), blocks,
@@ -627,9 +713,9 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
                      tr->loss_partials.as<float>(), blocks, n,
                      d_loss ? d_loss : tr->loss_out.as<float>());
   TMNN_HIP_TRY(hipGetLastError());
-  if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
-  if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 5)) != TMNN_OK) return rc;
+  if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 6)) != TMNN_OK) return rc;
   if (tr->prof_cur >= 0) tr->prof_acc.batch_size = static_cast<uint32_t>(n);
   tr->prof_cur = -1;
   ++tr->step;
@@ -1036,7 +1122,8 @@ int tmnn_evaluate_with_gradient(tmnn_trainer *tr, const float *positions, float 
     a.dx_out = tr->dx.as<float>();
     a.grad_partials = tr->partials.as<float>();
     a.loss_partials = tr->loss_partials.as<float>();
-    const int blocks = launch_field(tr, tr->grad_plan, a, n);
+    // the features of these points are the same for every output
+    const int blocks = launch_field(tr, tr->grad_plan, a, n, -1, m > 0);
     if (blocks < 0) return blocks;
     g.m = m;
     const dim3 grid((n + 255) / 256);

@@ -135,7 +135,9 @@ __device__ __forceinline__ void apply_bits(f32x4 (&t)[kWideHT][kNT], uint64_t b)
         if (!((b >> ((mt * kNT + nt) * 4 + r)) & 1ull)) t[mt][nt][r] = 0.0f;
 }
 
-template <int D, int F, int NHL, bool F16, bool TRAIN>
+// XMEM: input features read from a.xfeat (encode_features_kernel) instead
+// of encoded here.
+template <int D, int F, int NHL, bool F16, bool TRAIN, bool XMEM>
 __global__ void __launch_bounds__(kWideWaves * 64)
     __attribute__((amdgpu_waves_per_eu(1, 1))) wide_kernel(FieldArgs a) {
   constexpr int HT = kWideHT;
@@ -194,7 +196,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
       valid[nt] = tile < a.n_tiles && pt[nt] < a.n;
 #pragma unroll
       for (int d = 0; d < 4; ++d)
-        P[nt][d] = (valid[nt] && d < D) ? a.pos[static_cast<size_t>(pt[nt]) * D + d] : 0.0f;
+        P[nt][d] = (!XMEM && valid[nt] && d < D) ? a.pos[static_cast<size_t>(pt[nt]) * D + d] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int o = 4 * q + r;
@@ -203,7 +205,18 @@ __global__ void __launch_bounds__(kWideWaves * 64)
       }
     }
     f32x4 X[KT0][kNT];
-    encode_tile<KT0, DF>(a, res, q, P, X);
+    if constexpr (XMEM) {
+      const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
+#pragma unroll
+      for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          X[kt][nt] = tile < a.n_tiles
+                          ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      encode_tile<KT0, DF>(a, res, q, P, X);
+    }
 
     // ---- forward, one layer's weights in LDS at a time
     f32x4 act[HT][kNT];

@@ -93,6 +93,7 @@ class StepProfile(ctypes.Structure):
         ("gpu_reduce_us", ctypes.c_double),
         ("gpu_adam_us", ctypes.c_double),
         ("gpu_total_us", ctypes.c_double),
+        ("gpu_encode_us", ctypes.c_double),
     ]
 
 
