@@ -77,6 +77,11 @@ GEOMS = {
                       base_resolution=8.0, per_level_scale=1.4), dict(n_neurons=64, n_hidden_layers=2), 4),
     "small": (3, dict(n_levels=2, n_features_per_level=2, log2_hashmap_size=10,
                       base_resolution=4.0, per_level_scale=2.0), dict(n_neurons=8, n_hidden_layers=1), 1),
+    # 16 MB per level: the hash-grid backward runs level-major (large tables)
+    "3d_bigT": (3, dict(n_levels=4, n_features_per_level=2, log2_hashmap_size=21,
+                        base_resolution=16.0, per_level_scale=2.0), dict(n_neurons=64, n_hidden_layers=1), 1),
+    "4d_bigT": (4, dict(n_levels=4, n_features_per_level=2, log2_hashmap_size=21,
+                        base_resolution=8.0, per_level_scale=1.4), dict(n_neurons=64, n_hidden_layers=2), 4),
 }
 
 
@@ -161,7 +166,12 @@ def _grads_vs_oracle(oracle, name, precision, n, seed):
                       batch=1 << 20) as tr:
         hw, mw = tr.get_weights()
         pos = rng.random((n, d), dtype=np.float32)
-        g = rng.normal(0, 1.0, (n, m_out)).astype(np.float32)
+        if precision == "fp16":
+            # the fp16 forward is not the oracle's fp32 one: keep ReLU masks
+            # decidable (see away_from_relu_kinks)
+            pos = away_from_relu_kinks(oracle, tr, hw, mw, pos)
+            assert len(pos) > 0.95 * n
+        g = rng.normal(0, 1.0, (len(pos), m_out)).astype(np.float32)
         tr.zero_gradients()
         tr.backward_accumulate(pos, g)
         gh, gm = tr.debug_gradients()
@@ -170,7 +180,8 @@ def _grads_vs_oracle(oracle, name, precision, n, seed):
         return gh, gm, mask, ogh, ogm, omask, tr.config
 
 
-@pytest.mark.parametrize("name", ["2d_f2", "3d_f2", "3d_f4", "3d_f1", "4d_f2", "small"])
+@pytest.mark.parametrize("name", ["2d_f2", "3d_f2", "3d_f4", "3d_f1", "4d_f2", "small", "3d_bigT",
+                                  "4d_bigT"])
 def test_backward_fp32_matches_oracle(oracle, name):
     _say(f"backward fp32 {name}")
     gh, gm, mask, ogh, ogm, omask, _ = _grads_vs_oracle(oracle, name, "fp32", 2051, 3)
@@ -181,7 +192,7 @@ def test_backward_fp32_matches_oracle(oracle, name):
     assert (diff == 0).mean() > 0.99 and diff.max() <= 16, int(diff.max())
 
 
-@pytest.mark.parametrize("name", ["2d_f2", "3d_f2", "3d_f4", "4d_f2"])
+@pytest.mark.parametrize("name", ["2d_f2", "3d_f2", "3d_f4", "4d_f2", "3d_bigT", "4d_bigT"])
 def test_backward_fp16_matches_oracle(oracle, name):
     _say(f"backward fp16 {name}")
     gh, gm, mask, ogh, ogm, omask, _ = _grads_vs_oracle(oracle, name, "fp16", 4096, 4)

@@ -1,10 +1,8 @@
 // scatter_kernel.hpp -- hash-grid backward: input-feature gradients dx of a
 // batch -> int32 fixed-point table gradients + lazy-Adam visit flags.
 //
-// One thread per (point, level); the grid is level-major (blockIdx.y =
-// level), so at any moment the resident blocks hit one level's slice of the
-// table and Morton-sorted neighbours share cache lines. Few registers and no
-// LDS: many waves per SIMD hide the atomic latency.
+// One thread per point walking the levels; few registers and no LDS: many
+// waves per SIMD hide the atomic latency.
 //
 // Reference semantics (emitHashScatter, mlp_kernel_emitter.cpp:672-901;
 // mask :48-71): per corner and feature, int32(trunc(d * w * 65536)) with
@@ -76,31 +74,13 @@ __device__ __forceinline__ int64_t run_sum(uint32_t key, int64_t v, int lane, bo
   return v;
 }
 
+// One thread per point, all levels in turn: the thread reads its dx row with
+// 16-byte loads (coalesced across the wave) and the lanes of a wave still
+// hold consecutive Morton-sorted points at the same level, which keeps the
+// run merging.
 template <int D, int F>
-__global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterArgs a) {
-  const int l = blockIdx.y;
-  const int i = blockIdx.x * kScatterThreads + threadIdx.x;
-  const int lane = threadIdx.x & 63;
-  // lanes past the batch take part in the wave's run merging with a key no
-  // point can have and nothing to add
-  const bool valid = i < a.n;
-  const int ii = valid ? i : a.n - 1;
-  float p[D];
-#pragma unroll
-  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(ii) * D + k];
-  float d[F];
-  const float *src = a.dx + static_cast<size_t>(ii) * a.IN + l * F;
-  if constexpr (F == 2) {
-    const f32x2 v = *reinterpret_cast<const f32x2 *>(src);
-    d[0] = v[0];
-    d[1] = v[1];
-  } else if constexpr (F == 4) {
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(src);
-#pragma unroll
-    for (int f = 0; f < 4; ++f) d[f] = v[f];
-  } else {
-    d[0] = src[0];
-  }
+__device__ __forceinline__ void scatter_level(const ScatterArgs &a, int l, const float *p,
+                                              const float *d, bool valid, int lane) {
   const Cell<D> c = cell_of<D>(p, a.res[l]);
   const uint32_t tmask = (1u << a.log2T) - 1u;
   const size_t lbase = static_cast<size_t>(l) << a.log2T;
@@ -151,6 +131,70 @@ __global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterAr
       if (valid && tail) mark_entry(a.mask, entry);
     }
   }
+}
+
+template <int D, int F>
+__global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterArgs a) {
+  const int i = blockIdx.x * kScatterThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  // lanes past the batch take part in the wave's run merging with a key no
+  // point can have and nothing to add
+  const bool valid = i < a.n;
+  const int ii = valid ? i : a.n - 1;
+  float p[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(ii) * D + k];
+  const float *row = a.dx + static_cast<size_t>(ii) * a.IN;
+  // the levels of one 16-byte dx load (4 features: 4 / F levels) at a time
+  for (int fq = 0; fq * 4 < a.IN; ++fq) {
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (fq * 4 + 3 < a.IN && (a.IN & 3) == 0) {
+      v = *reinterpret_cast<const f32x4 *>(row + fq * 4);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (fq * 4 + r < a.IN) v[r] = row[fq * 4 + r];
+    }
+#pragma unroll
+    for (int lv = 0; lv < 4 / F; ++lv) {
+      const int l = fq * (4 / F) + lv;
+      if (l * F >= a.IN) break;  // IN = L * F
+      float d[F];
+#pragma unroll
+      for (int f = 0; f < F; ++f) d[f] = v[lv * F + f];
+      scatter_level<D, F>(a, l, p, d, valid, lane);
+    }
+  }
+}
+
+// Level-major variant for large tables: one thread per (point, level),
+// blockIdx.y = level, so the resident blocks work in one level's slice of the
+// table at a time (a 2^22-entry level is 32 MB; all levels together do not
+// stay in the caches).
+template <int D, int F>
+__global__ void __launch_bounds__(kScatterThreads) hash_scatter_level_kernel(ScatterArgs a) {
+  const int l = blockIdx.y;
+  const int i = blockIdx.x * kScatterThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const bool valid = i < a.n;
+  const int ii = valid ? i : a.n - 1;
+  float p[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(ii) * D + k];
+  float d[F];
+  const float *src = a.dx + static_cast<size_t>(ii) * a.IN + l * F;
+  if constexpr (F == 2) {
+    const f32x2 v = *reinterpret_cast<const f32x2 *>(src);
+    d[0] = v[0];
+    d[1] = v[1];
+  } else if constexpr (F == 4) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(src);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) d[f] = v[f];
+  } else {
+    d[0] = src[0];
+  }
+  scatter_level<D, F>(a, l, p, d, valid, lane);
 }
 
 }  // namespace tmnn_hip

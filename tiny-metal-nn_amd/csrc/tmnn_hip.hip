@@ -595,19 +595,29 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
   s.dx = tr->dx.as<float>();
   s.grad_hash = tr->grad_hash.as<int32_t>();
   s.mask = tr->mask[tr->mask_cur].as<uint8_t>();
-  const dim3 grid((n + kScatterThreads - 1) / kScatterThreads, tr->d.num_levels);
+  // point-major while a level's slice of the table is cache-sized, else
+  // level-major (one level's slice at a time)
+  const bool by_level = (static_cast<size_t>(tr->d.features_per_level) * 4u
+                         << tr->d.log2_hashmap_size) > (8u << 20);
+  const dim3 grid((n + kScatterThreads - 1) / kScatterThreads, by_level ? tr->d.num_levels : 1);
   hipStream_t st = tr->ctx->stream;
+#define TMNN_SCATTER(d, f)                                                                   \
+  if (by_level)                                                                              \
+    hipLaunchKernelGGL((hash_scatter_level_kernel<d, f>), grid, dim3(kScatterThreads), 0, st, s); \
+  else                                                                                       \
+    hipLaunchKernelGGL((hash_scatter_kernel<d, f>), grid, dim3(kScatterThreads), 0, st, s);
   switch (tr->d.spatial_dims * 8 + tr->d.features_per_level) {
-    case 2 * 8 + 1: hipLaunchKernelGGL((hash_scatter_kernel<2, 1>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 2 * 8 + 2: hipLaunchKernelGGL((hash_scatter_kernel<2, 2>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 2 * 8 + 4: hipLaunchKernelGGL((hash_scatter_kernel<2, 4>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 3 * 8 + 1: hipLaunchKernelGGL((hash_scatter_kernel<3, 1>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 3 * 8 + 2: hipLaunchKernelGGL((hash_scatter_kernel<3, 2>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 3 * 8 + 4: hipLaunchKernelGGL((hash_scatter_kernel<3, 4>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 4 * 8 + 1: hipLaunchKernelGGL((hash_scatter_kernel<4, 1>), grid, dim3(kScatterThreads), 0, st, s); break;
-    case 4 * 8 + 2: hipLaunchKernelGGL((hash_scatter_kernel<4, 2>), grid, dim3(kScatterThreads), 0, st, s); break;
-    default: hipLaunchKernelGGL((hash_scatter_kernel<4, 4>), grid, dim3(kScatterThreads), 0, st, s); break;
+    case 2 * 8 + 1: TMNN_SCATTER(2, 1) break;
+    case 2 * 8 + 2: TMNN_SCATTER(2, 2) break;
+    case 2 * 8 + 4: TMNN_SCATTER(2, 4) break;
+    case 3 * 8 + 1: TMNN_SCATTER(3, 1) break;
+    case 3 * 8 + 2: TMNN_SCATTER(3, 2) break;
+    case 3 * 8 + 4: TMNN_SCATTER(3, 4) break;
+    case 4 * 8 + 1: TMNN_SCATTER(4, 1) break;
+    case 4 * 8 + 2: TMNN_SCATTER(4, 2) break;
+    default: TMNN_SCATTER(4, 4) break;
   }
+#undef TMNN_SCATTER
   TMNN_HIP_TRY(hipGetLastError());
   return TMNN_OK;
 }
