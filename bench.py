@@ -11,16 +11,22 @@ Workload ("C2"): the image-fit training step.
     bilinearly at 2^18 uniform random coordinates per step;
   * full backward through the MLP and the hash table (int32 fixed-point
     scatter), then the fused Adam pass (lr 1e-2, b1 0.9, b2 0.99, eps 1e-15).
-One step = Morton sort + fused encode/MLP/loss/backward kernel + dW reduction
-+ loss reduction + Adam, all on the library's HIP stream, inputs resident in
-HBM before the timed region starts.
+One step = Morton sort (+ weight-image packing) -> hash-grid encode kernel ->
+MLP train kernel (forward, loss, backward, dW) -> hash-grid scatter kernel ->
+dW / loss reductions -> Adam, all on the library's HIP stream, inputs resident
+in HBM before the timed region starts.
 
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
-fp32, 2^16 points per call), the dominant kernel's roofline fraction (HIP
-event time of the fused kernel inside the timed region) and the CPU
-restatement of the reference math timed on this host.
+fp32, 2^16 points per call), per-kernel roofline fractions (HIP event time of
+each kernel inside the timed region; the slowest one is `roofline`) and the
+CPU restatement of the reference math timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5]
+
+--workload c3/c4/c5 time the other BASELINE training configs (synthetic
+inputs as described in BASELINE.json; the training step and a forward-only
+pass over the same batch, timed separately) and print one JSON line for them;
+the default, c2, is the headline line above.
 """
 from __future__ import annotations
 
@@ -42,6 +48,7 @@ B_TRAIN = 1 << 18
 B_INFER = 1 << 16
 IMG = 1024
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 
 C2_CONFIG = {
     "encoding": {"otype": "HashGrid", "n_levels": 16, "n_features_per_level": 2,
@@ -57,12 +64,162 @@ C2_CONFIG = {
 }
 
 
-def alg_bytes_per_point(d: int, levels: int, feats: int, n_out: int) -> int:
-    """Algorithmic HBM bytes of the fused train kernel per point: position and
-    target reads, the 2^D corner gathers of every level (fp32 features) and the
-    fp32 input-feature gradient it hands to the scatter kernel."""
+def kernel_models(d: int = 2, levels: int = 16, feats: int = 2, n_out: int = 3,
+                  inp: int = 32, hidden: int = 64, n_hidden: int = 2,
+                  hash_params: int = 16 << 16, mlp_params: int = 6467) -> dict:
+    """Algorithmic work of one step's kernels (per point, or per step for
+    Adam), as stated in DESIGN.md:
+      encode   -- position read, 2^D corner gathers of every level (fp32
+                  features), the X tile write (fp32, padded input width);
+      mlp      -- 3 x the forward FLOPs 2 * sum(in * out) (forward, delta chain,
+                  weight gradients; the split-fp16 forward's extra products and
+                  the transposes are overhead, not algorithmic work);
+      scatter  -- position and dx row reads, one F-float int32 update per
+                  corner and level;
+      adam     -- 28 B per parameter (param, m, v read+write, gradient read),
+                  the dense figure; the lazy pass reads a flag per table entry
+                  on top."""
     corners = 1 << d
-    return 4 * d + 4 * n_out + corners * levels * feats * 4 + levels * feats * 4
+    flops = 2 * (inp * hidden + (n_hidden - 1) * hidden * hidden + hidden * n_out)
+    return {
+        "encode": {"bound": "hbm", "per_point": 4 * d + corners * levels * feats * 4 + inp * 4},
+        "mlp": {"bound": "mfma", "per_point": 3 * flops},
+        "scatter": {"bound": "hbm", "per_point": 4 * d + levels * feats * 4 + corners * levels * feats * 4},
+        "adam": {"bound": "hbm", "per_step": 28 * (hash_params + mlp_params) + hash_params // feats},
+    }
+
+
+KERNELS = {  # model key -> (step-profile phase, kernel name in rocprof traces)
+    "encode": ("gpu_encode_us", "encode_features_kernel<2, 2>"),
+    "mlp": ("gpu_fwd_bwd_us", "mlp_train_kernel<64, 32, 2>"),
+    "scatter": ("gpu_scatter_us", "hash_scatter_kernel<2, 2>"),
+    "adam": ("gpu_adam_us", "adam_kernel<2>"),
+}
+
+
+def kernel_rooflines(prof: dict) -> list[dict]:
+    steps = max(1, prof["steps"])
+    out = []
+    for key, model in kernel_models().items():
+        phase, name = KERNELS[key]
+        us = prof[phase] / steps
+        work = model.get("per_point", 0) * B_TRAIN + model.get("per_step", 0)
+        if model["bound"] == "mfma":
+            achieved = work / (us * 1e-6) / 1e12
+            r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4)}
+        else:
+            achieved = work / (us * 1e-6) / 1e9
+            r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
+        r.update({"traffic": traffic_from_profiles(key), "kernel": name,
+                  "kernel_avg_us": round(us, 2), "work_per_launch": work})
+        out.append(r)
+    return out
+
+
+OTHER_WORKLOADS = {
+    # D, levels, feats, log2T, base, scale, hidden, hidden layers, outputs, loss, batch
+    "c3": (3, 16, 2, 19, 16.0, 1.381913, 64, 1, 16, "L2", 1 << 20),
+    "c4": (3, 16, 4, 21, 16.0, 1.5, 64, 3, 1, "L1", 1 << 19),
+    "c5": (4, 16, 2, 22, 8.0, 1.4, 128, 4, 4, "L2", 1 << 20),
+}
+
+
+def workload_batch(torch, which: str, n: int, gen, dev):
+    """Synthetic batch of BASELINE configs[2..4] (seeded):
+    c3 -- 70% of the points from 64 Gaussian blobs (sigma 0.02), 30% uniform in
+          [0,1)^3; target = sum of the blob Gaussians in output 0, zeros in the
+          other 15 (the reference's loss sums every output, so a 16-wide target
+          with the density in channel 0 is the faithful reading);
+    c4 -- 50% within +-0.01 of the union of 8 spheres (r 0.05-0.25), 50% uniform;
+          target = the analytic SDF of the union (L1);
+    c5 -- uniform in [0,1)^4; output c = sum of 16 seeded 4D sinusoids."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    if which == "c3":
+        centers = torch.rand(64, 3, device=dev, generator=g)
+        nb = int(0.7 * n)
+        idx = torch.randint(0, 64, (nb,), device=dev, generator=gen)
+        blob = centers[idx] + 0.02 * torch.randn(nb, 3, device=dev, generator=gen)
+        pos = torch.cat([blob, torch.rand(n - nb, 3, device=dev, generator=gen)]).clamp(0.0, 0.999999)
+        d2 = ((pos[:, None, :] - centers[None, :, :]) ** 2).sum(-1)
+        dens = torch.exp(-d2 / (2 * 0.02 ** 2)).sum(1, keepdim=True)
+        tgt = torch.cat([dens, torch.zeros(n, 15, device=dev)], 1)
+    elif which == "c4":
+        centers = 0.25 + 0.5 * torch.rand(8, 3, device=dev, generator=g)
+        radii = 0.05 + 0.2 * torch.rand(8, device=dev, generator=g)
+        nb = n // 2
+        k = torch.randint(0, 8, (nb,), device=dev, generator=gen)
+        dirs = torch.nn.functional.normalize(torch.randn(nb, 3, device=dev, generator=gen), dim=1)
+        shell = centers[k] + dirs * (radii[k] + 0.02 * torch.rand(nb, 1, device=dev, generator=gen).squeeze(1) - 0.01)[:, None]
+        pos = torch.cat([shell, torch.rand(n - nb, 3, device=dev, generator=gen)]).clamp(0.0, 0.999999)
+        sdf = ((pos[:, None, :] - centers[None]).norm(dim=-1) - radii[None]).amin(1, keepdim=True)
+        tgt = sdf
+    else:
+        pos = torch.rand(n, 4, device=dev, generator=gen)
+        freq = torch.rand(4, 16, 4, device=dev, generator=g) * 8.0 - 4.0
+        phase = torch.rand(4, 16, device=dev, generator=g) * 2 * math.pi
+        tgt = torch.sin(2 * math.pi * torch.einsum("nd,ckd->nck", pos, freq) + phase[None]).sum(-1) / 4.0
+    return pos.contiguous().float(), tgt.contiguous().float()
+
+
+def run_other_workload(args, which: str) -> int:
+    import torch
+    from tiny_metal_nn import Trainer
+    d, levels, feats, log2t, base, scale, hidden, nhl, m, loss, n = OTHER_WORKLOADS[which]
+    dev = torch.device("cuda:0")
+    cfg = {"encoding": {"otype": "HashGrid", "n_levels": levels, "n_features_per_level": feats,
+                        "log2_hashmap_size": log2t, "base_resolution": base,
+                        "per_level_scale": scale},
+           "network": {"otype": "FullyFusedMLP", "n_neurons": hidden, "n_hidden_layers": nhl},
+           "loss": {"otype": loss},
+           "optimizer": {"otype": "Adam", "learning_rate": 1e-2, "beta1": 0.9, "beta2": 0.99,
+                         "epsilon": 1e-15},
+           "weight_init": {"seed": 42}, "batch_size": n,
+           "mi355x": {"precision": "fp16", "hash_adam": "lazy", "morton_sort": True}}
+    gen = torch.Generator(device=dev).manual_seed(7)
+    batches = [workload_batch(torch, which, n, gen, dev) for _ in range(2)]
+    loss_dev = torch.zeros(args.steps + args.warmup + 1, device=dev)
+    tr = Trainer.from_config(cfg, n_input=d, n_output=m)
+    for i in range(args.warmup):
+        x, y = batches[i % 2]
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[i].data_ptr())
+    tr.synchronize()
+    tr.set_training_step_profiling(True)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        x, y = batches[i % 2]
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), n,
+                                loss_dev[args.warmup + i].data_ptr())
+    tr.synchronize()
+    el = time.perf_counter() - t0
+    prof = tr.training_step_profile()
+    out = torch.empty(n, m, device=dev)
+    x = batches[0][0]
+    for _ in range(3):
+        tr.inference_device(x.data_ptr(), out.data_ptr(), n)
+    tr.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        tr.inference_device(x.data_ptr(), out.data_ptr(), n)
+    tr.synchronize()
+    fwd = (time.perf_counter() - t1) / args.steps
+    losses = loss_dev.cpu().numpy()
+    tr.close()
+    steps_prof = max(1, prof["steps"])
+    print(json.dumps({
+        "metric": f"train samples/s ({which}); forward-only samples/s", "value": round(n * args.steps / el, 1),
+        "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(el * 1e3 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16 MFMA / f32 encode+Adam / i32 hash grads",
+        "data": "synthetic (see workload_batch)",
+        "config": {"workload": which, "batch": n, "encoding": f"{d}D L{levels} F{feats} T2^{log2t}",
+                   "mlp": f"{hidden}x{nhl}->{m}", "loss": loss},
+        "forward_samples_per_s": round(n / fwd, 1), "forward_ms": round(fwd * 1e3, 4),
+        "phase_us_per_step": {k: round(prof[k] / steps_prof, 2) for k in prof if k.startswith("gpu_")},
+        "loss_first_last": [round(float(losses[0]), 6),
+                            round(float(losses[args.warmup + args.steps - 1]), 6)]}), flush=True)
+    return 0
 
 
 def make_image(torch, seed: int, device):
@@ -133,15 +290,17 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
                       f"in {el:.1f} s on {threads} host threads (oracle/, -O3, OpenMP)"}
 
 
-def traffic_from_profiles() -> float | None:
-    """HBM bytes per launch of the fused train kernel, from the committed
-    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled
-    by the same counter's reading for a plain copy of known size)."""
-    f = REPO / "profiles" / "field_train_kernel_c2.md"
+def traffic_from_profiles(key: str) -> float | None:
+    """HBM bytes per launch of one kernel of the C2 step, from the committed
+    rocprofv3 PMC summary profiles/c2_step_kernels.md (FETCH_SIZE + WRITE_SIZE
+    per dispatch, each scaled by the same counter's reading for a plain copy
+    of known size)."""
+    f = REPO / "profiles" / "c2_step_kernels.md"
     if not f.exists():
         return None
+    tag = f"traffic_bytes_per_launch[{key}]:"
     for line in f.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(tag):
             try:
                 return float(line.split(":", 1)[1])
             except ValueError:
@@ -156,6 +315,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches): the "
                          "known-size reference for FETCH_SIZE / WRITE_SIZE counters")
@@ -182,6 +342,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
+    if args.workload != "c2":
+        return run_other_workload(args, args.workload)
     dev = torch.device("cuda:0")
     img = make_image(torch, 1234, dev)
     gen = torch.Generator(device=dev).manual_seed(7)
@@ -244,15 +406,8 @@ def main() -> int:
     tr.close()
 
     steps_prof = max(1, prof["steps"])
-    k_us = prof["gpu_fwd_bwd_us"] / steps_prof
-    bpp = alg_bytes_per_point(2, 16, 2, 3)
-    achieved = bpp * B_TRAIN / (k_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": traffic_from_profiles(),
-                "kernel": "field_train_kernel<64,32,fp16>",
-                "kernel_avg_us": round(k_us, 2),
-                "alg_bytes_per_point": bpp}
+    per_kernel = kernel_rooflines(prof)
+    roofline = max(per_kernel, key=lambda r: r["kernel_avg_us"])
     phases = {k: round(prof[k] / steps_prof, 2) for k in
               ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",
                "gpu_adam_us", "gpu_total_us")}
@@ -284,6 +439,7 @@ def main() -> int:
         "phase_us_per_step": phases,
         "loss_first_last": [round(first_loss, 6), round(last_loss, 6)],
         "roofline": roofline,
+        "kernel_rooflines": per_kernel,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -235,7 +235,7 @@ int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding,
 typedef struct tmnn_step_profile {
   uint32_t steps;             /* profiled steps summed below */
   uint32_t batch_size;        /* points of the last profiled step */
-  double gpu_sort_us;         /* Morton codes + radix sort + gather */
+  double gpu_sort_us;         /* Morton codes + radix sort + gather, weight-image packing */
   double gpu_fwd_bwd_us;      /* the MLP kernel: forward, loss, backward to dx */
   double gpu_scatter_us;      /* hash-grid backward scatter + visit flags */
   double gpu_reduce_us;       /* dW partial reduction + loss reduction */

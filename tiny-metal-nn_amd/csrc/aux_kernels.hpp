@@ -70,14 +70,20 @@ __global__ void gather_rows_kernel(const float *src_pos, const float *src_tgt,
                                    const uint32_t *perm, int32_t n,
                                    int32_t pos_dims, int32_t tgt_dims,
                                    float *dst_pos, float *dst_tgt) {
-  const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const size_t s = perm[i];
-  for (int d = 0; d < pos_dims; ++d)
-    dst_pos[static_cast<size_t>(i) * pos_dims + d] = src_pos[s * pos_dims + d];
-  if (src_tgt)
-    for (int d = 0; d < tgt_dims; ++d)
-      dst_tgt[static_cast<size_t>(i) * tgt_dims + d] = src_tgt[s * tgt_dims + d];
+  // one thread per element, elements of a row on consecutive lanes: the
+  // positions [n][pos_dims], then the targets [n][tgt_dims]
+  const size_t e = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t np = static_cast<size_t>(n) * pos_dims;
+  if (e < np) {
+    const size_t i = e / pos_dims, d = e % pos_dims;
+    dst_pos[e] = src_pos[static_cast<size_t>(perm[i]) * pos_dims + d];
+    return;
+  }
+  if (!src_tgt) return;
+  const size_t t = e - np;
+  if (t >= static_cast<size_t>(n) * tgt_dims) return;
+  const size_t i = t / tgt_dims, d = t % tgt_dims;
+  dst_tgt[t] = src_tgt[static_cast<size_t>(perm[i]) * tgt_dims + d];
 }
 
 // grad_mlp[i] += sum over the per-block partial rows partials[b][i].

@@ -1348,6 +1348,9 @@ __global__ void __launch_bounds__(kBlockThreads)
   field_body<HP, INP, F16, true, 0, NHLT, true>(a);
 }
 
+// Forward only (inference, the fp16 forward of the split training API),
+// encoding inline: unsorted inference batches gain nothing from the separate
+// encode pass, and the gathers of the next tile overlap this tile's MLP.
 template <int HP, int INP, bool F16, int DF>
 __global__ void __launch_bounds__(kBlockThreads) field_forward_kernel(FieldArgs a) {
   field_body<HP, INP, F16, false, DF, 0>(a);

@@ -76,8 +76,8 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
   if (D == d && F == f && NHL == nhl) {                                              \
     if (train) return {f16 ? wide_kernel<d, f, nhl, true, true, true>                \
                            : wide_kernel<d, f, nhl, false, true, true>, false, true, true}; \
-    return {f16 ? wide_kernel<d, f, nhl, true, false, false>                         \
-                : wide_kernel<d, f, nhl, false, false, false>, false, true, false};  \
+    return {f16 ? wide_kernel<d, f, nhl, true, false, true>                          \
+                : wide_kernel<d, f, nhl, false, false, true>, false, true, true};    \
   }
   TMNN_WIDE(4, 2, 4)
   TMNN_WIDE(3, 2, 2)
@@ -85,13 +85,24 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
   return {};
 }
 
-// Training kernels read their features from encode_features_kernel; the
-// BASELINE MLP shapes (compile-time hidden-layer count) keep dW in registers,
-// the rest accumulate it in LDS. Forward kernels encode inline, specialised
-// on the BASELINE geometries (compile-time D, F) or on the runtime geometry.
+// Training kernels read their input features from encode_features_kernel:
+// fp16 training of the 64-wide, 32-feature shapes runs mlp_train_kernel, the
+// other BASELINE MLP shapes (compile-time hidden-layer count) keep dW in
+// registers, the rest accumulate it in LDS. Forward kernels encode inline,
+// specialised on the BASELINE geometries (compile-time D, F) or on the
+// runtime geometry; the hidden-128 forward reads X tiles.
 KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL) {
   if (HP == kWideHP) return INP == 32 ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
   const int DF = D * 8 + F;
+#define TMNN_FWD_SPEC(hp, inp, df)                                                   \
+  if (!train && HP == hp && INP == inp && DF == df)                                  \
+    return {f16 ? field_forward_kernel<hp, inp, true, df>                            \
+                : field_forward_kernel<hp, inp, false, df>,                          \
+            false};
+  TMNN_FWD_SPEC(64, 32, 2 * 8 + 2)  // image fit: 2D, 16x2 features
+  TMNN_FWD_SPEC(64, 32, 3 * 8 + 2)  // NeRF density: 3D, 16x2
+  TMNN_FWD_SPEC(64, 64, 3 * 8 + 4)  // SDF: 3D, 16x4
+#undef TMNN_FWD_SPEC
   // fp16 training of the 64-wide, 32-feature shapes: transposes on the matrix
   // cores instead of LDS staging (mlp_kernel.hpp)
   if (train && f16 && HP == 64 && INP == 32 && NHL == 2)
@@ -109,15 +120,7 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
     TMNN_TRAIN_SPEC(64, 64, 3)  // SDF: 16x4, 64x3
 #undef TMNN_TRAIN_SPEC
   }
-#define TMNN_SPEC(hp, inp, df)                                                       \
-  if (!train && HP == hp && INP == inp && DF == df)                                  \
-    return {f16 ? field_forward_kernel<hp, inp, true, df>                            \
-                : field_forward_kernel<hp, inp, false, df>,                          \
-            false};
-  TMNN_SPEC(64, 32, 2 * 8 + 2)  // image fit: 2D, 16x2 features
-  TMNN_SPEC(64, 32, 3 * 8 + 2)  // NeRF density: 3D, 16x2
-  TMNN_SPEC(64, 64, 3 * 8 + 4)  // SDF: 3D, 16x4
-#undef TMNN_SPEC
+
 #define TMNN_SEL(hp, inp)                                                        \
   if (HP == hp && INP == inp) {                                                  \
     if (train)                                                                   \
@@ -460,6 +463,8 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n) {
   EncodeArgs e{};
   e.n = n;
   e.n_pad = (n + kTilePts - 1) / kTilePts * kTilePts;
+  // inference batches are not bounded by the training batch: size here
+  TMNN_HIP_TRY(tr->xfeat.ensure(static_cast<size_t>(e.n_pad) * tr->INP * sizeof(float)));
   e.L = tr->d.num_levels;
   e.KT0 = tr->INP / 16;
   e.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
@@ -573,8 +578,9 @@ int sort_batch(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
   TMNN_HIP_TRY(morton_sort_pairs(tr->sort_tmp.ptr, tr->sort_tmp.bytes, tr->keys0.as<uint32_t>(),
                                  tr->keys1.as<uint32_t>(), tr->vals0.as<uint32_t>(),
                                  tr->vals1.as<uint32_t>(), n, end_bit, st, &sorted_keys, &perm));
-  hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks), dim3(threads), 0, st, d_pos, d_tgt,
-                     perm, n, tr->d.spatial_dims, tgt_dims,
+  const size_t elems = static_cast<size_t>(n) * (tr->d.spatial_dims + (d_tgt ? tgt_dims : 0));
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<uint32_t>((elems + threads - 1) / threads)),
+                     dim3(threads), 0, st, d_pos, d_tgt, perm, n, tr->d.spatial_dims, tgt_dims,
                      tr->s_pos.as<float>(), d_tgt ? tr->s_tgt.as<float>() : nullptr);
   TMNN_HIP_TRY(hipGetLastError());
   *pos_out = tr->s_pos.as<float>();
@@ -632,6 +638,8 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   const uint32_t *perm = nullptr;
   int rc = prof_mark(tr, 0);
   if (rc != TMNN_OK) return rc;
+  // the packed weight image (rebuilt after every Adam step) counts with the sort
+  if ((rc = ensure_image(tr, tr->train_plan)) != TMNN_OK) return rc;
   rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm);
   if (rc != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 1)) != TMNN_OK) return rc;
