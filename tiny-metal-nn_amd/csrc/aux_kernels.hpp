@@ -30,39 +30,12 @@ __global__ void philox_uniform_kernel(float *out, uint32_t count, uint32_t k0,
   }
 }
 
-// Morton code per point (morton_sort.h:14-57): the reference's 10-bit (3D)
-// or 8-bit (4D) quantisation. 2D points are the reference's lifted
-// (x, y, 0); their z bits are all zero, so the code keeps only the x/y
-// interleave (20 bits), which sorts identically.
-__device__ __forceinline__ uint32_t expand_bits_2d(uint32_t v) {
-  v &= 0x3FFu;
-  v = (v | (v << 8)) & 0x00FF00FFu;
-  v = (v | (v << 4)) & 0x0F0F0F0Fu;
-  v = (v | (v << 2)) & 0x33333333u;
-  v = (v | (v << 1)) & 0x55555555u;
-  return v;
-}
-
+// Morton code per point (morton_code in device_common.hpp).
 __global__ void morton_codes_kernel(const float *pos, int32_t n, int32_t dims,
                                     uint32_t *codes) {
   const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float *p = pos + static_cast<size_t>(i) * dims;
-  uint32_t c;
-  if (dims == 4) {
-    c = (expand_bits_4d(morton_quant(p[3], 256.0f, 255.0f)) << 3) |
-        (expand_bits_4d(morton_quant(p[2], 256.0f, 255.0f)) << 2) |
-        (expand_bits_4d(morton_quant(p[1], 256.0f, 255.0f)) << 1) |
-        expand_bits_4d(morton_quant(p[0], 256.0f, 255.0f));
-  } else if (dims == 3) {
-    c = (expand_bits_3d(morton_quant(p[2], 1024.0f, 1023.0f)) << 2) |
-        (expand_bits_3d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
-        expand_bits_3d(morton_quant(p[0], 1024.0f, 1023.0f));
-  } else {
-    c = (expand_bits_2d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
-        expand_bits_2d(morton_quant(p[0], 1024.0f, 1023.0f));
-  }
-  codes[i] = c;
+  codes[i] = morton_code(pos + static_cast<size_t>(i) * dims, dims);
 }
 
 // dst_pos[i] = src_pos[perm[i]], dst_tgt[i] = src_tgt[perm[i]].
@@ -94,8 +67,22 @@ constexpr int kReduceCols = 64;
 constexpr int kReduceGroups = 16;
 __global__ void __launch_bounds__(kReduceCols * kReduceGroups)
     reduce_partials_kernel(const float *partials, int32_t blocks, int32_t count,
-                           float *grad_mlp) {
+                           float *grad_mlp, const float *loss_partials, int32_t n,
+                           float *loss_out) {
   __shared__ float red[kReduceGroups][kReduceCols + 1];
+  // the extra last block (launched when loss_out is set): the step's loss,
+  // sum of the per-block loss partials (fixed lane order) / N
+  if (loss_out && blockIdx.x == gridDim.x - 1) {
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      float t = 0.0f;
+      for (int32_t b = lane; b < blocks; b += 64) t += loss_partials[b];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+      if (lane == 0) *loss_out = n > 0 ? t / static_cast<float>(n) : 0.0f;
+    }
+    return;
+  }
   const int c = threadIdx.x % kReduceCols;
   const int g = threadIdx.x / kReduceCols;
   const int col = blockIdx.x * kReduceCols + c;
@@ -213,18 +200,6 @@ __global__ void zero_bytes_kernel(uint8_t *dst, size_t n) {
   for (size_t i = n16 * 16 + static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += stride)
     dst[i] = 0;
-}
-
-// loss = (sum over block partials) / N, written to *out. One wave: lane l
-// sums partials l, l+64, ... ascending, then a fixed xor-tree across lanes.
-__global__ void loss_reduce_kernel(const float *partials, int32_t blocks, int32_t n,
-                                   float *out) {
-  const int lane = threadIdx.x;
-  float t = 0.0f;
-  for (int32_t b = lane; b < blocks; b += 64) t += partials[b];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
-  if (lane == 0) *out = n > 0 ? t / static_cast<float>(n) : 0.0f;
 }
 
 // Encode-only inspection kernel: thread per (point, level).

@@ -155,4 +155,31 @@ __device__ __forceinline__ uint32_t morton_quant(float v, float scale,
   return static_cast<uint32_t>(fminf(fmaxf(mapped, 0.0f), top));
 }
 
+__device__ __forceinline__ uint32_t expand_bits_2d(uint32_t v) {
+  v &= 0x3FFu;
+  v = (v | (v << 8)) & 0x00FF00FFu;
+  v = (v | (v << 4)) & 0x0F0F0F0Fu;
+  v = (v | (v << 2)) & 0x33333333u;
+  v = (v | (v << 1)) & 0x55555555u;
+  return v;
+}
+
+// Morton code of one point (morton_sort.h:14-57): the reference's 10-bit (3D)
+// or 8-bit (4D) quantisation. 2D points are the reference's lifted
+// (x, y, 0); their z bits are all zero, so the code keeps only the x/y
+// interleave (20 bits), which sorts identically.
+__device__ __forceinline__ uint32_t morton_code(const float *p, int dims) {
+  if (dims == 4)
+    return (expand_bits_4d(morton_quant(p[3], 256.0f, 255.0f)) << 3) |
+           (expand_bits_4d(morton_quant(p[2], 256.0f, 255.0f)) << 2) |
+           (expand_bits_4d(morton_quant(p[1], 256.0f, 255.0f)) << 1) |
+           expand_bits_4d(morton_quant(p[0], 256.0f, 255.0f));
+  if (dims == 3)
+    return (expand_bits_3d(morton_quant(p[2], 1024.0f, 1023.0f)) << 2) |
+           (expand_bits_3d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
+           expand_bits_3d(morton_quant(p[0], 1024.0f, 1023.0f));
+  return (expand_bits_2d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
+         expand_bits_2d(morton_quant(p[0], 1024.0f, 1023.0f));
+}
+
 }  // namespace tmnn_hip

@@ -15,6 +15,11 @@
 // emitHashEncodeUnified, mlp_kernel_emitter.cpp:205-360) -- bit-identical
 // features.
 //
+// With a sort permutation, point i is pos[perm[i]], and the kernel also writes
+// the positions in point (sorted) order for the hash-grid backward (the MLP
+// kernels read targets through the permutation: per-thread row copies here
+// measured slower).
+//
 // Layout of the feature buffer ("X tiles"): point i = 32 t + 16 nt + p and
 // feature f = 16 kt + 4 q + r sit at float offset
 //   ((((t * KT0 + kt) * kNT + nt) * 64 + p + 16 q) * 4 + r,
@@ -35,9 +40,11 @@ struct EncodeArgs {
   int32_t KT0;     // input K tiles (16 features each)
   uint32_t log2T;
   float res[kMaxLevels];
-  const float *pos;    // [n][D]
-  const float *table;  // [L][T][F]
-  float *xfeat;        // X tiles, n_pad * 16 * KT0 floats
+  const float *pos;       // [n][D]
+  const uint32_t *perm;   // nullable: point i is pos[perm[i]] (Morton order)
+  float *pos_out;         // nullable: positions in point order, [n][D]
+  const float *table;     // [L][T][F]
+  float *xfeat;           // X tiles, n_pad * 16 * KT0 floats
 };
 
 constexpr int kEncodeThreads = 256;
@@ -58,8 +65,12 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeA
   if (i >= a.n_pad) return;
   const bool valid = i < a.n;
   float p[D];
+  const size_t src = valid ? (a.perm ? a.perm[i] : static_cast<uint32_t>(i)) : 0u;
 #pragma unroll
-  for (int k = 0; k < D; ++k) p[k] = valid ? a.pos[static_cast<size_t>(i) * D + k] : 0.0f;
+  for (int k = 0; k < D; ++k) p[k] = valid ? a.pos[src * D + k] : 0.0f;
+  if (a.pos_out && valid)
+#pragma unroll
+    for (int k = 0; k < D; ++k) a.pos_out[static_cast<size_t>(i) * D + k] = p[k];
   const uint32_t tmask = (1u << a.log2T) - 1u;
   const int nquads = 4 * a.KT0;
   for (int q0 = 0; q0 < nquads; q0 += QG) {

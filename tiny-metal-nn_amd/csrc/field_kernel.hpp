@@ -65,6 +65,7 @@ struct FieldArgs {
   const float *pos;         // [n][D]
   const float *xfeat;       // input features as X tiles (encode_kernel.hpp), XMEM kernels
   const float *target;      // [n][M] target (TrainLoss) or d_out (TrainExtGrad)
+  const uint32_t *tgt_index;// nullable: point i's target row is tgt_index[i]
   const float *table;       // [L][T][F] fp32
   const float *mlp;         // fp32 master MLP params (reference layout)
   const unsigned char *image; // packed LDS head (pack_image_kernel), s.dw_off bytes
@@ -1065,7 +1066,10 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       for (int r = 0; r < 4; ++r) {
         const int o = 4 * q + r;
         Tv[nt][r] = (TRAIN && a.mode != kModeInputGrad && valid[nt] && o < a.M)
-                        ? a.target[static_cast<size_t>(pt[nt]) * a.M + o] : 0.0f;
+                        ? a.target[static_cast<size_t>(a.tgt_index ? a.tgt_index[pt[nt]]
+                                                                   : static_cast<uint32_t>(pt[nt])) *
+                                       a.M + o]
+                        : 0.0f;
       }
     if constexpr (TRAIN) store_tiles<F16, KT0>(Xs, X, p, q);
 

@@ -267,7 +267,8 @@ __global__ void __launch_bounds__(kMlpWaves * 64)
     if (has_target) {
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) {
-        const size_t row = static_cast<size_t>(valid[nt] ? pt[nt] : 0) * a.M;
+        const uint32_t pr = valid[nt] ? static_cast<uint32_t>(pt[nt]) : 0u;
+        const size_t row = static_cast<size_t>(a.tgt_index ? a.tgt_index[pr] : pr) * a.M;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int o = 4 * q + r;

@@ -13,15 +13,16 @@
 // of a corner is its z = 0 entry XOR (805459861 mod T) within the level).
 //
 // Lanes of a wave hold consecutive Morton-sorted points of one level; runs of
-// lanes that hit the same entry are summed across lanes first and issue one
-// atomic (and one flag store) per run.
+// lanes that hit the same entry are summed across lanes first (int32 sums per
+// feature) and issue one atomic (and one flag store) per run.
 //
 // F == 2 packs both features of an entry into one 64-bit atomic:
 //   S += (int64)c1 * 2^32 + (int64)c0   (c0 sign-extended)
 // The low word is then exactly the int32 (wrapping) sum of c0, the high word
 // the sum of c1 minus one when that low sum is negative. Readers restore
 // feature 1 as hi + (lo < 0), exact whenever the true sum of c0 stays in
-// int32 range (|gradient| < 32768), as the reference's own sum must.
+// int32 range (|gradient| < 32768), as the reference's own sum must (and so
+// does each wave-merged run's partial sum, a subset of it).
 #pragma once
 
 #include "device_common.hpp"
@@ -51,27 +52,46 @@ __host__ __device__ inline int32_t unpack_hi(int32_t lo, int32_t hi) {
   return static_cast<int32_t>(static_cast<uint32_t>(hi) + (lo < 0 ? 1u : 0u));
 }
 
-// Sum of v over the run of equal keys that ends at this lane (runs are
-// maximal sequences of equal keys in lane order); is_tail is set on the last
-// lane of each run, which then owns the run's total. Integer sums are exact
-// in any order, so merging lanes leaves the table gradients bit-identical.
-__device__ __forceinline__ int64_t run_sum(uint32_t key, int64_t v, int lane, bool *is_tail) {
+// Inclusive prefix sum of v over the 64 lanes of the wave (wrapping int32),
+// on DPP lane shifts only: row_shr 1, 2, 4, 8 inside each 16-lane row, then
+// row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then lanes
+// 0..31's total into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ int32_t wave_incl_sum(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
+// Sums of c[0..N) over the run of equal keys that ends at this lane (runs are
+// maximal sequences of equal keys in lane order); *is_tail is set on the last
+// lane of each run, which then owns the run's totals. A run total is the
+// wave prefix sum at its tail minus the prefix sum just before its head;
+// int32 sums wrap, so the totals are exact modulo 2^32 in any order, like the
+// int32 atomics they feed.
+template <int N>
+__device__ __forceinline__ void run_sums(uint32_t key, int32_t (&c)[N], int lane, bool *is_tail) {
   const uint32_t prev = __shfl_up(key, 1);
   const bool head = lane == 0 || prev != key;
   const uint64_t heads = __ballot(head);
   if (heads == ~0ull) {  // no two neighbours share an entry
     *is_tail = true;
-    return v;
+    return;
   }
   const uint64_t le = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
   const int start = 63 - __clzll(heads & le);  // first lane of this lane's run
+  const int src = start > 0 ? start - 1 : 0;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int64_t up = __shfl_up(v, off);
-    if (lane - off >= start) v += up;
+  for (int f = 0; f < N; ++f) {
+    const int32_t incl = wave_incl_sum(c[f]);
+    const int32_t before = __shfl(incl, src);
+    c[f] = static_cast<int32_t>(static_cast<uint32_t>(incl) -
+                                (start > 0 ? static_cast<uint32_t>(before) : 0u));
   }
   *is_tail = lane == 63 || ((heads >> (lane + 1)) & 1ull);
-  return v;
 }
 
 // One thread per point, all levels in turn: the thread reads its dx row with
@@ -107,28 +127,22 @@ __device__ __forceinline__ void scatter_level(const ScatterArgs &a, int l, const
       ci[f] = valid ? f2i_trunc(v * kGradScale) : 0;
     }
     bool tail = true;
-    if constexpr (F == 2) {
-      // packed pair (see the file comment); merged over runs of equal entries
-      int64_t v64 = static_cast<int64_t>(
-          (static_cast<uint64_t>(static_cast<uint32_t>(ci[1])) << 32) +
-          static_cast<uint64_t>(static_cast<int64_t>(ci[0])));
-      v64 = run_sum(local, v64, lane, &tail);
-      if (valid && tail) {
+    run_sums<F>(local, ci, lane, &tail);
+    if (valid && tail) {
+      if constexpr (F == 2) {
+        // packed pair (see the file comment)
+        const int64_t v64 = static_cast<int64_t>(
+            (static_cast<uint64_t>(static_cast<uint32_t>(ci[1])) << 32) +
+            static_cast<uint64_t>(static_cast<int64_t>(ci[0])));
         if (v64 != 0)
           atomicAdd(reinterpret_cast<unsigned long long *>(a.grad_hash + entry * 2),
                     static_cast<unsigned long long>(v64));
-        mark_entry(a.mask, entry);
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int f = 0; f < F; ++f) {
-        bool t;
-        const int64_t sum = run_sum(local, ci[f], lane, &t);
-        tail = t;
-        if (valid && t && sum != 0)
-          atomicAdd(a.grad_hash + entry * F + f, static_cast<int32_t>(sum));
+        for (int f = 0; f < F; ++f)
+          if (ci[f] != 0) atomicAdd(a.grad_hash + entry * F + f, ci[f]);
       }
-      if (valid && tail) mark_entry(a.mask, entry);
+      mark_entry(a.mask, entry);
     }
   }
 }

@@ -1,10 +1,12 @@
-// sort.hip -- stable LSD radix sort of (Morton code, point index) pairs on the
+// sort.hip -- stable LSD radix sort of the batch by Morton code on the
 // trainer's stream, replacing the reference's per-step host std::sort
 // (src/tiny_metal_nn/runtime/morton_sort.h:60-110).
 //
-// 8-bit digits, ceil(end_bit / 8) passes, three kernels per pass:
+// RB-bit digits (10 for 2D's 20-bit codes: 2 passes; 8 for 3D's 30-bit and
+// 4D's 32-bit codes: 4 passes), three kernels per pass:
 //   hist   -- each block counts the digits of its 1024-key chunk (LDS atomics)
-//             into hist[digit][block];
+//             into hist[digit][block]; the first pass computes the Morton
+//             codes from the positions itself;
 //   scan   -- one block per digit: exclusive prefix of the digit's counts over
 //             the blocks, and the digit total;
 //   scatter-- each block ranks its chunk stably (wave ballots for the rank
@@ -16,33 +18,15 @@
 
 #include <algorithm>
 
+#include "device_common.hpp"
+
 namespace tmnn_hip {
 namespace {
 
-constexpr int kBins = 256;
 constexpr int kSortThreads = 256;
 constexpr int kKeysPerThread = 4;
 constexpr int kChunk = kSortThreads * kKeysPerThread;  // keys per block
 constexpr int kSortWaves = kSortThreads / 64;
-
-__device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift) {
-  return (key >> shift) & (kBins - 1);
-}
-
-__global__ void __launch_bounds__(kSortThreads)
-    radix_hist_kernel(const uint32_t *keys, int n, int shift, int blocks, uint32_t *hist) {
-  __shared__ uint32_t cnt[kBins];
-  cnt[threadIdx.x] = 0u;
-  __syncthreads();
-  const int base = blockIdx.x * kChunk;
-#pragma unroll 4
-  for (int r = 0; r < kKeysPerThread; ++r) {
-    const int i = base + r * kSortThreads + static_cast<int>(threadIdx.x);
-    if (i < n) atomicAdd(&cnt[digit_of(keys[i], shift)], 1u);
-  }
-  __syncthreads();
-  hist[threadIdx.x * blocks + blockIdx.x] = cnt[threadIdx.x];
-}
 
 // Inclusive scan of v over the 64 lanes of a wave.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
@@ -73,6 +57,42 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum,
   return before + inc - v;
 }
 
+// key of chunk-local element li: the Morton code of the position (first
+// pass) or the previous pass's output
+template <bool FIRST>
+__device__ __forceinline__ uint32_t load_key(const uint32_t *keys, const float *pos, int dims,
+                                             size_t i) {
+  if constexpr (FIRST) return morton_code(pos + i * dims, dims);
+  return keys[i];
+}
+
+template <int RB, bool FIRST>
+__global__ void __launch_bounds__(kSortThreads)
+    radix_hist_kernel(const uint32_t *keys, const float *pos, int dims, int n, int shift,
+                      int blocks, uint32_t *hist) {
+  constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
+  __shared__ uint32_t cnt[kBins];
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) cnt[t + kSortThreads * j] = 0u;
+  __syncthreads();
+  const int base = blockIdx.x * kChunk;
+#pragma unroll
+  for (int r = 0; r < kKeysPerThread; ++r) {
+    const int i = base + r * kSortThreads + t;
+    if (i < n) {
+      const uint32_t key = load_key<FIRST>(keys, pos, dims, static_cast<size_t>(i));
+      atomicAdd(&cnt[(key >> shift) & (kBins - 1)], 1u);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    const int d = t + kSortThreads * j;
+    hist[static_cast<size_t>(d) * blocks + blockIdx.x] = cnt[d];
+  }
+}
+
 // Row d of hist (the G per-block counts of digit d, contiguous): exclusive
 // prefix over blocks into pre[d][*], the digit's total into totals[d].
 // One block per digit; thread t owns blocks [t*k, (t+1)*k).
@@ -99,32 +119,51 @@ __global__ void __launch_bounds__(kSortThreads)
   if (t == 0) totals[d] = total;
 }
 
+template <int RB, bool FIRST>
 __global__ void __launch_bounds__(kSortThreads)
-    radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, int n, int shift,
-                         int blocks, const uint32_t *hist, const uint32_t *pre,
-                         const uint32_t *totals, uint32_t *keys_out, uint32_t *vals_out) {
+    radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const float *pos,
+                         int dims, int n, int shift, int blocks, const uint32_t *hist,
+                         const uint32_t *pre, const uint32_t *totals, uint32_t *keys_out,
+                         uint32_t *vals_out) {
+  constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
   __shared__ uint32_t s_keys[kChunk];
   __shared__ uint32_t s_vals[kChunk];
   __shared__ uint32_t glob[kBins];     // global start of this block's digit run
   __shared__ uint32_t local[kBins];    // start of the digit run within the chunk
   __shared__ uint32_t running[kBins];  // keys of each digit placed so far
-  __shared__ uint32_t wcnt[kSortWaves][kBins];
+  __shared__ uint16_t wcnt[kSortWaves][kBins];  // per-wave counts, then offsets (< kChunk)
+  __shared__ uint32_t wsum[kSortWaves];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   const int base = blockIdx.x * kChunk;
   const int nblk = std::min(kChunk, n - base);
 
-  __shared__ uint32_t wsum[kSortWaves];
-  // global start of each digit (exclusive scan of the digit totals) plus this
-  // block's prefix within the digit; chunk-local starts from its own counts
+  // thread t owns digits [t*BPT, (t+1)*BPT): global start of each digit
+  // (exclusive scan of the digit totals) plus this block's prefix within the
+  // digit; chunk-local starts from the block's own counts
   {
+    uint32_t tot[BPT], cnt[BPT], st = 0, sc = 0;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int d = t * BPT + j;
+      tot[j] = totals[d];
+      cnt[j] = hist[static_cast<size_t>(d) * blocks + blockIdx.x];
+      st += tot[j];
+      sc += cnt[j];
+    }
     uint32_t all = 0;
-    const uint32_t digit_base = block_excl_scan(totals[t], wsum, &all);
-    glob[t] = digit_base + pre[t * blocks + blockIdx.x];
-    const uint32_t count = hist[t * blocks + blockIdx.x];
-    local[t] = block_excl_scan(count, wsum, &all);
-    running[t] = 0u;
+    uint32_t gb = block_excl_scan(st, wsum, &all);
+    uint32_t lb = block_excl_scan(sc, wsum, &all);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int d = t * BPT + j;
+      glob[d] = gb + pre[static_cast<size_t>(d) * blocks + blockIdx.x];
+      local[d] = lb;
+      running[d] = 0u;
+      gb += tot[j];
+      lb += cnt[j];
+    }
   }
   __syncthreads();
 
@@ -132,14 +171,15 @@ __global__ void __launch_bounds__(kSortThreads)
   for (int r = 0; r < kKeysPerThread; ++r) {
     const int li = r * kSortThreads + t;  // chunk-local index (input order)
     const bool valid = li < nblk;
-    const uint32_t key = valid ? keys_in[base + li] : 0u;
-    const uint32_t val = valid ? (vals_in ? vals_in[base + li] : static_cast<uint32_t>(base + li))
+    const uint32_t key = valid ? load_key<FIRST>(keys_in, pos, dims, static_cast<size_t>(base + li))
                                : 0u;
-    const uint32_t d = digit_of(key, shift);
+    const uint32_t val =
+        valid ? (FIRST ? static_cast<uint32_t>(base + li) : vals_in[base + li]) : 0u;
+    const uint32_t d = (key >> shift) & (kBins - 1);
     // lanes of this wave holding the same digit
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < RB; ++b) {
       const bool bit = (d >> b) & 1u;
       const uint64_t m = __ballot(bit);
       peers &= bit ? m : ~m;
@@ -147,26 +187,30 @@ __global__ void __launch_bounds__(kSortThreads)
     const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt_mask));
     const bool leader = valid && rank == 0u;
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) wcnt[w][t] = 0u;
+    for (int w = 0; w < kSortWaves; ++w)
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) wcnt[w][t * BPT + j] = 0;
     __syncthreads();
-    if (leader) wcnt[wave][d] = static_cast<uint32_t>(__popcll(peers));
+    if (leader) wcnt[wave][d] = static_cast<uint16_t>(__popcll(peers));
     __syncthreads();
-    // per digit t: exclusive offsets across waves, then advance the run
-    {
-      uint32_t acc = running[t];
+    // per digit: exclusive offsets across waves, then advance the run
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int dd = t * BPT + j;
+      uint32_t acc = running[dd];
 #pragma unroll
       for (int w = 0; w < kSortWaves; ++w) {
-        const uint32_t c = wcnt[w][t];
-        wcnt[w][t] = acc;
+        const uint32_t c = wcnt[w][dd];
+        wcnt[w][dd] = static_cast<uint16_t>(acc);
         acc += c;
       }
-      running[t] = acc;
+      running[dd] = acc;
     }
     __syncthreads();
     if (valid) {
-      const uint32_t pos = local[d] + wcnt[wave][d] + rank;
-      s_keys[pos] = key;
-      s_vals[pos] = val;
+      const uint32_t p = local[d] + wcnt[wave][d] + rank;
+      s_keys[p] = key;
+      s_vals[p] = val;
     }
     __syncthreads();
   }
@@ -175,7 +219,7 @@ __global__ void __launch_bounds__(kSortThreads)
   // s_keys[j]; its global slot is glob[d] + (j - local[d]).
   for (int j = t; j < nblk; j += kSortThreads) {
     const uint32_t key = s_keys[j];
-    const uint32_t d = digit_of(key, shift);
+    const uint32_t d = (key >> shift) & (kBins - 1);
     const uint32_t dst = glob[d] + (static_cast<uint32_t>(j) - local[d]);
     keys_out[dst] = key;
     vals_out[dst] = s_vals[j];
@@ -184,37 +228,40 @@ __global__ void __launch_bounds__(kSortThreads)
 
 int sort_blocks(int n) { return (n + kChunk - 1) / kChunk; }
 
-}  // namespace
+// digit width per code width: two 10-bit passes for 2D's 20-bit codes; 8-bit
+// digits (4 passes) for 3D/4D, where wider digits measured slower per pass
+// than the pass they save
+int digit_bits(int end_bit) { return end_bit == 20 ? 10 : 8; }
 
-hipError_t morton_sort_temp_bytes(int n, size_t *bytes) {
-  // hist[kBins][G] + pre[kBins][G] + totals[kBins]
-  *bytes = (2 * static_cast<size_t>(kBins) * std::max(1, sort_blocks(n)) + kBins) *
-           sizeof(uint32_t);
-  return hipSuccess;
-}
-
-hipError_t morton_sort_pairs(void *tmp, size_t tmp_bytes, uint32_t *keys0, uint32_t *keys1,
-                             uint32_t *vals0, uint32_t *vals1, int n, int end_bit,
-                             hipStream_t stream, const uint32_t **keys_sorted,
-                             const uint32_t **vals_sorted) {
+template <int RB>
+hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const float *pos,
+                      int dims, uint32_t *keys0, uint32_t *keys1, uint32_t *vals0,
+                      uint32_t *vals1, int n, int end_bit, hipStream_t stream,
+                      const uint32_t **keys_sorted, const uint32_t **vals_sorted) {
   const int blocks = sort_blocks(n);
-  size_t need = 0;
-  morton_sort_temp_bytes(n, &need);
-  if (n <= 0 || tmp_bytes < need) return hipErrorInvalidValue;
-  uint32_t *hist = static_cast<uint32_t *>(tmp);
-  uint32_t *pre = hist + static_cast<size_t>(kBins) * blocks;
-  uint32_t *totals = pre + static_cast<size_t>(kBins) * blocks;
   uint32_t *kin = keys0, *kout = keys1, *vin = nullptr, *vout = vals1;
   uint32_t *vspare = vals0;
-  const int passes = std::max(1, (end_bit + 7) / 8);
+  const int passes = std::max(1, (end_bit + RB - 1) / RB);
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = 8 * pass;
-    hipLaunchKernelGGL(radix_hist_kernel, dim3(blocks), dim3(kSortThreads), 0, stream, kin, n,
-                       shift, blocks, hist);
-    hipLaunchKernelGGL(radix_scan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist,
+    const int shift = RB * pass;
+    if (pass == 0) {
+      hipLaunchKernelGGL((radix_hist_kernel<RB, true>), dim3(blocks), dim3(kSortThreads), 0, stream,
+                         nullptr, pos, dims, n, shift, blocks, hist);
+    } else {
+      hipLaunchKernelGGL((radix_hist_kernel<RB, false>), dim3(blocks), dim3(kSortThreads), 0,
+                         stream, kin, nullptr, dims, n, shift, blocks, hist);
+    }
+    hipLaunchKernelGGL(radix_scan_kernel, dim3(1 << RB), dim3(kSortThreads), 0, stream, hist,
                        blocks, pre, totals);
-    hipLaunchKernelGGL(radix_scatter_kernel, dim3(blocks), dim3(kSortThreads), 0, stream, kin,
-                       vin, n, shift, blocks, hist, pre, totals, kout, vout);
+    if (pass == 0) {
+      hipLaunchKernelGGL((radix_scatter_kernel<RB, true>), dim3(blocks), dim3(kSortThreads), 0,
+                         stream, nullptr, nullptr, pos, dims, n, shift, blocks, hist, pre, totals,
+                         kout, vout);
+    } else {
+      hipLaunchKernelGGL((radix_scatter_kernel<RB, false>), dim3(blocks), dim3(kSortThreads), 0,
+                         stream, kin, vin, nullptr, dims, n, shift, blocks, hist, pre, totals,
+                         kout, vout);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // next pass reads what this one wrote
@@ -226,6 +273,37 @@ hipError_t morton_sort_pairs(void *tmp, size_t tmp_bytes, uint32_t *keys0, uint3
   *keys_sorted = kin;
   *vals_sorted = vin;
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t morton_sort_temp_bytes(int n, size_t *bytes) {
+  // hist[kBins][G] + pre[kBins][G] + totals[kBins] at the widest digit
+  const size_t bins = size_t(1) << 10;
+  *bytes = (2 * bins * std::max(1, sort_blocks(n)) + bins) * sizeof(uint32_t);
+  return hipSuccess;
+}
+
+hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int dims,
+                             uint32_t *keys0, uint32_t *keys1, uint32_t *vals0, uint32_t *vals1,
+                             int n, hipStream_t stream, const uint32_t **keys_sorted,
+                             const uint32_t **vals_sorted) {
+  size_t need = 0;
+  morton_sort_temp_bytes(n, &need);
+  if (n <= 0 || tmp_bytes < need || dims < 2 || dims > 4) return hipErrorInvalidValue;
+  // 2D codes interleave x and y only (the lifted z = 0 bits are all zero,
+  // which leaves the order unchanged): 20 bits; 3D 30 bits; 4D 32 bits.
+  const int end_bit = dims == 2 ? 20 : (dims == 3 ? 30 : 32);
+  const int blocks = sort_blocks(n);
+  const size_t bins = size_t(1) << digit_bits(end_bit);
+  uint32_t *hist = static_cast<uint32_t *>(tmp);
+  uint32_t *pre = hist + bins * blocks;
+  uint32_t *totals = pre + bins * blocks;
+  if (digit_bits(end_bit) == 8)
+    return run_passes<8>(hist, pre, totals, pos, dims, keys0, keys1, vals0, vals1, n, end_bit,
+                         stream, keys_sorted, vals_sorted);
+  return run_passes<10>(hist, pre, totals, pos, dims, keys0, keys1, vals0, vals1, n, end_bit,
+                        stream, keys_sorted, vals_sorted);
 }
 
 }  // namespace tmnn_hip

@@ -458,8 +458,10 @@ int ensure_image(tmnn_trainer *tr, KernelPlan &plan) {
   return TMNN_OK;
 }
 
-// Input features of n points at pos as X tiles in tr->xfeat.
-int launch_encode(tmnn_trainer *tr, const float *pos, int n) {
+// Input features of n points at pos as X tiles in tr->xfeat; with perm,
+// point i is pos[perm[i]] and its position is also written to pos_out[i].
+int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *perm = nullptr,
+                  float *pos_out = nullptr) {
   EncodeArgs e{};
   e.n = n;
   e.n_pad = (n + kTilePts - 1) / kTilePts * kTilePts;
@@ -470,6 +472,8 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n) {
   e.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
   for (int l = 0; l < kMaxLevels; ++l) e.res[l] = tr->res[l];
   e.pos = pos;
+  e.perm = perm;
+  e.pos_out = pos_out;
   e.table = tr->params.as<float>();
   e.xfeat = tr->xfeat.as<float>();
   const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads);
@@ -493,11 +497,12 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n) {
 // into tr->xfeat (unless reuse_x: the features of these points are there
 // already), with profile mark prof_after_encode (if >= 0) in between.
 int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
-                 int prof_after_encode = -1, bool reuse_x = false) {
+                 int prof_after_encode = -1, bool reuse_x = false,
+                 const uint32_t *perm = nullptr, float *pos_out = nullptr) {
   int rc = ensure_image(tr, plan);
   if (rc != TMNN_OK) return rc;
   if (plan.xmem) {
-    if (!reuse_x && (rc = launch_encode(tr, a.pos, n)) != TMNN_OK) return rc;
+    if (!reuse_x && (rc = launch_encode(tr, a.pos, n, perm, pos_out)) != TMNN_OK) return rc;
     a.xfeat = tr->xfeat.as<float>();
   }
   if (prof_after_encode >= 0 && (rc = prof_mark(tr, prof_after_encode)) != TMNN_OK) return rc;
@@ -555,11 +560,13 @@ int ensure_batch(tmnn_trainer *tr, int n) {
   return TMNN_OK;
 }
 
-// Sorted copies of (pos, tgt) into s_pos / s_tgt; returns the permutation
-// (sorted i -> original row) or nullptr when sorting is off.
+// Morton order of the batch: returns the permutation (sorted i -> original
+// row), or nullptr when sorting is off. With gather, also the sorted copies
+// of (pos, tgt) in s_pos / s_tgt (else *pos_out / *tgt_out are the inputs:
+// the training path reads them through the permutation).
 int sort_batch(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
                int tgt_dims, int n, const float **pos_out,
-               const float **tgt_out, const uint32_t **perm_out) {
+               const float **tgt_out, const uint32_t **perm_out, bool gather = true) {
   hipStream_t st = tr->ctx->stream;
   if (!tr->d.morton_sort || n <= 1) {
     *pos_out = d_pos;
@@ -567,17 +574,18 @@ int sort_batch(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
     *perm_out = nullptr;
     return TMNN_OK;
   }
-  const int threads = 256, blocks = (n + threads - 1) / threads;
-  hipLaunchKernelGGL(morton_codes_kernel, dim3(blocks), dim3(threads), 0, st, d_pos, n,
-                     tr->d.spatial_dims, tr->keys0.as<uint32_t>());
-  TMNN_HIP_TRY(hipGetLastError());
-  // 2D codes interleave x and y only (the lifted z = 0 bits are all zero,
-  // which leaves the order unchanged): 20 bits; 3D 30 bits; 4D 32 bits.
-  const int end_bit = tr->d.spatial_dims == 2 ? 20 : (tr->d.spatial_dims == 3 ? 30 : 32);
+  const int threads = 256;
   const uint32_t *sorted_keys = nullptr, *perm = nullptr;
-  TMNN_HIP_TRY(morton_sort_pairs(tr->sort_tmp.ptr, tr->sort_tmp.bytes, tr->keys0.as<uint32_t>(),
-                                 tr->keys1.as<uint32_t>(), tr->vals0.as<uint32_t>(),
-                                 tr->vals1.as<uint32_t>(), n, end_bit, st, &sorted_keys, &perm));
+  TMNN_HIP_TRY(morton_sort_batch(tr->sort_tmp.ptr, tr->sort_tmp.bytes, d_pos, tr->d.spatial_dims,
+                                 tr->keys0.as<uint32_t>(), tr->keys1.as<uint32_t>(),
+                                 tr->vals0.as<uint32_t>(), tr->vals1.as<uint32_t>(), n, st,
+                                 &sorted_keys, &perm));
+  if (!gather) {
+    *pos_out = d_pos;
+    *tgt_out = d_tgt;
+    *perm_out = perm;
+    return TMNN_OK;
+  }
   const size_t elems = static_cast<size_t>(n) * (tr->d.spatial_dims + (d_tgt ? tgt_dims : 0));
   hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<uint32_t>((elems + threads - 1) / threads)),
                      dim3(threads), 0, st, d_pos, d_tgt, perm, n, tr->d.spatial_dims, tgt_dims,
@@ -632,7 +640,7 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
 // accumulated into grad_hash / grad_mlp / mask. Returns the block count used
 // (for the loss reduction) or a negative status.
 int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
-                         int n, bool external_grad) {
+                         int n, bool external_grad, float *d_loss = nullptr) {
   const bool f16 = tr->d.precision == TMNN_PRECISION_FP16;
   const float *pos = d_pos, *tgt = d_tgt;
   const uint32_t *perm = nullptr;
@@ -640,7 +648,8 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   if (rc != TMNN_OK) return rc;
   // the packed weight image (rebuilt after every Adam step) counts with the sort
   if ((rc = ensure_image(tr, tr->train_plan)) != TMNN_OK) return rc;
-  rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm);
+  rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm,
+                  !tr->train_plan.xmem);
   if (rc != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 1)) != TMNN_OK) return rc;
   FieldArgs a = base_args(tr);
@@ -650,18 +659,25 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   a.inv_loss_scale = 1.0f / a.loss_scale;
   a.pos = pos;
   a.target = tgt;
+  // feature-tile plans read the batch through the permutation: the encode
+  // kernel writes the sorted positions (for the scatter), targets are indexed
+  const bool indexed = tr->train_plan.xmem && perm != nullptr;
+  a.tgt_index = indexed ? perm : nullptr;
+  float *sorted_pos = indexed ? tr->s_pos.as<float>() : nullptr;
   a.grad_partials = tr->partials.as<float>();
   a.loss_partials = tr->loss_partials.as<float>();
   a.dx_out = tr->dx.as<float>();
-  const int blocks = launch_field(tr, tr->train_plan, a, n, 2);
+  const int blocks = launch_field(tr, tr->train_plan, a, n, 2, false, a.tgt_index, sorted_pos);
   if (blocks < 0) return blocks;
   if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
-  if ((rc = launch_scatter(tr, pos, n)) != TMNN_OK) return rc;
+  if ((rc = launch_scatter(tr, indexed ? sorted_pos : pos, n)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((tr->mlp_count + kReduceCols - 1) / kReduceCols),
-                     dim3(kReduceCols * kReduceGroups), 0,
+  // dW rows, plus (training steps) the loss in one extra block
+  const uint32_t rblocks = (tr->mlp_count + kReduceCols - 1) / kReduceCols + (d_loss ? 1 : 0);
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3(rblocks), dim3(kReduceCols * kReduceGroups), 0,
                      tr->ctx->stream, tr->partials.as<float>(), blocks,
-                     static_cast<int32_t>(tr->mlp_count), tr->grad_mlp.as<float>());
+                     static_cast<int32_t>(tr->mlp_count), tr->grad_mlp.as<float>(),
+                     tr->loss_partials.as<float>(), n, d_loss);
   TMNN_HIP_TRY(hipGetLastError());
   return blocks;
 }
@@ -725,12 +741,9 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
                       float *d_loss) {
   int rc = prof_begin_step(tr);
   if (rc != TMNN_OK) return rc;
-  const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false);
+  const int blocks =
+      run_forward_backward(tr, d_pos, d_tgt, n, false, d_loss ? d_loss : tr->loss_out.as<float>());
   if (blocks < 0) return blocks;
-  hipLaunchKernelGGL(loss_reduce_kernel, dim3(1), dim3(64), 0, tr->ctx->stream,
-                     tr->loss_partials.as<float>(), blocks, n,
-                     d_loss ? d_loss : tr->loss_out.as<float>());
-  TMNN_HIP_TRY(hipGetLastError());
   if ((rc = prof_mark(tr, 5)) != TMNN_OK) return rc;
   if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 6)) != TMNN_OK) return rc;

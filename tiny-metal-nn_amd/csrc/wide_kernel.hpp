@@ -201,7 +201,10 @@ __global__ void __launch_bounds__(kWideWaves * 64)
       for (int r = 0; r < 4; ++r) {
         const int o = 4 * q + r;
         Tv[nt][r] = (TRAIN && a.mode != kModeInputGrad && valid[nt] && o < a.M)
-                        ? a.target[static_cast<size_t>(pt[nt]) * a.M + o] : 0.0f;
+                        ? a.target[static_cast<size_t>(a.tgt_index ? a.tgt_index[pt[nt]]
+                                                                   : static_cast<uint32_t>(pt[nt])) *
+                                       a.M + o]
+                        : 0.0f;
       }
     }
     f32x4 X[KT0][kNT];
