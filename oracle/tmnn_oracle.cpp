@@ -223,7 +223,8 @@ void forward_point(const Geo &g, const Offsets &o, const float *res,
 // Loss and output gradient of one point (emitLoss, mlp_kernel_emitter.cpp:562-670).
 // RelativeL2 is not in the reference: it follows tcnn's published definition
 // r^2 / (y^2 + 0.01) with the denominator held constant in the gradient,
-// summed over outputs and divided by N like the reference's L2.
+// summed over outputs and divided by N like the reference's L2; one division
+// per element (inv = 1 / den, then products), as the GPU kernels compute it.
 float loss_point(const orc_model *m, const Geo &g, const float *out,
                  const float *tgt, float inv_n, float *d_out) {
   float loss = 0.0f;
@@ -268,8 +269,9 @@ float loss_point(const orc_model *m, const Geo &g, const float *out,
       }
       case ORC_RELATIVE_L2: {
         const float den = out[k] * out[k] + 0.01f;
-        term = (r * r) / den;
-        d = ((2.0f * r) / den) * inv_n;
+        const float inv = 1.0f / den;
+        term = (r * r) * inv;
+        d = ((2.0f * r) * inv) * inv_n;
         break;
       }
       default:  // L2

@@ -142,6 +142,31 @@ __device__ __forceinline__ void adam_update(float &w, float &mo, float &ve,
   w = w - (lr * mh) / (sqrtf(vh) + a.eps);
 }
 
+// F contiguous 4-byte values at an F-aligned address, as one access.
+template <int F, class T>
+__device__ __forceinline__ void load_vec(const T *p, T (&out)[F]) {
+  typedef T vec __attribute__((ext_vector_type(F)));
+  if constexpr (F == 1) {
+    out[0] = p[0];
+  } else {
+    const vec v = *reinterpret_cast<const vec *>(p);
+#pragma unroll
+    for (int f = 0; f < F; ++f) out[f] = v[f];
+  }
+}
+template <int F, class T>
+__device__ __forceinline__ void store_vec(T *p, const T (&in)[F]) {
+  typedef T vec __attribute__((ext_vector_type(F)));
+  if constexpr (F == 1) {
+    p[0] = in[0];
+  } else {
+    vec v;
+#pragma unroll
+    for (int f = 0; f < F; ++f) v[f] = in[f];
+    *reinterpret_cast<vec *>(p) = v;
+  }
+}
+
 // One pass over [hash entries | mlp params]. Thread j < hash_entries owns
 // table entry j (its F floats); in lazy mode the entry is updated only if it
 // was visited (its flag, or for lifted 2D points its z = 0 partner's flag) -- the lazy sparse semantics of
@@ -161,21 +186,29 @@ __global__ void adam_kernel(AdamArgs a) {
       }
       if (a.clear_mask) a.mask_next[j] = 0;
       if (a.lazy && !visited) continue;
+      // the entry's F floats / ints are contiguous and F-aligned: one vector
+      // load and store per array
       int32_t gi[F];
-#pragma unroll
-      for (int f = 0; f < F; ++f) gi[f] = a.grad_hash[static_cast<size_t>(j) * F + f];
+      float w[F], mo[F], ve[F];
+      load_vec<F>(a.grad_hash + static_cast<size_t>(j) * F, gi);
+      load_vec<F>(a.params + static_cast<size_t>(j) * F, w);
+      load_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
+      load_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
       // F == 2 entries accumulate as one packed 64-bit sum (scatter_kernel.hpp)
       if constexpr (F == 2) gi[1] = unpack_hi(gi[0], gi[1]);
 #pragma unroll
       for (int f = 0; f < F; ++f) {
-        const size_t i = static_cast<size_t>(j) * F + f;
         const float g = static_cast<float>(gi[f]) * (1.0f / 65536.0f);
-        float w = a.params[i], mo = a.m[i], ve = a.v[i];
-        adam_update(w, mo, ve, g, a.lr_hash, a, false);
-        a.params[i] = w;
-        a.m[i] = mo;
-        a.v[i] = ve;
-        if (a.clear_grads) a.grad_hash[i] = 0;
+        adam_update(w[f], mo[f], ve[f], g, a.lr_hash, a, false);
+      }
+      store_vec<F>(a.params + static_cast<size_t>(j) * F, w);
+      store_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
+      store_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
+      if (a.clear_grads) {
+        int32_t z[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) z[f] = 0;
+        store_vec<F>(a.grad_hash + static_cast<size_t>(j) * F, z);
       }
     } else {
       const uint32_t k = j - a.hash_entries;

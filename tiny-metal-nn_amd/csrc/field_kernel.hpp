@@ -739,8 +739,9 @@ __device__ __forceinline__ float elem_loss(int kind, float y, float t,
     }
     case kLossRelL2: {
       const float den = y * y + 0.01f;
-      *d = ((2.0f * r) / den) * inv_n;
-      return (r * r) / den;
+      const float inv = 1.0f / den;  // one division per element
+      *d = ((2.0f * r) * inv) * inv_n;
+      return (r * r) * inv;
     }
     default:
       *d = (2.0f * r) * inv_n;

@@ -164,16 +164,17 @@ __device__ __forceinline__ void pack_tiles(const f32x4 (&t)[KT][kNT], half8 (&b)
 }
 
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef int16_t i16x8 __attribute__((ext_vector_type(8)));
 
 // ReLU' of a packed fp16 activation tile pair as a 16-bit lane mask
 // (0xFFFF where the activation is > 0): |bits| != 0, since the activations
-// are max(v, 0) (the sign bit masks out a -0).
+// are max(v, 0) (the sign bit masks out a -0). (|bits| + 0x7fff) has bit 15
+// set exactly when |bits| >= 1; an arithmetic shift spreads it. Two packed
+// 16-bit integer ops per pair of elements.
 __device__ __forceinline__ u16x8 relu_mask_words(half8 h) {
   const u16x8 b = __builtin_bit_cast(u16x8, h) & static_cast<uint16_t>(0x7fff);
-  const u16x8 one = static_cast<uint16_t>(1);
-  const u16x8 m = b < one ? b : one;  // 1 where nonzero
-  const u16x8 zero = static_cast<uint16_t>(0);
-  return zero - m;                    // 0xFFFF or 0
+  const u16x8 s = b + static_cast<uint16_t>(0x7fff);
+  return __builtin_bit_cast(u16x8, __builtin_bit_cast(i16x8, s) >> static_cast<int16_t>(15));
 }
 
 __device__ __forceinline__ half8 apply_mask(half8 v, u16x8 m) {
