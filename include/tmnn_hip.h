@@ -52,6 +52,30 @@ extern "C" {
 #define TMNN_HASH_ADAM_LAZY 0
 #define TMNN_HASH_ADAM_DENSE 1
 
+/* Network families: NetworkFamily (detail/network_planning.h:29-33), same
+ * numbering. On this GPU: FULLY_FUSED = the shape-specialised MFMA kernels
+ * (weight gradients in registers / owned tiles, inline or separate encode);
+ * TILED = the generic kernels (runtime layer count and geometry, weight
+ * gradients accumulated in LDS); SAFE_DEBUG = the generic kernels in fp32
+ * without the Morton sort. AUTO lets the planner choose. */
+#define TMNN_FAMILY_AUTO (-1)
+#define TMNN_FAMILY_FULLY_FUSED 0
+#define TMNN_FAMILY_TILED 1
+#define TMNN_FAMILY_SAFE_DEBUG 2
+
+/* Planner fallback reasons: PlannerFallbackReason (network_planning.h:45-58),
+ * same numbering (bit r of tmnn_network_plan.reasons). NO_FUSED_INSTANCE has
+ * no reference counterpart: no FULLY_FUSED kernel is instantiated for the
+ * shape (compile-time hidden-layer count / widths / geometry). */
+#define TMNN_PLAN_NO_GPU_CONTEXT 1
+#define TMNN_PLAN_THREADGROUP_MEMORY_EXCEEDED 4
+#define TMNN_PLAN_UNSUPPORTED_INPUT_DIMS 6
+#define TMNN_PLAN_UNSUPPORTED_OUTPUT_DIMS 7
+#define TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED 9
+#define TMNN_PLAN_FORCED_TILED 10
+#define TMNN_PLAN_FORCED_SAFE_DEBUG 11
+#define TMNN_PLAN_NO_FUSED_INSTANCE 13
+
 /* ---- descriptors ------------------------------------------------------ */
 
 /* Model descriptor: HashGridEncoding::Config (hash_grid.h:19-26),
@@ -68,7 +92,7 @@ typedef struct tmnn_model_desc {
   float base_resolution;
   float per_level_scale;
   /* network */
-  int32_t hidden_dim;         /* 1..64 in this build */
+  int32_t hidden_dim;         /* 1..64; 128 (fp16 training, 16x2 inputs) */
   int32_t num_hidden_layers;  /* 1..8 */
   int32_t num_outputs;        /* 1..16 in this build */
   /* loss */
@@ -92,7 +116,38 @@ typedef struct tmnn_model_desc {
   /* weight init */
   uint64_t seed;
   float hash_init_range;      /* U(-r, r) for the table */
+  /* planner: NetworkFactoryOptions::forced_family (network_planning.h:146-158) */
+  int32_t forced_family;      /* TMNN_FAMILY_* (AUTO by default) */
 } tmnn_model_desc;
+
+/* Device capabilities the planner decides on: DeviceCapabilities of the
+ * reference (common.h), MI355X terms. */
+typedef struct tmnn_device_caps {
+  uint32_t struct_size;       /* sizeof(tmnn_device_caps) */
+  int32_t gpu_available;
+  int32_t cu_count;
+  int32_t lds_bytes_per_cu;   /* LDS one block may use (gfx950: 160 KB) */
+  int32_t wave_size;          /* 64 */
+  int32_t has_mfma_f16;       /* v_mfma_f32_16x16x32_f16 */
+  uint64_t global_mem_bytes;
+} tmnn_device_caps;
+
+/* NetworkPlan (network_planning.h:160-174): the selected family, whether the
+ * evaluator / training kernels are the fused (specialised) ones, the
+ * candidates that were eligible (bit per family) and the recorded fallback
+ * reasons (bit per reason). */
+typedef struct tmnn_network_plan {
+  uint32_t struct_size;       /* sizeof(tmnn_network_plan) */
+  int32_t selected_family;    /* TMNN_FAMILY_*; -1 when no family can run the model */
+  int32_t fused_eval;
+  int32_t fused_train;
+  uint64_t planner_fingerprint;  /* FNV-1a of the encoding/network/precision shape */
+  uint32_t candidate_families;
+  uint32_t reasons;
+  int32_t train_lds_bytes;    /* LDS per block of the selected training kernel */
+  int32_t train_waves_per_block;
+  tmnn_device_caps capabilities;
+} tmnn_network_plan;
 
 /* Result of one fused training step: TrainingStepResult (common.h:97-110). */
 typedef struct tmnn_step_result {
@@ -103,7 +158,7 @@ typedef struct tmnn_step_result {
 
 /* Realized kernel geometry: TrainerRuntimeInspection (trainer.h:63-87). */
 typedef struct tmnn_inspection {
-  int32_t family;             /* 0 FullyFusedMFMA (the only family here) */
+  int32_t family;             /* TMNN_FAMILY_* the trainer runs */
   int32_t precision;          /* TMNN_PRECISION_* of the training kernel */
   int32_t hidden_padded;      /* MFMA tile width of the hidden layers */
   int32_t input_padded;       /* MFMA tile width of the encoded input */
@@ -134,6 +189,19 @@ int tmnn_context_destroy(tmnn_context *ctx);
 int tmnn_context_device_info(tmnn_context *ctx, int32_t *cu_count,
                              uint64_t *global_mem_bytes, char *name,
                              size_t name_capacity);
+/* The context's device capabilities (MetalContext::capabilities). */
+int tmnn_context_caps(tmnn_context *ctx, tmnn_device_caps *out);
+/* Nominal MI355X capabilities (256 CUs, 160 KB LDS, wave 64, MFMA), for
+ * planning without a device. */
+void tmnn_device_caps_init(tmnn_device_caps *caps);
+
+/* ---- planner: plan_network (network_planning.h:176-190;
+ * network_planner.cpp:132-300). Pure host logic, no allocation: family
+ * eligibility from the kernels this library instantiates and their LDS plans
+ * against caps->lds_bytes_per_cu. tmnn_trainer_create runs the same planner
+ * on its context's capabilities and builds its kernels from the result. */
+int tmnn_plan_network(const tmnn_device_caps *caps, const tmnn_model_desc *desc,
+                      tmnn_network_plan *out);
 
 /* ---- model: try_create_trainer (default_trainer.cpp:2771-2818) ---------- */
 void tmnn_model_desc_init(tmnn_model_desc *desc);
@@ -143,6 +211,8 @@ int tmnn_trainer_destroy(tmnn_trainer *tr);
 int tmnn_trainer_param_counts(tmnn_trainer *tr, uint32_t *hash_count,
                               uint32_t *mlp_count);
 int tmnn_trainer_inspect(tmnn_trainer *tr, tmnn_inspection *out);
+/* The plan the trainer was built from. */
+int tmnn_trainer_get_plan(tmnn_trainer *tr, tmnn_network_plan *out);
 
 /* ---- compute ------------------------------------------------------------ */
 /* ITrainerRuntime::training_step (trainer.h:140-141; default_trainer.cpp:

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
     assert set(declared_symbols()) == set(_lib.SIGNATURES)
-    assert lib.tmnn_abi_version() == 1
+    assert lib.tmnn_abi_version() == 2
 
 
 def test_desc_defaults_and_struct_size():

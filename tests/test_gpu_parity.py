@@ -30,7 +30,7 @@ def _say(msg: str) -> None:
 
 def make_trainer(n_input, n_output, enc, net, loss="L2", lr=1e-2, batch=1 << 16,
                  precision="fp32", hash_adam="lazy", morton=True, seed=42, hash_range=1e-4,
-                 huber_delta=None):
+                 huber_delta=None, family="auto"):
     from tiny_metal_nn import Trainer
     lo = {"otype": loss}
     if huber_delta is not None:
@@ -39,7 +39,8 @@ def make_trainer(n_input, n_output, enc, net, loss="L2", lr=1e-2, batch=1 << 16,
            "loss": lo, "optimizer": {"otype": "Adam", "learning_rate": lr},
            "weight_init": {"seed": seed, "hash_grid_range": hash_range},
            "batch_size": batch,
-           "mi355x": {"precision": precision, "hash_adam": hash_adam, "morton_sort": morton}}
+           "mi355x": {"precision": precision, "hash_adam": hash_adam, "morton_sort": morton,
+                      "family": family}}
     return Trainer.from_config(cfg, n_input=n_input, n_output=n_output)
 
 
@@ -159,11 +160,11 @@ def test_inference_empty_and_errors():
 
 # ------------------------------------------------------------- gradients --
 
-def _grads_vs_oracle(oracle, name, precision, n, seed):
+def _grads_vs_oracle(oracle, name, precision, n, seed, family="auto"):
     d, enc, net, m_out = GEOMS[name]
     rng = np.random.default_rng(seed)
     with make_trainer(d, m_out, enc, net, precision=precision, hash_range=0.5,
-                      batch=1 << 20) as tr:
+                      batch=1 << 20, family=family) as tr:
         hw, mw = tr.get_weights()
         pos = rng.random((n, d), dtype=np.float32)
         if precision == "fp16":
@@ -199,6 +200,46 @@ def test_backward_fp16_matches_oracle(oracle, name):
     assert np.array_equal(mask, omask)
     assert rel_tensor(gm, ogm) <= 2e-3
     assert rel_tensor(gh, ogh) <= 2e-3
+
+
+@pytest.mark.parametrize("family,precision", [("Tiled", "fp16"), ("Tiled", "fp32"),
+                                              ("SafeDebug", "fp16")])
+def test_planner_families_match_oracle(oracle, family, precision):
+    """Every family the planner can select runs the same math: the generic
+    (Tiled) kernels, and SafeDebug (generic, fp32, input order)."""
+    _say(f"family {family} {precision}")
+    gh, gm, mask, ogh, ogm, omask, _ = _grads_vs_oracle(oracle, "2d_f2", precision, 3000, 6,
+                                                        family=family)
+    assert np.array_equal(mask, omask)
+    exact = family == "SafeDebug" or precision == "fp32"
+    assert rel_tensor(gm, ogm) <= (1e-5 if exact else 2e-3)
+    if exact:
+        diff = np.abs(gh.astype(np.int64) - ogh.astype(np.int64))
+        assert (diff == 0).mean() > 0.99 and diff.max() <= 16
+    else:
+        assert rel_tensor(gh, ogh) <= 2e-3
+    d, enc, net, m_out = GEOMS["2d_f2"]
+    with make_trainer(d, m_out, enc, net, precision=precision, family=family) as tr:
+        ins = tr.inspect_runtime()
+        assert ins["family_name"] == family
+        assert tr.network_plan()["selected_family"] == family
+        if family == "SafeDebug":
+            assert ins["precision"] == 0
+        rng = np.random.default_rng(1)
+        pos = rng.random((4096, 2), dtype=np.float32)
+        tgt = rng.random((4096, m_out), dtype=np.float32)
+        l0 = tr.training_step(pos, tgt)
+        for _ in range(5):
+            l1 = tr.training_step(pos, tgt)
+        assert np.isfinite(l1) and l1 < l0
+
+
+def test_default_plan_is_fully_fused_for_the_image_fit():
+    d, enc, net, m_out = GEOMS["2d_f2"]
+    with make_trainer(d, m_out, enc, net, precision="fp16") as tr:
+        p = tr.network_plan()
+        assert p["selected_family"] == "FullyFused" and p["fused_train"]
+        assert tr.inspect_runtime()["waves_per_block_train"] == p["train_waves_per_block"]
 
 
 def test_int_hash_gradients_are_deterministic():

@@ -34,7 +34,7 @@ using namespace tmnn_hip;
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 1u;
+constexpr uint32_t kAbiVersion = 2u;
 constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr uint32_t kOptimizerBlobVersion = 1u;  // detail/checkpoint_contract.h:14
 
@@ -91,11 +91,14 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
 // registers, the rest accumulate it in LDS. Forward kernels encode inline,
 // specialised on the BASELINE geometries (compile-time D, F) or on the
 // runtime geometry; the hidden-128 forward reads X tiles.
-KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL) {
-  if (HP == kWideHP) return INP == 32 ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
+KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL,
+                           int family) {
+  const bool fused = family == TMNN_FAMILY_FULLY_FUSED;
+  if (HP == kWideHP)
+    return INP == 32 && fused ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
   const int DF = D * 8 + F;
 #define TMNN_FWD_SPEC(hp, inp, df)                                                   \
-  if (!train && HP == hp && INP == inp && DF == df)                                  \
+  if (fused && !train && HP == hp && INP == inp && DF == df)                         \
     return {f16 ? field_forward_kernel<hp, inp, true, df>                            \
                 : field_forward_kernel<hp, inp, false, df>,                          \
             false};
@@ -105,11 +108,11 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
 #undef TMNN_FWD_SPEC
   // fp16 training of the 64-wide, 32-feature shapes: transposes on the matrix
   // cores instead of LDS staging (mlp_kernel.hpp)
-  if (train && f16 && HP == 64 && INP == 32 && NHL == 2)
+  if (fused && train && f16 && HP == 64 && INP == 32 && NHL == 2)
     return {mlp_train_kernel<64, 32, 2>, true, false, true, true};
-  if (train && f16 && HP == 64 && INP == 32 && NHL == 1)
+  if (fused && train && f16 && HP == 64 && INP == 32 && NHL == 1)
     return {mlp_train_kernel<64, 32, 1>, true, false, true, true};
-  if (train) {
+  if (fused && train) {
 #define TMNN_TRAIN_SPEC(hp, inp, nhl)                                              \
   if (HP == hp && INP == inp && NHL == nhl)                                        \
     return {f16 ? field_train_kernel<hp, inp, true, nhl>                           \
@@ -131,6 +134,9 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
                 : field_forward_kernel<hp, inp, false, 0>,                       \
             false};                                                              \
   }
+  // FULLY_FUSED training needs one of the shape-specialised kernels above;
+  // every family's forward may use the generic one
+  if (fused && train) return {};
   TMNN_SEL(32, 32)
   TMNN_SEL(32, 64)
   TMNN_SEL(64, 32)
@@ -202,6 +208,8 @@ struct tmnn_trainer {
   float res[kMaxLevels] = {};
   uint32_t step = 0;
   float lr_enc = 0.f, lr_net = 0.f;
+  int family = TMNN_FAMILY_FULLY_FUSED;  // of the plan the kernels were chosen from
+  tmnn_network_plan plan{};
 
   DevBuf params, m, v, grad_hash, grad_mlp;
   DevBuf mask[2];  // visit flags, double-buffered: Adam reads one, zeroes the other
@@ -267,6 +275,8 @@ bool desc_ok(const tmnn_model_desc *d, std::string &why) {
     return bad("invalid precision");
   if (d->hash_adam_mode != TMNN_HASH_ADAM_LAZY && d->hash_adam_mode != TMNN_HASH_ADAM_DENSE)
     return bad("invalid hash_adam_mode");
+  if (d->forced_family < TMNN_FAMILY_AUTO || d->forced_family > TMNN_FAMILY_SAFE_DEBUG)
+    return bad("invalid forced_family");
   return true;
 }
 
@@ -312,90 +322,198 @@ int prof_collect(tmnn_trainer *tr) {
   return TMNN_OK;
 }
 
-int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
-  const KernelChoice kc = select_kernel(tr->HP, tr->INP, f16, train, tr->d.spatial_dims,
-                                        tr->d.features_per_level, tr->d.num_hidden_layers);
+// Padded widths and parameter count of a model (the kernels' view of it).
+struct ModelShape {
+  int D, F, L, IN, INP, H, HP, NHL, M, mlp_count;
+};
+
+ModelShape shape_of(const tmnn_model_desc &d) {
+  ModelShape m{};
+  m.D = d.spatial_dims;
+  m.F = d.features_per_level;
+  m.L = d.num_levels;
+  m.IN = d.num_levels * d.features_per_level;
+  m.INP = m.IN <= 32 ? 32 : 64;
+  m.H = d.hidden_dim;
+  m.HP = d.hidden_dim <= 32 ? 32 : (d.hidden_dim <= 64 ? 64 : kWideHP);
+  m.NHL = d.num_hidden_layers;
+  m.M = d.num_outputs;
+  m.mlp_count = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, 0, false, false, 1).mlp_count();
+  return m;
+}
+
+// Kernel choice and LDS sizing of one plan (host arithmetic only): the
+// family's kernel for the shape, waves per block, LDS bytes against
+// lds_limit. Returns false with *why when the family has no kernel or its
+// LDS plan does not fit.
+bool size_plan(const ModelShape &m, bool f16, bool train, int family, int lds_limit,
+               KernelPlan &out, int *why) {
+  const KernelChoice kc = select_kernel(m.HP, m.INP, f16, train, m.D, m.F, m.NHL, family);
   out.fn = kc.fn;
   out.reg_dw = kc.reg_dw;
   out.wide = kc.wide;
   out.xmem = kc.xmem;
   out.mlp = kc.mlp;
-  if (!out.fn) return fail(TMNN_ERR_UNSUPPORTED, "no kernel for this geometry");
-  if (out.mlp) {
-    const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
-                                      tr->d.num_hidden_layers, tr->d.num_outputs,
-                                      static_cast<int>(tr->mlp_count), true, true, kMlpWaves,
-                                      false, true);
-    out.wpb = kMlpWaves;
-    out.lds = mlp_lds(s).total;
-    if (out.lds > kMaxLdsBytes) return fail(TMNN_ERR_UNSUPPORTED, "MLP train kernel LDS plan too large");
-    out.f16 = f16;
-    out.train = train;
-    out.image_bytes = static_cast<size_t>(s.dw_off);
-    TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
-    TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, out.lds));
-    int per_cu = 0;
-    TMNN_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, reinterpret_cast<const void *>(out.fn), 64 * out.wpb, out.lds));
-    if (per_cu < 1) return fail(TMNN_ERR_UNSUPPORTED, "MLP train kernel cannot be resident");
-    out.max_blocks = per_cu * tr->ctx->cu_count;
-    return TMNN_OK;
-  }
-  if (out.wide) {
-    const FieldLayout fl = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
-                                       tr->d.num_hidden_layers, tr->d.num_outputs,
-                                       static_cast<int>(tr->mlp_count), f16, train, 1);
-    const WideLayout wl = make_wide_layout(fl, f16, train);
-    out.wpb = kWideWaves;
-    out.lds = wl.total;
-    out.f16 = f16;
-    out.train = train;
-    out.image_bytes = static_cast<size_t>(fl.dw_off);
-    TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
-    TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, out.lds));
-    int per_cu = 0;
-    TMNN_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, reinterpret_cast<const void *>(out.fn), 64 * kWideWaves, out.lds));
-    if (per_cu < 1) return fail(TMNN_ERR_UNSUPPORTED, "wide field kernel cannot be resident");
-    out.max_blocks = per_cu * tr->ctx->cu_count;
-    return TMNN_OK;
-  }
-  // Most waves per block whose LDS plan fits; failing that, move the dW
-  // accumulator out of LDS (global float atomics into the block's row).
-  int wpb = 0;
-  for (int dwg = 0; dwg <= (train && !kc.reg_dw ? 1 : 0) && wpb == 0; ++dwg) {
-    for (int w = 4; w >= 1; --w) {
-      const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
-                                        tr->d.num_hidden_layers, tr->d.num_outputs,
-                                        static_cast<int>(tr->mlp_count), f16, train, w,
-                                        dwg != 0, kc.reg_dw);
-      if (s.total <= kMaxLdsBytes) {
-        out.lds = s.total;
-        out.dw_global = dwg != 0;
-        wpb = w;
-        break;
-      }
-    }
-  }
-  if (wpb < 1) return fail(TMNN_ERR_UNSUPPORTED, "model does not fit in LDS");
-  out.wpb = wpb;
   out.f16 = f16;
   out.train = train;
-  {
-    const FieldLayout s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim,
-                                      tr->d.num_hidden_layers, tr->d.num_outputs,
-                                      static_cast<int>(tr->mlp_count), f16, train, 1);
-    out.image_bytes = static_cast<size_t>(s.dw_off);
-    TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
+  *why = 0;
+  if (!out.fn) {
+    *why = (m.HP == kWideHP && family != TMNN_FAMILY_FULLY_FUSED) ? TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED
+                                                                  : TMNN_PLAN_NO_FUSED_INSTANCE;
+    return false;
   }
+  if (out.mlp) {
+    const FieldLayout s = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, true, true,
+                                      kMlpWaves, false, true);
+    out.wpb = kMlpWaves;
+    out.lds = mlp_lds(s).total;
+    out.image_bytes = static_cast<size_t>(s.dw_off);
+  } else if (out.wide) {
+    const FieldLayout fl = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, f16, train, 1);
+    out.wpb = kWideWaves;
+    out.lds = make_wide_layout(fl, f16, train).total;
+    out.image_bytes = static_cast<size_t>(fl.dw_off);
+  } else {
+    // Most waves per block whose LDS plan fits; failing that, move the dW
+    // accumulator out of LDS (global float atomics into the block's row).
+    out.wpb = 0;
+    for (int dwg = 0; dwg <= (train && !kc.reg_dw ? 1 : 0) && out.wpb == 0; ++dwg) {
+      for (int w = 4; w >= 1; --w) {
+        const FieldLayout s = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, f16,
+                                          train, w, dwg != 0, kc.reg_dw);
+        if (s.total <= lds_limit) {
+          out.lds = s.total;
+          out.dw_global = dwg != 0;
+          out.wpb = w;
+          break;
+        }
+      }
+    }
+    if (out.wpb < 1) {
+      out.lds = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, f16, train, 1,
+                            train && !kc.reg_dw, kc.reg_dw).total;
+    }
+    out.image_bytes = static_cast<size_t>(
+        make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, f16, train, 1).dw_off);
+  }
+  if (out.wpb < 1 || out.lds > lds_limit) {
+    *why = TMNN_PLAN_THREADGROUP_MEMORY_EXCEEDED;
+    return false;
+  }
+  return true;
+}
+
+// FNV-1a over the shape fields the kernels depend on.
+uint64_t planner_fingerprint(const tmnn_model_desc &d) {
+  uint64_t h = 1469598103934665603ull;
+  auto mix = [&](uint64_t v) {
+    for (int i = 0; i < 8; ++i) {
+      h ^= (v >> (8 * i)) & 0xffu;
+      h *= 1099511628211ull;
+    }
+  };
+  mix(static_cast<uint64_t>(d.spatial_dims));
+  mix(static_cast<uint64_t>(d.num_levels));
+  mix(static_cast<uint64_t>(d.features_per_level));
+  mix(static_cast<uint64_t>(d.log2_hashmap_size));
+  mix(static_cast<uint64_t>(d.base_resolution * 1000000.0f));
+  mix(static_cast<uint64_t>(d.per_level_scale * 1000000.0f));
+  mix(static_cast<uint64_t>(d.hidden_dim));
+  mix(static_cast<uint64_t>(d.num_hidden_layers));
+  mix(static_cast<uint64_t>(d.num_outputs));
+  mix(static_cast<uint64_t>(d.precision));
+  return h;
+}
+
+// plan_with_capabilities (network_planner.cpp:132-300) for this library:
+// FULLY_FUSED when its training kernel is instantiated for the shape and its
+// LDS plan fits, else TILED (generic kernels), SAFE_DEBUG only when forced;
+// the reasons record why a family was not eligible or was overridden.
+void plan_network_impl(const tmnn_device_caps &caps, const tmnn_model_desc &d,
+                       tmnn_network_plan &p) {
+  std::memset(&p, 0, sizeof p);
+  p.struct_size = sizeof p;
+  p.capabilities = caps;
+  p.selected_family = -1;
+  p.planner_fingerprint = planner_fingerprint(d);
+  auto reason = [&](int r) { p.reasons |= 1u << r; };
+  if (!caps.gpu_available) {
+    reason(TMNN_PLAN_NO_GPU_CONTEXT);
+    return;
+  }
+  if (d.spatial_dims < 2 || d.spatial_dims > 4 || d.num_levels * d.features_per_level > 64) {
+    reason(TMNN_PLAN_UNSUPPORTED_INPUT_DIMS);
+    return;
+  }
+  if (d.num_outputs < 1 || d.num_outputs > 16) {
+    reason(TMNN_PLAN_UNSUPPORTED_OUTPUT_DIMS);
+    return;
+  }
+  if (d.hidden_dim < 1 || d.hidden_dim > kWideHP ||
+      (d.hidden_dim > 64 && (d.num_levels * d.features_per_level > 32 ||
+                             d.precision != TMNN_PRECISION_FP16))) {
+    reason(TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED);
+    return;
+  }
+  const ModelShape m = shape_of(d);
+  const bool f16 = d.precision == TMNN_PRECISION_FP16;
+  struct Elig {
+    bool train = false, eval = false;
+    KernelPlan tp;
+  } fam[3];
+  for (int f = 0; f < 3; ++f) {
+    const bool ff16 = f == TMNN_FAMILY_SAFE_DEBUG ? false : f16;
+    int why = 0, why_eval = 0;
+    fam[f].train = size_plan(m, ff16, true, f, caps.lds_bytes_per_cu, fam[f].tp, &why);
+    KernelPlan ep;
+    fam[f].eval = size_plan(m, false, false, f, caps.lds_bytes_per_cu, ep, &why_eval);
+    if (f == TMNN_FAMILY_FULLY_FUSED && !fam[f].train && why) reason(why);
+    if (f == TMNN_FAMILY_TILED && !fam[f].train && why == TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED)
+      reason(why);
+    if (fam[f].train && fam[f].eval) p.candidate_families |= 1u << f;
+  }
+  int sel = -1;
+  if (d.forced_family == TMNN_FAMILY_SAFE_DEBUG) {
+    reason(TMNN_PLAN_FORCED_SAFE_DEBUG);
+    sel = TMNN_FAMILY_SAFE_DEBUG;
+  } else if (d.forced_family == TMNN_FAMILY_TILED) {
+    reason(TMNN_PLAN_FORCED_TILED);
+    sel = TMNN_FAMILY_TILED;
+  } else if (p.candidate_families & (1u << TMNN_FAMILY_FULLY_FUSED)) {
+    sel = TMNN_FAMILY_FULLY_FUSED;
+  } else if (p.candidate_families & (1u << TMNN_FAMILY_TILED)) {
+    sel = TMNN_FAMILY_TILED;
+  }
+  if (sel < 0 || !(p.candidate_families & (1u << sel))) return;
+  p.selected_family = sel;
+  p.fused_train = sel == TMNN_FAMILY_FULLY_FUSED;
+  {
+    // the evaluator is fused when the family's forward kernel is specialised
+    KernelPlan ep;
+    int why = 0;
+    p.fused_eval = sel == TMNN_FAMILY_FULLY_FUSED &&
+                   size_plan(m, false, false, sel, caps.lds_bytes_per_cu, ep, &why) &&
+                   (ep.wide || ep.fn != select_kernel(m.HP, m.INP, false, false, m.D, m.F, m.NHL,
+                                                      TMNN_FAMILY_TILED).fn);
+  }
+  p.train_lds_bytes = fam[sel].tp.lds;
+  p.train_waves_per_block = fam[sel].tp.wpb;
+}
+
+// size_plan for the trainer's family, then the device side: the packed
+// image buffer, the dynamic LDS attribute and the resident block count.
+int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
+  int why = 0;
+  if (!size_plan(shape_of(tr->d), f16, train, tr->family, kMaxLdsBytes, out, &why))
+    return fail(TMNN_ERR_UNSUPPORTED,
+                why == TMNN_PLAN_THREADGROUP_MEMORY_EXCEEDED ? "model does not fit in LDS"
+                                                             : "no kernel for this geometry");
+  TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
   TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   out.lds));
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, out.lds));
   int per_cu = 0;
   TMNN_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      &per_cu, reinterpret_cast<const void *>(out.fn), 64 * wpb, out.lds));
+      &per_cu, reinterpret_cast<const void *>(out.fn), 64 * out.wpb, out.lds));
   if (per_cu < 1) return fail(TMNN_ERR_UNSUPPORTED, "field kernel cannot be resident");
   out.max_blocks = per_cu * tr->ctx->cu_count;
   return TMNN_OK;
@@ -907,6 +1025,46 @@ void tmnn_model_desc_init(tmnn_model_desc *d) {
   d->morton_sort = 1;
   d->seed = 42u;
   d->hash_init_range = 1.0e-4f;
+  d->forced_family = TMNN_FAMILY_AUTO;
+}
+
+void tmnn_device_caps_init(tmnn_device_caps *c) {
+  if (!c) return;
+  std::memset(c, 0, sizeof *c);
+  c->struct_size = sizeof *c;
+  c->gpu_available = 1;
+  c->cu_count = 256;
+  c->lds_bytes_per_cu = kMaxLdsBytes;
+  c->wave_size = 64;
+  c->has_mfma_f16 = 1;
+  c->global_mem_bytes = 288ull << 30;
+}
+
+int tmnn_context_caps(tmnn_context *ctx, tmnn_device_caps *out) {
+  if (!ctx || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  tmnn_device_caps_init(out);
+  out->cu_count = ctx->cu_count;
+  out->global_mem_bytes = ctx->mem_bytes;
+  return TMNN_OK;
+}
+
+int tmnn_plan_network(const tmnn_device_caps *caps, const tmnn_model_desc *desc,
+                      tmnn_network_plan *out) {
+  if (!caps || !desc || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (caps->struct_size != sizeof(tmnn_device_caps))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_device_caps.struct_size mismatch");
+  if (desc->struct_size != sizeof(tmnn_model_desc))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_model_desc.struct_size mismatch");
+  std::string why;
+  if (!desc_ok(desc, why)) return fail(TMNN_ERR_INVALID_ARGUMENT, "KernelSpec: " + why);
+  plan_network_impl(*caps, *desc, *out);
+  return TMNN_OK;
+}
+
+int tmnn_trainer_get_plan(tmnn_trainer *tr, tmnn_network_plan *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  *out = tr->plan;
+  return TMNN_OK;
 }
 
 int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_trainer **out) {
@@ -931,10 +1089,26 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
     return fail(TMNN_ERR_UNSUPPORTED, "num_levels * features_per_level > 64 is not built");
   TMNN_HIP_TRY(hipSetDevice(ctx->device));
 
+  // the planner decides the family the kernels come from
+  tmnn_device_caps caps;
+  int rc = tmnn_context_caps(ctx, &caps);
+  if (rc != TMNN_OK) return rc;
+  tmnn_network_plan plan;
+  plan_network_impl(caps, *desc, plan);
+  if (plan.selected_family < 0)
+    return fail(TMNN_ERR_UNSUPPORTED, "planner: no network family can run this model (reasons mask " +
+                                          std::to_string(plan.reasons) + ")");
+
   std::unique_ptr<tmnn_trainer> tr(new (std::nothrow) tmnn_trainer());
   if (!tr) return fail(TMNN_ERR_RUNTIME, "out of host memory");
   tr->ctx = ctx;
   tr->d = *desc;
+  tr->plan = plan;
+  tr->family = plan.selected_family;
+  if (tr->family == TMNN_FAMILY_SAFE_DEBUG) {  // fp32 generic kernels, batches in input order
+    tr->d.precision = TMNN_PRECISION_FP32;
+    tr->d.morton_sort = 0;
+  }
   tr->IN = IN;
   tr->INP = IN <= 32 ? 32 : 64;
   tr->HP = desc->hidden_dim <= 32 ? 32 : (desc->hidden_dim <= 64 ? 64 : kWideHP);
@@ -962,11 +1136,10 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
     }
   }
 
-  int rc;
-  if ((rc = plan_kernel(tr.get(), desc->precision == TMNN_PRECISION_FP16, true,
+  if ((rc = plan_kernel(tr.get(), tr->d.precision == TMNN_PRECISION_FP16, true,
                         tr->train_plan)) != TMNN_OK)
     return rc;
-  if ((rc = plan_kernel(tr.get(), desc->precision == TMNN_PRECISION_FP16, false,
+  if ((rc = plan_kernel(tr.get(), tr->d.precision == TMNN_PRECISION_FP16, false,
                         tr->fwd_plan)) != TMNN_OK)
     return rc;
   if ((rc = plan_kernel(tr.get(), false, false, tr->infer_plan)) != TMNN_OK) return rc;
@@ -1010,7 +1183,7 @@ int tmnn_trainer_param_counts(tmnn_trainer *tr, uint32_t *hash_count, uint32_t *
 int tmnn_trainer_inspect(tmnn_trainer *tr, tmnn_inspection *o) {
   if (!tr || !o) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
   std::memset(o, 0, sizeof *o);
-  o->family = 0;
+  o->family = tr->family;
   o->precision = tr->d.precision;
   o->hidden_padded = tr->HP;
   o->input_padded = tr->INP;

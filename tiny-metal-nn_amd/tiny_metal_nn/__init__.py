@@ -9,7 +9,7 @@ from __future__ import annotations
 
 from .config import ConfigError, canonicalize_model_config
 from .trainer import (ClosedError, ConcurrentTrainingStepError, DTypeError,
-                      OptimizerStateBlob, Trainer, philox_uniform)
+                      OptimizerStateBlob, Trainer, philox_uniform, plan_network)
 
 __version__ = "0.1.0"
 
@@ -22,5 +22,6 @@ __all__ = [
     "Trainer",
     "canonicalize_model_config",
     "philox_uniform",
+    "plan_network",
     "__version__",
 ]

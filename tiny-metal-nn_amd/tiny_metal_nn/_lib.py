@@ -54,7 +54,43 @@ class ModelDesc(ctypes.Structure):
         ("morton_sort", ctypes.c_int32),
         ("seed", ctypes.c_uint64),
         ("hash_init_range", ctypes.c_float),
+        ("forced_family", ctypes.c_int32),
     ]
+
+
+class DeviceCaps(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("gpu_available", ctypes.c_int32),
+        ("cu_count", ctypes.c_int32),
+        ("lds_bytes_per_cu", ctypes.c_int32),
+        ("wave_size", ctypes.c_int32),
+        ("has_mfma_f16", ctypes.c_int32),
+        ("global_mem_bytes", ctypes.c_uint64),
+    ]
+
+
+class NetworkPlan(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("selected_family", ctypes.c_int32),
+        ("fused_eval", ctypes.c_int32),
+        ("fused_train", ctypes.c_int32),
+        ("planner_fingerprint", ctypes.c_uint64),
+        ("candidate_families", ctypes.c_uint32),
+        ("reasons", ctypes.c_uint32),
+        ("train_lds_bytes", ctypes.c_int32),
+        ("train_waves_per_block", ctypes.c_int32),
+        ("capabilities", DeviceCaps),
+    ]
+
+
+# NetworkFamily / PlannerFallbackReason names (network_planning.h:29-58)
+FAMILIES = {0: "FullyFused", 1: "Tiled", 2: "SafeDebug"}
+FAMILY_CODES = {"auto": -1, "FullyFused": 0, "Tiled": 1, "SafeDebug": 2}
+PLAN_REASONS = {1: "NoGPUContext", 4: "ThreadgroupMemoryExceeded", 6: "UnsupportedInputDims",
+                7: "UnsupportedOutputDims", 9: "HiddenDimUnsupported", 10: "ForcedTiled",
+                11: "ForcedSafeDebug", 13: "NoFusedInstance"}
 
 
 class StepResult(ctypes.Structure):
@@ -117,6 +153,11 @@ SIGNATURES = {
     "tmnn_trainer_destroy": (ctypes.c_int, [_V]),
     "tmnn_trainer_param_counts": (ctypes.c_int, [_V, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
     "tmnn_trainer_inspect": (ctypes.c_int, [_V, ctypes.POINTER(Inspection)]),
+    "tmnn_trainer_get_plan": (ctypes.c_int, [_V, ctypes.POINTER(NetworkPlan)]),
+    "tmnn_context_caps": (ctypes.c_int, [_V, ctypes.POINTER(DeviceCaps)]),
+    "tmnn_device_caps_init": (None, [ctypes.POINTER(DeviceCaps)]),
+    "tmnn_plan_network": (ctypes.c_int, [ctypes.POINTER(DeviceCaps), ctypes.POINTER(ModelDesc),
+                                         ctypes.POINTER(NetworkPlan)]),
     "tmnn_training_step": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(StepResult)]),
     "tmnn_training_step_device": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
     "tmnn_inference": (ctypes.c_int, [_V, _V, _V, _I32]),

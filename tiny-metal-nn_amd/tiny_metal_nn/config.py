@@ -192,13 +192,17 @@ def canonicalize_model_config(n_input: int, n_output: int, config: dict) -> dict
         errors.append("batch_size: must be >= 1")
 
     mi = config.get("mi355x", {}) or {}
-    _known(mi, {"precision", "hash_adam", "morton_sort", "grad_clip"}, "mi355x", errors)
+    _known(mi, {"precision", "hash_adam", "morton_sort", "grad_clip", "family"}, "mi355x", errors)
     m = {
         "precision": _get(mi, "precision", "fp32", str, "mi355x", errors),
         "hash_adam": _get(mi, "hash_adam", "lazy", str, "mi355x", errors),
         "morton_sort": _get(mi, "morton_sort", True, bool, "mi355x", errors),
         "grad_clip": _get(mi, "grad_clip", 0.0, float, "mi355x", errors),
+        # NetworkFactoryOptions::forced_family (network_planning.h:146-158)
+        "family": _get(mi, "family", "auto", str, "mi355x", errors),
     }
+    if m["family"] not in _lib.FAMILY_CODES:
+        errors.append("mi355x.family: must be one of " + ", ".join(sorted(_lib.FAMILY_CODES)))
     if m["precision"] not in ("fp32", "fp16"):
         errors.append("mi355x.precision: must be 'fp32' or 'fp16'")
     if m["hash_adam"] not in ("lazy", "dense"):
@@ -248,4 +252,5 @@ def model_desc(canonical: dict) -> _lib.ModelDesc:
     d.morton_sort = 1 if m["morton_sort"] else 0
     d.seed = w["seed"]
     d.hash_init_range = w["hash_grid_range"]
+    d.forced_family = _lib.FAMILY_CODES[m.get("family", "auto")]
     return d

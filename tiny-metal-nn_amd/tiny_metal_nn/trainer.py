@@ -172,7 +172,16 @@ class Trainer:
         self._check_open()
         ins = _lib.Inspection()
         _lib.check(self._lib.tmnn_trainer_inspect(self._h, ctypes.byref(ins)))
-        return {k: getattr(ins, k) for k, _ in _lib.Inspection._fields_}
+        out = {k: getattr(ins, k) for k, _ in _lib.Inspection._fields_}
+        out["family_name"] = _lib.FAMILIES.get(out["family"], "Unknown")
+        return out
+
+    def network_plan(self) -> dict:
+        """The NetworkPlan this trainer's kernels were chosen from."""
+        self._check_open()
+        p = _lib.NetworkPlan()
+        _lib.check(self._lib.tmnn_trainer_get_plan(self._h, ctypes.byref(p)))
+        return plan_to_dict(p)
 
     # ---- fused path -----------------------------------------------------------
     def training_step(self, input, target) -> float:
@@ -375,3 +384,38 @@ def philox_uniform(seed: int, counter_base: int, count: int, low: float, high: f
 
 __all__ = ["Trainer", "ConfigError", "DTypeError", "ClosedError",
            "ConcurrentTrainingStepError", "OptimizerStateBlob", "philox_uniform"]
+
+
+def plan_to_dict(p) -> dict:
+    caps = {k: getattr(p.capabilities, k) for k, _ in _lib.DeviceCaps._fields_ if k != "struct_size"}
+    return {
+        "selected_family": _lib.FAMILIES.get(p.selected_family) if p.selected_family >= 0 else None,
+        "fused_eval": bool(p.fused_eval),
+        "fused_train": bool(p.fused_train),
+        "planner_fingerprint": p.planner_fingerprint,
+        "candidate_families": [n for f, n in _lib.FAMILIES.items() if p.candidate_families >> f & 1],
+        "reasons": [n for r, n in sorted(_lib.PLAN_REASONS.items()) if p.reasons >> r & 1],
+        "train_lds_bytes": p.train_lds_bytes,
+        "train_waves_per_block": p.train_waves_per_block,
+        "capabilities": caps,
+    }
+
+
+def plan_network(config: dict, n_input: int, n_output: int, capabilities: dict | None = None) -> dict:
+    """plan_network(model, capabilities) (network_planning.h:176-190): the
+    family this library would run `config` with on a device of the given
+    capabilities (default: a nominal MI355X; runs without a GPU)."""
+    from .config import canonicalize_model_config, model_desc
+    canon = canonicalize_model_config(int(n_input), int(n_output), config)
+    d = model_desc(canon)
+    lib = _lib.load()
+    caps = _lib.DeviceCaps()
+    lib.tmnn_device_caps_init(caps)
+    for k, v in (capabilities or {}).items():
+        if k == "struct_size" or not hasattr(caps, k):
+            raise ValueError(f"unknown capability {k!r}")
+        setattr(caps, k, v)
+    p = _lib.NetworkPlan()
+    _lib.check(lib.tmnn_plan_network(ctypes.byref(caps), ctypes.byref(d), ctypes.byref(p)))
+    return plan_to_dict(p)
+
