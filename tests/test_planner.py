@@ -41,6 +41,15 @@ def test_image_fit_is_fully_fused():
     assert 0 < p["train_lds_bytes"] <= 160 * 1024
 
 
+def test_sdf_shape_runs_four_waves():
+    # 16x4 features into 64x3: the weight image leaves LDS for four waves' parking
+    c = cfg(encoding__n_features_per_level=4, network__n_hidden_layers=3)
+    p = plan_network(c, 3, 1)
+    assert p["selected_family"] == "FullyFused" and p["fused_train"]
+    assert p["train_waves_per_block"] == 4
+    assert 0 < p["train_lds_bytes"] <= 160 * 1024
+
+
 def test_unspecialised_depth_falls_back_to_tiled():
     p = plan_network(cfg(network__n_hidden_layers=4), 2, 3)
     assert p["selected_family"] == "Tiled"

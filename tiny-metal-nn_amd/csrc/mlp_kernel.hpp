@@ -15,7 +15,9 @@
 //
 // Occupancy and weight gradients: eight waves per block, two per SIMD (256
 // registers each), so one wave's MFMA / LDS latencies hide behind the other's
-// work. The block walks its tiles in rounds of eight (one per wave); each
+// work; shapes whose weight image leaves no LDS for eight waves' parking run
+// four waves, one per SIMD (mlp_waves). The block walks its tiles in rounds
+// of one tile per wave; each
 // wave parks the transposed operands of its tile in LDS (lane-private 16-byte
 // slots), and after a barrier every wave accumulates the dW tiles it OWNS over
 // all eight waves' points, in wave order, in registers that live across all
@@ -38,7 +40,12 @@
 
 namespace tmnn_hip {
 
-constexpr int kMlpWaves = 8;
+// Waves per block of mlp_train_kernel: eight (two per SIMD, 256 registers
+// each) where the weight image and eight waves' parking slots fit in LDS,
+// else four (one per SIMD with the whole register file).
+__host__ __device__ constexpr int mlp_waves(int INP, int NHL) {
+  return (INP <= 32 && NHL <= 2) ? 8 : 4;
+}
 
 // LDS plan of mlp_train_kernel (bytes): the packed weight image, the per-wave
 // loss slots, then per wave its parking slots (16 bytes per lane each):
@@ -48,12 +55,12 @@ struct MlpLds {
   int32_t loss, park, park_bytes, total;
 };
 
-__host__ __device__ inline MlpLds mlp_lds(const FieldLayout &s) {
+__host__ __device__ inline MlpLds mlp_lds(const FieldLayout &s, int waves) {
   MlpLds m;
   m.loss = s.dw_off;
   m.park = m.loss + 16 * 4;
   m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + 1) * 64 * 16;
-  m.total = m.park + kMlpWaves * m.park_bytes;
+  m.total = m.park + waves * m.park_bytes;
   return m;
 }
 
@@ -181,15 +188,14 @@ __device__ __forceinline__ half8 apply_mask(half8 v, u16x8 m) {
   return __builtin_bit_cast(half8, __builtin_bit_cast(u16x8, v) & m);
 }
 
-template <int HP, int INP, int NHL>
-__global__ void __launch_bounds__(kMlpWaves * 64)
-    __attribute__((amdgpu_waves_per_eu(2, 2))) mlp_train_kernel(FieldArgs a) {
+template <int HP, int INP, int NHL, int W = mlp_waves(INP, NHL)>
+__global__ void __launch_bounds__(W * 64)
+    __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) mlp_train_kernel(FieldArgs a) {
   constexpr int HT = HP / 16;    // unit tiles of a hidden layer
   constexpr int HS = HT / 2;     // K steps over a hidden layer
   constexpr int KT0 = INP / 16;  // input feature tiles
   constexpr int XS = KT0 / 2;    // K steps over the input
-  constexpr int W = kMlpWaves;
-  static_assert(HT % 2 == 0 && KT0 % 2 == 0 && NHL >= 1, "shape");
+  static_assert(HT % 2 == 0 && KT0 % 2 == 0 && NHL >= 1 && W % 4 == 0, "shape");
   // owned jobs (dW tiles + bias tiles) per phase, wave w owns jobs w + W j
   constexpr int kJobsOut = HT + 1;        // dW_out tiles (units x outputs) + b_out
   constexpr int kJobsHid = HT * HT + HT;  // dW_k tiles + b_k tiles
@@ -201,7 +207,7 @@ __global__ void __launch_bounds__(kMlpWaves * 64)
 
   const FieldLayout s = make_layout(INP, HP, a.IN, a.H, NHL, a.M, a.mlp_count, true, true, W,
                                     false, true);
-  const MlpLds ml = mlp_lds(s);
+  const MlpLds ml = mlp_lds(s, W);
   stage_weights<true, true>(a, s, smem);
   // parked operands of absent tiles must be finite (they meet zero deltas)
   for (int e = threadIdx.x; e < W * ml.park_bytes / 16; e += blockDim.x)

@@ -86,9 +86,9 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
 }
 
 // Training kernels read their input features from encode_features_kernel:
-// fp16 training of the 64-wide, 32-feature shapes runs mlp_train_kernel, the
-// other BASELINE MLP shapes (compile-time hidden-layer count) keep dW in
-// registers, the rest accumulate it in LDS. Forward kernels encode inline,
+// fp16 training of the 64-wide BASELINE shapes runs mlp_train_kernel, their
+// fp32 training (compile-time hidden-layer count) keeps dW in registers, the
+// rest accumulate it in LDS. Forward kernels encode inline,
 // specialised on the BASELINE geometries (compile-time D, F) or on the
 // runtime geometry; the hidden-128 forward reads X tiles.
 KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL,
@@ -106,12 +106,14 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
   TMNN_FWD_SPEC(64, 32, 3 * 8 + 2)  // NeRF density: 3D, 16x2
   TMNN_FWD_SPEC(64, 64, 3 * 8 + 4)  // SDF: 3D, 16x4
 #undef TMNN_FWD_SPEC
-  // fp16 training of the 64-wide, 32-feature shapes: transposes on the matrix
+  // fp16 training of the 64-wide BASELINE shapes: transposes on the matrix
   // cores instead of LDS staging (mlp_kernel.hpp)
   if (fused && train && f16 && HP == 64 && INP == 32 && NHL == 2)
     return {mlp_train_kernel<64, 32, 2>, true, false, true, true};
   if (fused && train && f16 && HP == 64 && INP == 32 && NHL == 1)
     return {mlp_train_kernel<64, 32, 1>, true, false, true, true};
+  if (fused && train && f16 && HP == 64 && INP == 64 && NHL == 3)
+    return {mlp_train_kernel<64, 64, 3>, true, false, true, true};
   if (fused && train) {
 #define TMNN_TRAIN_SPEC(hp, inp, nhl)                                              \
   if (HP == hp && INP == inp && NHL == nhl)                                        \
@@ -364,9 +366,9 @@ bool size_plan(const ModelShape &m, bool f16, bool train, int family, int lds_li
   }
   if (out.mlp) {
     const FieldLayout s = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, true, true,
-                                      kMlpWaves, false, true);
-    out.wpb = kMlpWaves;
-    out.lds = mlp_lds(s).total;
+                                      mlp_waves(m.INP, m.NHL), false, true);
+    out.wpb = mlp_waves(m.INP, m.NHL);
+    out.lds = mlp_lds(s, out.wpb).total;
     out.image_bytes = static_cast<size_t>(s.dw_off);
   } else if (out.wide) {
     const FieldLayout fl = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, f16, train, 1);
