@@ -719,41 +719,58 @@ __device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLay
 // ------------------------------------------------------------------ loss ----
 
 // Loss term and output gradient of one element (emitLoss, L2/L1/Huber; and
-// RelativeL2 = r^2/(y^2+0.01) with the denominator held constant).
-__device__ __forceinline__ float elem_loss(int kind, float y, float t,
-                                           float delta, float inv_n,
-                                           float *d) {
+// RelativeL2 = r^2/(y^2+0.01) with the denominator held constant). FAST_RCP
+// (fp16 training only, whose gradient is rounded to fp16 next) takes the
+// RelativeL2 reciprocal from v_rcp_f32 (1 ulp) instead of a division.
+template <int KIND, bool FAST_RCP>
+__device__ __forceinline__ float elem_loss(float y, float t, float delta, float inv_n, float *d) {
   const float r = y - t;
-  switch (kind) {
-    case kLossL1:
-      *d = (r > 0.0f ? 1.0f : (r < 0.0f ? -1.0f : 0.0f)) * inv_n;
-      return fabsf(r);
-    case kLossHuber: {
-      const float ar = fabsf(r);
-      if (ar <= delta) {
-        *d = r * inv_n;
-        return (0.5f * r) * r;
-      }
-      *d = (delta * (r > 0.0f ? 1.0f : -1.0f)) * inv_n;
-      return delta * (ar - 0.5f * delta);
+  if constexpr (KIND == kLossL1) {
+    *d = (r > 0.0f ? 1.0f : (r < 0.0f ? -1.0f : 0.0f)) * inv_n;
+    return fabsf(r);
+  } else if constexpr (KIND == kLossHuber) {
+    const float ar = fabsf(r);
+    if (ar <= delta) {
+      *d = r * inv_n;
+      return (0.5f * r) * r;
     }
-    case kLossRelL2: {
-      const float den = y * y + 0.01f;
-      const float inv = 1.0f / den;  // one division per element
-      *d = ((2.0f * r) * inv) * inv_n;
-      return (r * r) * inv;
-    }
-    default:
-      *d = (2.0f * r) * inv_n;
-      return r * r;
+    *d = (delta * (r > 0.0f ? 1.0f : -1.0f)) * inv_n;
+    return delta * (ar - 0.5f * delta);
+  } else if constexpr (KIND == kLossRelL2) {
+    const float den = y * y + 0.01f;
+    const float inv = FAST_RCP ? __builtin_amdgcn_rcpf(den) : 1.0f / den;
+    *d = ((2.0f * r) * inv) * inv_n;
+    return (r * r) * inv;
+  } else {
+    *d = (2.0f * r) * inv_n;
+    return r * r;
   }
+}
+
+// Loss terms and output gradients of the valid outputs of a wave tile for a
+// compile-time loss kind (the kind is uniform: one branch per tile).
+template <int KIND, bool FAST_RCP>
+__device__ __forceinline__ void tile_loss(const FieldArgs &a, const f32x4 (&y)[1][kNT],
+                                          const float (&Tv)[kNT][4], const bool (&valid)[kNT],
+                                          int q, float &lane_loss, f32x4 &g0, f32x4 &g1) {
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = 4 * q + r;
+      if (valid[nt] && o < a.M) {
+        float d;
+        lane_loss += elem_loss<KIND, FAST_RCP>(y[0][nt][r], Tv[nt][r], a.huber_delta, a.inv_n, &d);
+        (nt == 0 ? g0 : g1)[r] = d * a.loss_scale;
+      }
+    }
 }
 
 // Loss term and output gradient of one wave tile (emitLoss,
 // mlp_kernel_emitter.cpp:562-670) in D layout: output 4*q + r of point
 // 16*nt + p. kModeInputGrad instead writes the outputs and seeds
 // d out_{grad_output} = 1; kModeTrainExtGrad takes d_out from Tv.
-template <int OKT>
+template <int OKT, bool FAST_RCP = false>
 __device__ __forceinline__ void output_grad(const FieldArgs &a, const f32x4 (&y)[1][kNT],
                                             const float (&Tv)[kNT][4], const bool (&valid)[kNT],
                                             const int (&pt)[kNT], int q, float &lane_loss,
@@ -823,18 +840,21 @@ __device__ __forceinline__ void output_grad(const FieldArgs &a, const f32x4 (&y)
       }
     }
   } else {
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int o = 4 * q + r;
-        if (valid[nt] && o < a.M) {
-          float d;
-          lane_loss += elem_loss(a.loss_kind, y[0][nt][r], Tv[nt][r], a.huber_delta,
-                                 a.inv_n, &d);
-          g[0][nt][r] = d * a.loss_scale;
-        }
-      }
+    static_assert(kNT == 2, "two point tiles per wave tile");
+    switch (a.loss_kind) {
+      case kLossL1:
+        tile_loss<kLossL1, FAST_RCP>(a, y, Tv, valid, q, lane_loss, g[0][0], g[0][1]);
+        break;
+      case kLossHuber:
+        tile_loss<kLossHuber, FAST_RCP>(a, y, Tv, valid, q, lane_loss, g[0][0], g[0][1]);
+        break;
+      case kLossRelL2:
+        tile_loss<kLossRelL2, FAST_RCP>(a, y, Tv, valid, q, lane_loss, g[0][0], g[0][1]);
+        break;
+      default:
+        tile_loss<kLossL2, FAST_RCP>(a, y, Tv, valid, q, lane_loss, g[0][0], g[0][1]);
+        break;
+    }
   }
 }
 

@@ -29,11 +29,13 @@
 // Everything else follows field_body in the fp16 training configuration:
 // split-fp16 forward (hi/lo operands, three MFMAs per product), fp16 backward
 // with a power-of-two loss scale, input features read as X tiles from
-// encode_features_kernel. Two details differ and are of fp16 size: the ReLU
+// encode_features_kernel. Details that differ are of fp16 size: the ReLU
 // derivative is taken from the fp16 activation (a positive activation below
-// 2^-25 rounds to 0 and masks its delta), and the bias gradients sum the
-// fp16 deltas on the matrix cores (an all-ones A operand against the
-// transposed delta tiles).
+// 2^-25 rounds to 0 and masks its delta), the bias gradients sum the fp16
+// deltas on the matrix cores (an all-ones A operand against the transposed
+// delta tiles), each layer's bias is the accumulator's initial value (added
+// before the products, not after), and RelativeL2 takes its reciprocal from
+// v_rcp_f32.
 #pragma once
 
 #include "field_kernel.hpp"
@@ -124,18 +126,22 @@ __device__ __forceinline__ void mma_packed(const unsigned char *frag, const half
   }
 }
 
-// Split-fp16 forward product (as layer_mma_split) on prepacked operands.
+// Split-fp16 forward product (as layer_mma_split) on prepacked operands,
+// accumulated onto the layer's bias (units 16 mt + 4 q + r of bias): the
+// bias enters first instead of last, one fp32 rounding apart.
 template <int KS, int MT>
 __device__ __forceinline__ void mma_split_packed(const unsigned char *frag_hi,
                                                  const unsigned char *frag_lo,
                                                  const half8 (&bh)[KS][kNT],
-                                                 const half8 (&bl)[KS][kNT],
+                                                 const half8 (&bl)[KS][kNT], const float *bias,
                                                  f32x4 (&out)[MT][kNT], int lane) {
+  const int q = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + 16 * mt + 4 * q);
     f32x4 acc[kNT];
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < kNT; ++nt) acc[nt] = bv;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int off = ((mt * KS + ks) * 64 + lane) * 16;
@@ -170,23 +176,21 @@ __device__ __forceinline__ void pack_tiles(const f32x4 (&t)[KT][kNT], half8 (&b)
     for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = pack8(t[2 * ks][nt], t[2 * ks + 1][nt]);
 }
 
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-typedef int16_t i16x8 __attribute__((ext_vector_type(8)));
-
-// ReLU' of a packed fp16 activation tile pair as a 16-bit lane mask
-// (0xFFFF where the activation is > 0): |bits| != 0, since the activations
-// are max(v, 0) (the sign bit masks out a -0). (|bits| + 0x7fff) has bit 15
-// set exactly when |bits| >= 1; an arithmetic shift spreads it. Two packed
-// 16-bit integer ops per pair of elements.
-__device__ __forceinline__ u16x8 relu_mask_words(half8 h) {
-  const u16x8 b = __builtin_bit_cast(u16x8, h) & static_cast<uint16_t>(0x7fff);
-  const u16x8 s = b + static_cast<uint16_t>(0x7fff);
-  return __builtin_bit_cast(u16x8, __builtin_bit_cast(i16x8, s) >> static_cast<int16_t>(15));
+// ReLU' of a packed fp16 activation tile pair as fp16 factors: 1 where the
+// activation is > 0, else 0 (or -0 for a -0 activation): min(h * 65504 *
+// 65504, 1) lifts the smallest positive fp16 (2^-24) above 1. Three packed
+// fp16 ops per pair of elements here, one packed multiply (exact) to apply;
+// integer masks instead are rewritten by the compiler into per-element
+// compares and selects.
+__device__ __forceinline__ half8 relu_factors(half8 h) {
+  const half8 big = static_cast<_Float16>(65504.0f);
+  const half8 one = static_cast<_Float16>(1.0f);
+  return __builtin_elementwise_min((h * big) * big, one);
 }
 
-__device__ __forceinline__ half8 apply_mask(half8 v, u16x8 m) {
-  return __builtin_bit_cast(half8, __builtin_bit_cast(u16x8, v) & m);
-}
+// max(x, 0) as one v_maximum3_f32 (fmaxf on an MFMA result adds a NaN-quieting
+// max(x, x)); -0 maps to +0
+__device__ __forceinline__ float relu_f32(float x) { return __builtin_elementwise_maximum(x, 0.0f); }
 
 template <int HP, int INP, int NHL, int W = mlp_waves(INP, NHL)>
 __global__ void __launch_bounds__(W * 64)
@@ -287,7 +291,7 @@ __global__ void __launch_bounds__(W * 64)
 
     // ---- forward; transposed fp16 layer inputs parked, ReLU masks kept
     f32x4 act[HT][kNT];
-    u16x8 mask[NHL][HS][kNT];
+    half8 mask[NHL][HS][kNT];  // ReLU' factors of the hidden layers
     {
       half8 bh[XS][kNT], bl[XS][kNT];
       pack_split_tiles<KT0>(X, bh, bl);
@@ -295,54 +299,48 @@ __global__ void __launch_bounds__(W * 64)
       transpose_tiles<XS>(bh, sel_lo, sel_hi, xT);
 #pragma unroll
       for (int ft = 0; ft < KT0; ++ft) park(pk, ft, lane, xT[ft]);
-      mma_split_packed<XS, HT>(smem + s.fwd_off(0), smem + s.fwd_lo_off(0), bh, bl, act, lane);
+      mma_split_packed<XS, HT>(smem + s.fwd_off(0), smem + s.fwd_lo_off(0), bh, bl,
+                               reinterpret_cast<const float *>(smem + s.bias_off(0)), act, lane);
     }
-    auto bias_relu = [&](int k) {
-      const float *bias = reinterpret_cast<const float *>(smem + s.bias_off(k));
+    auto relu = [&]() {
 #pragma unroll
-      for (int mt = 0; mt < HT; ++mt) {
-        const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + 16 * mt + 4 * q);
+      for (int mt = 0; mt < HT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) act[mt][nt][r] = __builtin_fmaxf(act[mt][nt][r] + bv[r], 0.0f);
-      }
+          for (int r = 0; r < 4; ++r) act[mt][nt][r] = relu_f32(act[mt][nt][r]);
     };
     auto pack_hidden = [&](int k, half8 (&bh)[HS][kNT], half8 (&bl)[HS][kNT]) {
       pack_split_tiles<HT>(act, bh, bl);
 #pragma unroll
       for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) mask[k][ks][nt] = relu_mask_words(bh[ks][nt]);
+        for (int nt = 0; nt < kNT; ++nt) mask[k][ks][nt] = relu_factors(bh[ks][nt]);
       half8 hT[HT];
       transpose_tiles<HS>(bh, sel_lo, sel_hi, hT);
 #pragma unroll
       for (int it = 0; it < HT; ++it) park(pk, hslot(k, it), lane, hT[it]);
     };
-    bias_relu(0);
+    relu();
 #pragma unroll
     for (int k = 1; k < NHL; ++k) {
       half8 bh[HS][kNT], bl[HS][kNT];
       pack_hidden(k - 1, bh, bl);
-      mma_split_packed<HS, HT>(smem + s.fwd_off(k), smem + s.fwd_lo_off(k), bh, bl, act, lane);
-      bias_relu(k);
+      mma_split_packed<HS, HT>(smem + s.fwd_off(k), smem + s.fwd_lo_off(k), bh, bl,
+                               reinterpret_cast<const float *>(smem + s.bias_off(k)), act, lane);
+      relu();
     }
     f32x4 y[1][kNT];
     {
       half8 bh[HS][kNT], bl[HS][kNT];
       pack_hidden(NHL - 1, bh, bl);
-      mma_split_packed<HS, 1>(smem + s.fwd_off(NHL), smem + s.fwd_lo_off(NHL), bh, bl, y, lane);
-      const f32x4 bv = *reinterpret_cast<const f32x4 *>(
-          reinterpret_cast<const float *>(smem + s.bias_off(NHL)) + 4 * q);
-#pragma unroll
-      for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) y[0][nt][r] = y[0][nt][r] + bv[r];
+      mma_split_packed<HS, 1>(smem + s.fwd_off(NHL), smem + s.fwd_lo_off(NHL), bh, bl,
+                              reinterpret_cast<const float *>(smem + s.bias_off(NHL)), y, lane);
     }
 
     // ---- loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
     f32x4 g[2][kNT];
-    output_grad<2>(a, y, Tv, valid, pt, q, lane_loss, g);
+    output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, g);
     half8 gb[1][kNT];
     pack_tiles<2>(g, gb);
     {
@@ -380,7 +378,7 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
       for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = apply_mask(b[ks][nt], mask[k][ks][nt]);
+        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = b[ks][nt] * mask[k][ks][nt];
       {
         half8 dT[HT];
         transpose_tiles<HS>(b, sel_lo, sel_hi, dT);
