@@ -253,41 +253,80 @@ __global__ void __launch_bounds__(W * 64)
   const bool dx_vec = (a.IN & 3) == 0;
   const int n_rounds = (a.n_tiles + W - 1) / W;
 
+  // Software pipeline over the block's rounds: the X tiles and target rows
+  // of the next round are requested once this round's X is packed, its
+  // targets (a gather through the rows) after this round's loss, so the
+  // loads overlap a round of work instead of opening the next one.
+  f32x4 Xn[KT0][kNT];
+  uint32_t rown[kNT];
+  float Tn[kNT][4];
+  auto point_valid = [&](int tile, int nt) {
+    return tile < a.n_tiles && tile * kTilePts + 16 * nt + p < a.n;
+  };
+  auto fetch_x = [&](int tile) {
+#pragma unroll
+    for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+        Xn[kt][nt] = tile < a.n_tiles
+                         ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto fetch_rows = [&](int tile) {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const uint32_t pr =
+          point_valid(tile, nt) ? static_cast<uint32_t>(tile * kTilePts + 16 * nt + p) : 0u;
+      rown[nt] = has_target ? (a.tgt_index ? a.tgt_index[pr] : pr) : 0u;
+    }
+  };
+  // raw values: the validity select waits until the round that uses them
+  auto fetch_targets = [&]() {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const size_t row = static_cast<size_t>(rown[nt]) * a.M;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        Tn[nt][r] = has_target ? a.target[row + (o < a.M ? o : a.M - 1)] : 0.0f;
+      }
+    }
+  };
+  if (blockIdx.x < n_rounds) {
+    fetch_x(blockIdx.x * W + wave);
+    fetch_rows(blockIdx.x * W + wave);
+    fetch_targets();
+  }
+
   for (int round = blockIdx.x; round < n_rounds; round += gridDim.x) {
     const int tile = round * W + wave;
+    const int next_tile = (round + gridDim.x) * W + wave;  // >= n_tiles: zeros
     const bool have = tile < a.n_tiles;  // waves past the batch park zero deltas
     int pt[kNT];
     bool valid[kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       pt[nt] = tile * kTilePts + 16 * nt + p;
-      valid[nt] = have && pt[nt] < a.n;
+      valid[nt] = point_valid(tile, nt);
     }
     f32x4 X[KT0][kNT];
 #pragma unroll
     for (int kt = 0; kt < KT0; ++kt)
 #pragma unroll
-      for (int nt = 0; nt < kNT; ++nt)
-        X[kt][nt] = have ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
-                         : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < kNT; ++nt) X[kt][nt] = Xn[kt][nt];
     float Tv[kNT][4];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Tv[nt][r] = 0.0f;
-    if (has_target) {
-#pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) {
-        const uint32_t pr = valid[nt] ? static_cast<uint32_t>(pt[nt]) : 0u;
-        const size_t row = static_cast<size_t>(a.tgt_index ? a.tgt_index[pr] : pr) * a.M;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int o = 4 * q + r;
-          const float v = a.target[row + (o < a.M ? o : a.M - 1)];
-          Tv[nt][r] = (valid[nt] && o < a.M) ? v : 0.0f;
-        }
-      }
-    }
+      for (int r = 0; r < 4; ++r) Tv[nt][r] = (valid[nt] && 4 * q + r < a.M) ? Tn[nt][r] : 0.0f;
+    // the targets arrived during the previous round: take them here, before
+    // this round's requests (an empty asm: orders, emits nothing), so that the
+    // wait for them does not also wait for the loads issued below
+    asm volatile(""
+                 : "+v"(Tv[0][0]), "+v"(Tv[0][1]), "+v"(Tv[0][2]), "+v"(Tv[0][3]),
+                   "+v"(Tv[1][0]), "+v"(Tv[1][1]), "+v"(Tv[1][2]), "+v"(Tv[1][3])
+                 :
+                 : "memory");
 
     // ---- forward; transposed fp16 layer inputs parked, ReLU masks kept
     f32x4 act[HT][kNT];
@@ -295,6 +334,8 @@ __global__ void __launch_bounds__(W * 64)
     {
       half8 bh[XS][kNT], bl[XS][kNT];
       pack_split_tiles<KT0>(X, bh, bl);
+      fetch_x(next_tile);
+      fetch_rows(next_tile);
       half8 xT[KT0];
       transpose_tiles<XS>(bh, sel_lo, sel_hi, xT);
 #pragma unroll
@@ -341,6 +382,7 @@ __global__ void __launch_bounds__(W * 64)
     // ---- loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
     f32x4 g[2][kNT];
     output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, g);
+    fetch_targets();
     half8 gb[1][kNT];
     pack_tiles<2>(g, gb);
     {
