@@ -74,7 +74,9 @@ __device__ __forceinline__ int32_t wave_incl_sum(int32_t v) {
 // int32 atomics they feed.
 template <int N>
 __device__ __forceinline__ void run_sums(uint32_t key, int32_t (&c)[N], int lane, bool *is_tail) {
-  const uint32_t prev = __shfl_up(key, 1);
+  // previous lane's key: DPP wave_shr:1 (lane 0 keeps the old value)
+  const uint32_t prev = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(-1, static_cast<int>(key), 0x138, 0xf, 0xf, false));
   const bool head = lane == 0 || prev != key;
   const uint64_t heads = __ballot(head);
   if (heads == ~0ull) {  // no two neighbours share an entry
@@ -94,11 +96,22 @@ __device__ __forceinline__ void run_sums(uint32_t key, int32_t (&c)[N], int lane
   *is_tail = lane == 63 || ((heads >> (lane + 1)) & 1ull);
 }
 
+// |d| < 32768 for every feature: then every product d * w (w in [0, 1]) times
+// 65536 lies inside int32, and the conversion needs no saturation or NaN
+// handling (f2i_trunc's branches)
+template <int F>
+__device__ __forceinline__ bool grads_fit(const float *d) {
+  bool ok = true;
+#pragma unroll
+  for (int f = 0; f < F; ++f) ok = ok && __builtin_fabsf(d[f]) < 32768.0f;
+  return ok;
+}
+
 // One thread per point, all levels in turn: the thread reads its dx row with
 // 16-byte loads (coalesced across the wave) and the lanes of a wave still
 // hold consecutive Morton-sorted points at the same level, which keeps the
-// run merging.
-template <int D, int F>
+// run merging. FITS: every lane's d passed grads_fit (plain conversion).
+template <int D, int F, bool FITS>
 __device__ __forceinline__ void scatter_level(const ScatterArgs &a, int l, const float *p,
                                               const float *d, bool valid, int lane) {
   const Cell<D> c = cell_of<D>(p, a.res[l]);
@@ -124,7 +137,10 @@ __device__ __forceinline__ void scatter_level(const ScatterArgs &a, int l, const
         if constexpr (D >= 3) v = v * wc[2];
         if constexpr (D == 4) v = v * wc[3];
       }
-      ci[f] = valid ? f2i_trunc(v * kGradScale) : 0;
+      if constexpr (FITS)
+        ci[f] = valid ? static_cast<int32_t>(v * kGradScale) : 0;
+      else
+        ci[f] = valid ? f2i_trunc(v * kGradScale) : 0;
     }
     bool tail = true;
     run_sums<F>(local, ci, lane, &tail);
@@ -176,7 +192,10 @@ __global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterAr
       float d[F];
 #pragma unroll
       for (int f = 0; f < F; ++f) d[f] = v[lv * F + f];
-      scatter_level<D, F>(a, l, p, d, valid, lane);
+      if (__all(grads_fit<F>(d)))
+        scatter_level<D, F, true>(a, l, p, d, valid, lane);
+      else
+        scatter_level<D, F, false>(a, l, p, d, valid, lane);
     }
   }
 }
@@ -208,7 +227,10 @@ __global__ void __launch_bounds__(kScatterThreads) hash_scatter_level_kernel(Sca
   } else {
     d[0] = src[0];
   }
-  scatter_level<D, F>(a, l, p, d, valid, lane);
+  if (__all(grads_fit<F>(d)))
+    scatter_level<D, F, true>(a, l, p, d, valid, lane);
+  else
+    scatter_level<D, F, false>(a, l, p, d, valid, lane);
 }
 
 }  // namespace tmnn_hip
