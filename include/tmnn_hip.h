@@ -345,6 +345,15 @@ int tmnn_debug_morton_sort(tmnn_trainer *tr, const float *positions, int32_t n,
 /* Per-level resolution table used by every kernel (L floats). */
 int tmnn_debug_get_resolutions(tmnn_trainer *tr, float *out, int32_t count);
 
+/* The training plan's packed weight image (LDS head: weight fragments,
+ * biases, resolution table): `current` as the training step left it (a fused
+ * step updates it in place with the new weights) and `repacked` as rebuilt
+ * from the parameters now; the two are byte-identical. *bytes receives the
+ * image size; pass NULL for both buffers to query it. Host memory. No
+ * counterpart in the reference (its weights live in device buffers read by
+ * the kernels directly). */
+int tmnn_debug_train_image(tmnn_trainer *tr, void *current, void *repacked, uint64_t *bytes);
+
 /* The seeded Philox-4x32-10 uniform fill used for weight init
  * (detail::context_dispatch_init_uniform, metal_context.cpp:731-982):
  * out[count] = low + u * (high - low), counters base, base+1, ...

@@ -542,3 +542,26 @@ def test_wide_training_loss_tracks_oracle(oracle):
             lg = tr.training_step(pos, tgt)
             lo = oracle.training_step(m, a, step, params, m1, m2, pos, tgt)
             assert lg == pytest.approx(lo, rel=0.01), (step, lg, lo)
+
+
+# ------------------------------------------------------ fused step image --
+
+@pytest.mark.parametrize("name,precision", [("2d_f2", "fp16"), ("3d_f4", "fp16"), ("3d_f2", "fp16"),
+                                            ("2d_f2", "fp32"), ("small", "fp32"),
+                                            ("4d_w128", "fp16")])
+def test_fused_step_keeps_the_training_image_current(name, precision):
+    """The fused end of a training step writes every updated MLP weight into
+    the training plan's packed LDS image (forward hi/lo and backward
+    fragments, biases): after several steps it equals a repack from the
+    parameters, byte for byte."""
+    _say(f"fused step image {name} {precision}")
+    d, enc, net, m_out = GEOMS[name] if name in GEOMS else WIDE_GEOMS[name]
+    rng = np.random.default_rng(5)
+    with make_trainer(d, m_out, enc, net, precision=precision, hash_range=0.1) as tr:
+        for _ in range(3):
+            pos = rng.random((5000, d), dtype=np.float32)
+            tgt = rng.random((5000, m_out), dtype=np.float32)
+            tr.training_step(pos, tgt)
+        cur, rep = tr.debug_train_image()
+    assert cur.size > 0
+    assert np.array_equal(cur, rep)

@@ -173,53 +173,65 @@ __device__ __forceinline__ void store_vec(T *p, const T (&in)[F]) {
 // neural_sdf_adam_hash_sparse (adam_kernel_msl.h:120-164) without the host
 // compaction (default_trainer.cpp:1882-1960). Threads past the table own one
 // MLP parameter each (neural_sdf_adam_mlp_dense, adam_kernel_msl.h:166-203).
+// Adam of hash entry j (its F floats): skipped in lazy mode unless visited;
+// zeroes the entry's flag in the next step's buffer.
+template <int F>
+__device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j) {
+  bool visited = a.mask[j] != 0;
+  if (a.partner_xor) {  // lifted 2D: also visited as some corner's z = 1 partner
+    const uint32_t tmask = (1u << a.log2T) - 1u;
+    visited = visited || a.mask[(j & ~tmask) | ((j & tmask) ^ a.partner_xor)] != 0;
+  }
+  if (a.clear_mask) a.mask_next[j] = 0;
+  if (a.lazy && !visited) return;
+  // the entry's F floats / ints are contiguous and F-aligned: one vector
+  // load and store per array
+  int32_t gi[F];
+  float w[F], mo[F], ve[F];
+  load_vec<F>(a.grad_hash + static_cast<size_t>(j) * F, gi);
+  load_vec<F>(a.params + static_cast<size_t>(j) * F, w);
+  load_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
+  load_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
+  // F == 2 entries accumulate as one packed 64-bit sum (scatter_kernel.hpp)
+  if constexpr (F == 2) gi[1] = unpack_hi(gi[0], gi[1]);
+#pragma unroll
+  for (int f = 0; f < F; ++f) {
+    const float g = static_cast<float>(gi[f]) * (1.0f / 65536.0f);
+    adam_update(w[f], mo[f], ve[f], g, a.lr_hash, a, false);
+  }
+  store_vec<F>(a.params + static_cast<size_t>(j) * F, w);
+  store_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
+  store_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
+  if (a.clear_grads) {
+    int32_t z[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) z[f] = 0;
+    store_vec<F>(a.grad_hash + static_cast<size_t>(j) * F, z);
+  }
+}
+
+// Adam of MLP parameter k with gradient g; returns the new weight.
+template <int F>
+__device__ __forceinline__ float adam_mlp_param(const AdamArgs &a, uint32_t k, float g) {
+  const size_t i = static_cast<size_t>(a.hash_entries) * F + k;
+  float w = a.params[i], mo = a.m[i], ve = a.v[i];
+  adam_update(w, mo, ve, g, a.lr_mlp, a, true);
+  a.params[i] = w;
+  a.m[i] = mo;
+  a.v[i] = ve;
+  if (a.clear_grads) a.grad_mlp[k] = 0.0f;
+  return w;
+}
+
 template <int F>
 __global__ void adam_kernel(AdamArgs a) {
   const uint32_t total = a.hash_entries + a.mlp_count;
   const uint32_t stride = gridDim.x * blockDim.x;
   for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < total; j += stride) {
-    if (j < a.hash_entries) {
-      bool visited = a.mask[j] != 0;
-      if (a.partner_xor) {  // lifted 2D: also visited as some corner's z = 1 partner
-        const uint32_t tmask = (1u << a.log2T) - 1u;
-        visited = visited || a.mask[(j & ~tmask) | ((j & tmask) ^ a.partner_xor)] != 0;
-      }
-      if (a.clear_mask) a.mask_next[j] = 0;
-      if (a.lazy && !visited) continue;
-      // the entry's F floats / ints are contiguous and F-aligned: one vector
-      // load and store per array
-      int32_t gi[F];
-      float w[F], mo[F], ve[F];
-      load_vec<F>(a.grad_hash + static_cast<size_t>(j) * F, gi);
-      load_vec<F>(a.params + static_cast<size_t>(j) * F, w);
-      load_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
-      load_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
-      // F == 2 entries accumulate as one packed 64-bit sum (scatter_kernel.hpp)
-      if constexpr (F == 2) gi[1] = unpack_hi(gi[0], gi[1]);
-#pragma unroll
-      for (int f = 0; f < F; ++f) {
-        const float g = static_cast<float>(gi[f]) * (1.0f / 65536.0f);
-        adam_update(w[f], mo[f], ve[f], g, a.lr_hash, a, false);
-      }
-      store_vec<F>(a.params + static_cast<size_t>(j) * F, w);
-      store_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
-      store_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
-      if (a.clear_grads) {
-        int32_t z[F];
-#pragma unroll
-        for (int f = 0; f < F; ++f) z[f] = 0;
-        store_vec<F>(a.grad_hash + static_cast<size_t>(j) * F, z);
-      }
-    } else {
-      const uint32_t k = j - a.hash_entries;
-      const size_t i = static_cast<size_t>(a.hash_entries) * F + k;
-      float w = a.params[i], mo = a.m[i], ve = a.v[i];
-      adam_update(w, mo, ve, a.grad_mlp[k], a.lr_mlp, a, true);
-      a.params[i] = w;
-      a.m[i] = mo;
-      a.v[i] = ve;
-      if (a.clear_grads) a.grad_mlp[k] = 0.0f;
-    }
+    if (j < a.hash_entries)
+      adam_hash_entry<F>(a, j);
+    else
+      adam_mlp_param<F>(a, j - a.hash_entries, a.grad_mlp[j - a.hash_entries]);
   }
 }
 

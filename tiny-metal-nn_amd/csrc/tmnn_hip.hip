@@ -28,6 +28,7 @@
 #include "mlp_kernel.hpp"
 #include "scatter_kernel.hpp"
 #include "sort.hpp"
+#include "step_kernel.hpp"
 #include "wide_kernel.hpp"
 
 using namespace tmnn_hip;
@@ -760,7 +761,8 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
 // accumulated into grad_hash / grad_mlp / mask. Returns the block count used
 // (for the loss reduction) or a negative status.
 int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
-                         int n, bool external_grad, float *d_loss = nullptr) {
+                         int n, bool external_grad, float *d_loss = nullptr,
+                         bool reduce = true) {
   const bool f16 = tr->d.precision == TMNN_PRECISION_FP16;
   const float *pos = d_pos, *tgt = d_tgt;
   const uint32_t *perm = nullptr;
@@ -792,6 +794,7 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
   if ((rc = launch_scatter(tr, indexed ? sorted_pos : pos, n)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
+  if (!reduce) return blocks;  // finish_step_kernel reduces the rows and the loss
   // dW rows, plus (training steps) the loss in one extra block
   const uint32_t rblocks = (tr->mlp_count + kReduceCols - 1) / kReduceCols + (d_loss ? 1 : 0);
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(rblocks), dim3(kReduceCols * kReduceGroups), 0,
@@ -802,7 +805,7 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   return blocks;
 }
 
-int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
+AdamArgs adam_args(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
   AdamArgs a{};
   a.params = tr->params.as<float>();
   a.m = tr->m.as<float>();
@@ -832,6 +835,11 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
   a.weight_decay = tr->d.weight_decay;
   a.clear_grads = clear_grads ? 1 : 0;
   a.clear_mask = clear_mask ? 1 : 0;
+  return a;
+}
+
+int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
+  const AdamArgs a = adam_args(tr, clear_grads, clear_mask);
   const uint32_t total = tr->hash_entries + tr->mlp_count;
   const uint32_t blocks = std::min<uint32_t>((total + 255) / 256,
                                              static_cast<uint32_t>(tr->ctx->cu_count) * 16u);
@@ -843,6 +851,40 @@ int run_adam(tmnn_trainer *tr, bool clear_grads, bool clear_mask) {
   TMNN_HIP_TRY(hipGetLastError());
   if (clear_mask) tr->mask_cur ^= 1;  // the zeroed buffer collects the next step
   ++tr->weights_version;
+  return TMNN_OK;
+}
+
+// The end of a fused training step (finish_step_kernel): dW reduction of the
+// part_blocks partial rows, the loss, Adam (grads and flags cleared), and the
+// training plan's image updated in place when it was current.
+int run_finish(tmnn_trainer *tr, int part_blocks, int n, float *d_loss) {
+  FinishArgs f{};
+  f.adam = adam_args(tr, true, true);
+  f.partials = tr->partials.as<float>();
+  f.part_blocks = part_blocks;
+  f.loss_partials = tr->loss_partials.as<float>();
+  f.n = n;
+  f.loss_out = d_loss;
+  f.mlp_blocks = static_cast<int32_t>((tr->mlp_count + kReduceCols - 1) / kReduceCols);
+  KernelPlan &plan = tr->train_plan;
+  const bool image_current = plan.image && plan.packed_version == tr->weights_version;
+  f.s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim, tr->d.num_hidden_layers,
+                    tr->d.num_outputs, static_cast<int>(tr->mlp_count), plan.f16, plan.train, 1);
+  f.f16 = plan.f16 ? 1 : 0;
+  f.image = image_current ? static_cast<unsigned char *>(plan.image) : nullptr;
+  const uint32_t hash_blocks = std::max<uint32_t>(
+      1u, std::min<uint32_t>((tr->hash_entries + kFinishThreads - 1) / kFinishThreads,
+                             static_cast<uint32_t>(tr->ctx->cu_count) * 4u));
+  const dim3 grid(static_cast<uint32_t>(f.mlp_blocks) + 1u + hash_blocks);
+  switch (tr->d.features_per_level) {
+    case 1: hipLaunchKernelGGL(finish_step_kernel<1>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
+    case 2: hipLaunchKernelGGL(finish_step_kernel<2>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
+    default: hipLaunchKernelGGL(finish_step_kernel<4>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
+  }
+  TMNN_HIP_TRY(hipGetLastError());
+  tr->mask_cur ^= 1;  // the zeroed buffer collects the next step
+  ++tr->weights_version;
+  if (image_current) plan.packed_version = tr->weights_version;
   return TMNN_OK;
 }
 
@@ -861,11 +903,12 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
                       float *d_loss) {
   int rc = prof_begin_step(tr);
   if (rc != TMNN_OK) return rc;
-  const int blocks =
-      run_forward_backward(tr, d_pos, d_tgt, n, false, d_loss ? d_loss : tr->loss_out.as<float>());
+  float *loss = d_loss ? d_loss : tr->loss_out.as<float>();
+  const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false, loss, false);
   if (blocks < 0) return blocks;
   if ((rc = prof_mark(tr, 5)) != TMNN_OK) return rc;
-  if ((rc = run_adam(tr, true, true)) != TMNN_OK) return rc;
+  // dW reduction, loss and Adam in one kernel (the reduce phase reads ~0)
+  if ((rc = run_finish(tr, blocks, n, loss)) != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 6)) != TMNN_OK) return rc;
   if (tr->prof_cur >= 0) tr->prof_acc.batch_size = static_cast<uint32_t>(n);
   tr->prof_cur = -1;
@@ -1731,6 +1774,38 @@ int tmnn_debug_get_resolutions(tmnn_trainer *tr, float *out, int32_t count) {
   if (count != tr->d.num_levels) return fail(TMNN_ERR_INVALID_ARGUMENT, "count must equal num_levels");
   for (int l = 0; l < count; ++l) out[l] = tr->res[l];
   return TMNN_OK;
+}
+
+int tmnn_debug_train_image(tmnn_trainer *tr, void *current, void *repacked, uint64_t *bytes) {
+  if (!tr || !bytes) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  KernelPlan &plan = tr->train_plan;
+  if (!plan.image) return fail(TMNN_ERR_RUNTIME, "the trainer has no training plan image");
+  *bytes = plan.image_bytes;
+  if (!current && !repacked) return TMNN_OK;
+  if (!current || !repacked) return fail(TMNN_ERR_INVALID_ARGUMENT, "null image buffer");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  TMNN_HIP_TRY(hipMemcpyAsync(current, plan.image, plan.image_bytes, hipMemcpyDeviceToHost, st));
+  // repack into a copy (bytes the packer does not write stay as they are)
+  KernelPlan tmp = plan;
+  TMNN_HIP_TRY(hipMalloc(&tmp.image, plan.image_bytes));
+  int rc = TMNN_OK;
+  if (hipMemcpyAsync(tmp.image, plan.image, plan.image_bytes, hipMemcpyDeviceToDevice, st) !=
+      hipSuccess) {
+    rc = fail(TMNN_ERR_RUNTIME, "image copy failed");
+  } else {
+    tmp.packed_version = ~0ull;
+    rc = ensure_image(tr, tmp);
+    if (rc == TMNN_OK &&
+        (hipMemcpyAsync(repacked, tmp.image, plan.image_bytes, hipMemcpyDeviceToHost, st) !=
+             hipSuccess ||
+         hipStreamSynchronize(st) != hipSuccess))
+      rc = fail(TMNN_ERR_RUNTIME, "image readback failed");
+  }
+  if (hipStreamSynchronize(st) != hipSuccess && rc == TMNN_OK)
+    rc = fail(TMNN_ERR_RUNTIME, "stream synchronize failed");
+  if (hipFree(tmp.image) != hipSuccess && rc == TMNN_OK) rc = fail(TMNN_ERR_RUNTIME, "free failed");
+  return rc;
 }
 
 int tmnn_debug_philox_uniform(tmnn_context *ctx, uint64_t seed, uint32_t counter_base,

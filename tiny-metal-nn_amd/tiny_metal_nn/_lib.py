@@ -183,6 +183,7 @@ SIGNATURES = {
     "tmnn_debug_get_active_mask": (ctypes.c_int, [_V, _V, _SZ]),
     "tmnn_debug_morton_sort": (ctypes.c_int, [_V, _V, _I32, _V, _V]),
     "tmnn_debug_get_resolutions": (ctypes.c_int, [_V, _V, _I32]),
+    "tmnn_debug_train_image": (ctypes.c_int, [_V, _V, _V, ctypes.POINTER(ctypes.c_uint64)]),
     "tmnn_debug_philox_uniform": (ctypes.c_int, [_V, ctypes.c_uint64, _U32, _U32, _F, _F, _V]),
 }
 

@@ -364,6 +364,17 @@ class Trainer:
                                                         _ptr(perm)))
         return codes, perm
 
+    def debug_train_image(self) -> tuple[np.ndarray, np.ndarray]:
+        """(current, repacked) bytes of the training plan's packed weight image."""
+        self._check_open()
+        nbytes = ctypes.c_uint64(0)
+        _lib.check(self._lib.tmnn_debug_train_image(self._h, None, None, ctypes.byref(nbytes)))
+        cur = np.empty(nbytes.value, np.uint8)
+        rep = np.empty(nbytes.value, np.uint8)
+        _lib.check(self._lib.tmnn_debug_train_image(self._h, _ptr(cur), _ptr(rep),
+                                                    ctypes.byref(nbytes)))
+        return cur, rep
+
     def debug_resolutions(self) -> np.ndarray:
         self._check_open()
         L = self.config["encoding"]["n_levels"]
