@@ -11,10 +11,10 @@ Workload ("C2"): the image-fit training step.
     bilinearly at 2^18 uniform random coordinates per step;
   * full backward through the MLP and the hash table (int32 fixed-point
     scatter), then the fused Adam pass (lr 1e-2, b1 0.9, b2 0.99, eps 1e-15).
-One step = Morton sort (+ weight-image packing) -> hash-grid encode kernel ->
-MLP train kernel (forward, loss, backward, dW) -> hash-grid scatter kernel ->
-dW / loss reductions -> Adam, all on the library's HIP stream, inputs resident
-in HBM before the timed region starts.
+One step = Morton sort -> hash-grid encode kernel -> MLP train kernel
+(forward, loss, backward, dW) -> hash-grid scatter kernel -> finish kernel
+(dW / loss reductions, Adam, weight image for the next step), all on the
+library's HIP stream, inputs resident in HBM before the timed region starts.
 
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
 fp32, 2^16 points per call), per-kernel roofline fractions (HIP event time of
@@ -78,7 +78,9 @@ def kernel_models(d: int = 2, levels: int = 16, feats: int = 2, n_out: int = 3,
                   corner and level;
       adam     -- 28 B per parameter (param, m, v read+write, gradient read),
                   the dense figure; the lazy pass reads a flag per table entry
-                  on top."""
+                  on top. The kernel that runs it (finish_step_kernel) also
+                  reduces the MLP kernel's per-block dW rows and writes the
+                  weight image: overhead, not counted."""
     corners = 1 << d
     flops = 2 * (inp * hidden + (n_hidden - 1) * hidden * hidden + hidden * n_out)
     return {
@@ -91,9 +93,9 @@ def kernel_models(d: int = 2, levels: int = 16, feats: int = 2, n_out: int = 3,
 
 KERNELS = {  # model key -> (step-profile phase, kernel name in rocprof traces)
     "encode": ("gpu_encode_us", "encode_features_kernel<2, 2>"),
-    "mlp": ("gpu_fwd_bwd_us", "mlp_train_kernel<64, 32, 2>"),
+    "mlp": ("gpu_fwd_bwd_us", "mlp_train_kernel<64, 32, 2, 8>"),
     "scatter": ("gpu_scatter_us", "hash_scatter_kernel<2, 2>"),
-    "adam": ("gpu_adam_us", "adam_kernel<2>"),
+    "adam": ("gpu_adam_us", "finish_step_kernel<2>"),
 }
 
 
