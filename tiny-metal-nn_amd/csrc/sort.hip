@@ -4,15 +4,17 @@
 //
 // RB-bit digits (10 for 2D's 20-bit codes: 2 passes; 8 for 3D's 30-bit and
 // 4D's 32-bit codes: 4 passes), three kernels per pass:
-//   hist   -- each block counts the digits of its 1024-key chunk (LDS atomics)
+//   hist   -- each block counts the digits of its 2048-key chunk (LDS atomics)
 //             into hist[digit][block]; the first pass computes the Morton
 //             codes from the positions itself;
 //   scan   -- one block per digit: exclusive prefix of the digit's counts over
 //             the blocks, and the digit total;
-//   scatter-- each block ranks its chunk stably (wave ballots for the rank
-//             among equal digits, wave order and round order for the rest),
-//             sorts it locally in LDS and writes it out digit run by digit
-//             run, so consecutive lanes store consecutive addresses.
+//   scatter-- each block ranks its chunk stably: every wave ranks a
+//             contiguous quarter of it against its own LDS counters (wave
+//             ballots for the rank among equal digits, rounds in input
+//             order), then a per-digit prefix over the waves; it sorts the
+//             chunk locally in LDS and writes it out digit run by digit run,
+//             so consecutive lanes store consecutive addresses.
 // Ties keep input order (stable), so the sorted order is deterministic.
 #include "sort.hpp"
 
@@ -24,8 +26,9 @@ namespace tmnn_hip {
 namespace {
 
 constexpr int kSortThreads = 256;
-constexpr int kKeysPerThread = 4;
+constexpr int kKeysPerThread = 8;
 constexpr int kChunk = kSortThreads * kKeysPerThread;  // keys per block
+constexpr int kWaveKeys = 64 * kKeysPerThread;         // keys per wave in the scatter
 constexpr int kSortWaves = kSortThreads / 64;
 
 // Inclusive scan of v over the 64 lanes of a wave.
@@ -122,61 +125,47 @@ __global__ void __launch_bounds__(kSortThreads)
 template <int RB, bool FIRST>
 __global__ void __launch_bounds__(kSortThreads)
     radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const float *pos,
-                         int dims, int n, int shift, int blocks, const uint32_t *hist,
+                         int dims, int n, int shift, int blocks, const uint32_t * /*hist*/,
                          const uint32_t *pre, const uint32_t *totals, uint32_t *keys_out,
                          uint32_t *vals_out) {
   constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
   __shared__ uint32_t s_keys[kChunk];
   __shared__ uint32_t s_vals[kChunk];
-  __shared__ uint32_t glob[kBins];     // global start of this block's digit run
-  __shared__ uint32_t local[kBins];    // start of the digit run within the chunk
-  __shared__ uint32_t running[kBins];  // keys of each digit placed so far
   __shared__ uint16_t wcnt[kSortWaves][kBins];  // per-wave counts, then offsets (< kChunk)
+  __shared__ uint32_t lstart[kBins];            // start of the digit run within the chunk
+  __shared__ uint32_t glob[kBins];              // global slot of chunk index 0 of the run
   __shared__ uint32_t wsum[kSortWaves];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   const int base = blockIdx.x * kChunk;
   const int nblk = std::min(kChunk, n - base);
-
-  // thread t owns digits [t*BPT, (t+1)*BPT): global start of each digit
-  // (exclusive scan of the digit totals) plus this block's prefix within the
-  // digit; chunk-local starts from the block's own counts
-  {
-    uint32_t tot[BPT], cnt[BPT], st = 0, sc = 0;
-#pragma unroll
-    for (int j = 0; j < BPT; ++j) {
-      const int d = t * BPT + j;
-      tot[j] = totals[d];
-      cnt[j] = hist[static_cast<size_t>(d) * blocks + blockIdx.x];
-      st += tot[j];
-      sc += cnt[j];
-    }
-    uint32_t all = 0;
-    uint32_t gb = block_excl_scan(st, wsum, &all);
-    uint32_t lb = block_excl_scan(sc, wsum, &all);
-#pragma unroll
-    for (int j = 0; j < BPT; ++j) {
-      const int d = t * BPT + j;
-      glob[d] = gb + pre[static_cast<size_t>(d) * blocks + blockIdx.x];
-      local[d] = lb;
-      running[d] = 0u;
-      gb += tot[j];
-      lb += cnt[j];
-    }
-  }
+  for (int i = t; i < kSortWaves * kBins / 2; i += kSortThreads)
+    reinterpret_cast<uint32_t *>(&wcnt[0][0])[i] = 0u;
   __syncthreads();
 
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // wave w ranks chunk keys [w * kWaveKeys, (w + 1) * kWaveKeys), 64 per
+  // round in input order, against its own counters (no barriers): piw = keys
+  // of the same digit before it in the wave. All loads are issued first.
+  uint32_t key[kKeysPerThread], val[kKeysPerThread], piw[kKeysPerThread];
+#pragma unroll
   for (int r = 0; r < kKeysPerThread; ++r) {
-    const int li = r * kSortThreads + t;  // chunk-local index (input order)
+    const int li = wave * kWaveKeys + r * 64 + lane;
     const bool valid = li < nblk;
-    const uint32_t key = valid ? load_key<FIRST>(keys_in, pos, dims, static_cast<size_t>(base + li))
-                               : 0u;
-    const uint32_t val =
-        valid ? (FIRST ? static_cast<uint32_t>(base + li) : vals_in[base + li]) : 0u;
-    const uint32_t d = (key >> shift) & (kBins - 1);
-    // lanes of this wave holding the same digit
+    const size_t gi = static_cast<size_t>(base + (valid ? li : 0));
+    if constexpr (FIRST) {
+      key[r] = valid ? load_key<true>(nullptr, pos, dims, gi) : 0u;
+      val[r] = static_cast<uint32_t>(gi);
+    } else {
+      key[r] = valid ? keys_in[gi] : 0u;
+      val[r] = valid ? vals_in[gi] : 0u;
+    }
+  }
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int r = 0; r < kKeysPerThread; ++r) {
+    const bool valid = wave * kWaveKeys + r * 64 + lane < nblk;
+    const uint32_t d = (key[r] >> shift) & (kBins - 1);
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
@@ -185,43 +174,63 @@ __global__ void __launch_bounds__(kSortThreads)
       peers &= bit ? m : ~m;
     }
     const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt_mask));
-    const bool leader = valid && rank == 0u;
-#pragma unroll
-    for (int w = 0; w < kSortWaves; ++w)
-#pragma unroll
-      for (int j = 0; j < BPT; ++j) wcnt[w][t * BPT + j] = 0;
-    __syncthreads();
-    if (leader) wcnt[wave][d] = static_cast<uint16_t>(__popcll(peers));
-    __syncthreads();
-    // per digit: exclusive offsets across waves, then advance the run
-#pragma unroll
-    for (int j = 0; j < BPT; ++j) {
-      const int dd = t * BPT + j;
-      uint32_t acc = running[dd];
-#pragma unroll
-      for (int w = 0; w < kSortWaves; ++w) {
-        const uint32_t c = wcnt[w][dd];
-        wcnt[w][dd] = static_cast<uint16_t>(acc);
-        acc += c;
-      }
-      running[dd] = acc;
-    }
-    __syncthreads();
-    if (valid) {
-      const uint32_t p = local[d] + wcnt[wave][d] + rank;
-      s_keys[p] = key;
-      s_vals[p] = val;
-    }
-    __syncthreads();
+    // every lane reads the wave's running count before the leader advances
+    // it (the LDS operations of one wave complete in program order)
+    const uint32_t c = valid ? wcnt[wave][d] : 0u;
+    piw[r] = c + rank;
+    if (valid && rank == 0u) wcnt[wave][d] = static_cast<uint16_t>(c + __popcll(peers));
   }
+  __syncthreads();
 
-  // write the locally sorted chunk: position j belongs to the digit run of
-  // s_keys[j]; its global slot is glob[d] + (j - local[d]).
+  // thread t owns digits [t*BPT, (t+1)*BPT): offsets across waves, the
+  // chunk's count, the run's start in the chunk and its global slot
+  // (exclusive scan of the digit totals plus this block's prefix in the digit)
+  uint32_t cnt[BPT], tot[BPT], sc = 0, st = 0;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    const int dd = t * BPT + j;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
+      const uint32_t c = wcnt[w][dd];
+      wcnt[w][dd] = static_cast<uint16_t>(acc);
+      acc += c;
+    }
+    cnt[j] = acc;
+    tot[j] = totals[dd];
+    sc += acc;
+    st += tot[j];
+  }
+  uint32_t all = 0;
+  uint32_t lb = block_excl_scan(sc, wsum, &all);
+  uint32_t gb = block_excl_scan(st, wsum, &all);
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    const int dd = t * BPT + j;
+    lstart[dd] = lb;
+    glob[dd] = gb + pre[static_cast<size_t>(dd) * blocks + blockIdx.x] - lb;  // modulo 2^32
+    lb += cnt[j];
+    gb += tot[j];
+  }
+  __syncthreads();
+
+  // sort the chunk in LDS (input order within each digit)
+#pragma unroll
+  for (int r = 0; r < kKeysPerThread; ++r) {
+    if (wave * kWaveKeys + r * 64 + lane < nblk) {
+      const uint32_t d = (key[r] >> shift) & (kBins - 1);
+      const uint32_t p = lstart[d] + wcnt[wave][d] + piw[r];
+      s_keys[p] = key[r];
+      s_vals[p] = val[r];
+    }
+  }
+  __syncthreads();
+
+  // consecutive threads write consecutive slots of a digit run
   for (int j = t; j < nblk; j += kSortThreads) {
-    const uint32_t key = s_keys[j];
-    const uint32_t d = (key >> shift) & (kBins - 1);
-    const uint32_t dst = glob[d] + (static_cast<uint32_t>(j) - local[d]);
-    keys_out[dst] = key;
+    const uint32_t k = s_keys[j];
+    const uint32_t dst = glob[(k >> shift) & (kBins - 1)] + static_cast<uint32_t>(j);
+    keys_out[dst] = k;
     vals_out[dst] = s_vals[j];
   }
 }
