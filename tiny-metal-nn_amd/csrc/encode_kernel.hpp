@@ -130,4 +130,74 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeA
   }
 }
 
+// Level-major variant for large tables: one thread per (point, level),
+// blockIdx.y = level, so the resident blocks gather from one level's slice of
+// the table at a time (a 2^22-entry level is 32 MB; all levels together do not
+// stay in the caches). Same arithmetic as encode_features_kernel; the thread
+// stores its level's F features into their X-tile quad (the whole quad for
+// F = 4, half of it for F = 2, one float for F = 1); the last level's threads
+// also zero the padding features, level 0's write the sorted position.
+template <int D, int F>
+__global__ void __launch_bounds__(kEncodeThreads) encode_level_kernel(EncodeArgs a) {
+  constexpr int C = 1 << D;  // corners per level
+  const int l = blockIdx.y;
+  const int i = blockIdx.x * kEncodeThreads + threadIdx.x;
+  if (i >= a.n_pad) return;
+  const bool valid = i < a.n;
+  float p[D];
+  const size_t src = valid ? (a.perm ? a.perm[i] : static_cast<uint32_t>(i)) : 0u;
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = valid ? a.pos[src * D + k] : 0.0f;
+  if (l == 0 && a.pos_out && valid)
+#pragma unroll
+    for (int k = 0; k < D; ++k) a.pos_out[static_cast<size_t>(i) * D + k] = p[k];
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  const Cell<D> c = cell_of<D>(p, a.res[l]);
+  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+  float v[C][F];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const float *e = a.table + (lbase + hash_corner<D>(co, tmask)) * F;
+    if constexpr (F == 1) {
+      v[k][0] = e[0];
+    } else if constexpr (F == 2) {
+      const f32x2 t = *reinterpret_cast<const f32x2 *>(e);
+      v[k][0] = t[0];
+      v[k][1] = t[1];
+    } else {
+      const f32x4 t = *reinterpret_cast<const f32x4 *>(e);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) v[k][f] = t[f];
+    }
+  }
+  float feat[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f) feat[f] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const float w = corner_weight<D>(wc);
+#pragma unroll
+    for (int f = 0; f < F; ++f) feat[f] = feat[f] + w * v[k][f];
+  }
+  const int f0 = l * F;  // the level's first feature
+  float *dst = a.xfeat + xtile_offset(i, f0 / 4, a.KT0) + f0 % 4;
+  if constexpr (F == 4) {
+    *reinterpret_cast<f32x4 *>(dst) = valid ? f32x4{feat[0], feat[1], feat[2], feat[3]}
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+  } else if constexpr (F == 2) {
+    *reinterpret_cast<f32x2 *>(dst) = valid ? f32x2{feat[0], feat[1]} : f32x2{0.f, 0.f};
+  } else {
+    *dst = valid ? feat[0] : 0.0f;
+  }
+  if (l == a.L - 1)
+    for (int f = a.L * F; f < 16 * a.KT0; ++f)
+      a.xfeat[xtile_offset(i, f / 4, a.KT0) + f % 4] = 0.0f;
+}
+
 }  // namespace tmnn_hip

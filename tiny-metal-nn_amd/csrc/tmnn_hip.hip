@@ -581,6 +581,13 @@ int ensure_image(tmnn_trainer *tr, KernelPlan &plan) {
 
 // Input features of n points at pos as X tiles in tr->xfeat; with perm,
 // point i is pos[perm[i]] and its position is also written to pos_out[i].
+// Hash-grid kernels walk the levels one at a time (level-major) when a
+// level's slice of the table exceeds 8 MB, else all levels per point.
+bool level_major(const tmnn_trainer *tr) {
+  return (static_cast<size_t>(tr->d.features_per_level) * 4u << tr->d.log2_hashmap_size) >
+         (8u << 20);
+}
+
 int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *perm = nullptr,
                   float *pos_out = nullptr) {
   EncodeArgs e{};
@@ -597,19 +604,29 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *per
   e.pos_out = pos_out;
   e.table = tr->params.as<float>();
   e.xfeat = tr->xfeat.as<float>();
-  const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads);
+  // level-major for large tables (the scatter's rule) when the positions are
+  // read in place; through a sort permutation every level would re-read them
+  // at random (measured slower than point-major)
+  const bool by_level = level_major(tr) && perm == nullptr;
+  const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads, by_level ? e.L : 1);
   hipStream_t st = tr->ctx->stream;
+#define TMNN_ENCODE(d, f)                                                                     \
+  if (by_level)                                                                               \
+    hipLaunchKernelGGL((encode_level_kernel<d, f>), grid, dim3(kEncodeThreads), 0, st, e);    \
+  else                                                                                        \
+    hipLaunchKernelGGL((encode_features_kernel<d, f>), grid, dim3(kEncodeThreads), 0, st, e);
   switch (tr->d.spatial_dims * 8 + tr->d.features_per_level) {
-    case 2 * 8 + 1: hipLaunchKernelGGL((encode_features_kernel<2, 1>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 2 * 8 + 2: hipLaunchKernelGGL((encode_features_kernel<2, 2>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 2 * 8 + 4: hipLaunchKernelGGL((encode_features_kernel<2, 4>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 3 * 8 + 1: hipLaunchKernelGGL((encode_features_kernel<3, 1>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 3 * 8 + 2: hipLaunchKernelGGL((encode_features_kernel<3, 2>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 3 * 8 + 4: hipLaunchKernelGGL((encode_features_kernel<3, 4>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 4 * 8 + 1: hipLaunchKernelGGL((encode_features_kernel<4, 1>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    case 4 * 8 + 2: hipLaunchKernelGGL((encode_features_kernel<4, 2>), grid, dim3(kEncodeThreads), 0, st, e); break;
-    default: hipLaunchKernelGGL((encode_features_kernel<4, 4>), grid, dim3(kEncodeThreads), 0, st, e); break;
+    case 2 * 8 + 1: TMNN_ENCODE(2, 1) break;
+    case 2 * 8 + 2: TMNN_ENCODE(2, 2) break;
+    case 2 * 8 + 4: TMNN_ENCODE(2, 4) break;
+    case 3 * 8 + 1: TMNN_ENCODE(3, 1) break;
+    case 3 * 8 + 2: TMNN_ENCODE(3, 2) break;
+    case 3 * 8 + 4: TMNN_ENCODE(3, 4) break;
+    case 4 * 8 + 1: TMNN_ENCODE(4, 1) break;
+    case 4 * 8 + 2: TMNN_ENCODE(4, 2) break;
+    default: TMNN_ENCODE(4, 4) break;
   }
+#undef TMNN_ENCODE
   TMNN_HIP_TRY(hipGetLastError());
   return TMNN_OK;
 }
@@ -732,8 +749,7 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
   s.mask = tr->mask[tr->mask_cur].as<uint8_t>();
   // point-major while a level's slice of the table is cache-sized, else
   // level-major (one level's slice at a time)
-  const bool by_level = (static_cast<size_t>(tr->d.features_per_level) * 4u
-                         << tr->d.log2_hashmap_size) > (8u << 20);
+  const bool by_level = level_major(tr);
   const dim3 grid((n + kScatterThreads - 1) / kScatterThreads, by_level ? tr->d.num_levels : 1);
   hipStream_t st = tr->ctx->stream;
 #define TMNN_SCATTER(d, f)                                                                   \
