@@ -30,6 +30,7 @@
 #include "sort.hpp"
 #include "step_kernel.hpp"
 #include "wide_kernel.hpp"
+#include "wide_train_kernel.hpp"
 
 using namespace tmnn_hip;
 
@@ -68,15 +69,17 @@ struct KernelChoice {
   bool wide = false;    // hidden width 128: the block-cooperative wide kernel
   bool xmem = false;    // input features from encode_features_kernel
   bool mlp = false;     // mlp_train_kernel (no activation staging in LDS)
+  bool wide_train = false;  // wide_train_kernel (fp16 training at width 128)
 };
 
-// Hidden width 128 (wide_kernel.hpp): instantiated for the BASELINE 4D shape
-// (16 levels x 2 features, 4 hidden layers) and a 3D two-layer shape.
+// Hidden width 128: instantiated for the BASELINE 4D shape (16 levels x 2
+// features, 4 hidden layers) and a 3D two-layer shape. fp16 training runs
+// wide_train_kernel (wide_train_kernel.hpp), the rest wide_kernel.
 KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
 #define TMNN_WIDE(d, f, nhl)                                                         \
   if (D == d && F == f && NHL == nhl) {                                              \
-    if (train) return {f16 ? wide_kernel<d, f, nhl, true, true, true>                \
-                           : wide_kernel<d, f, nhl, false, true, true>, false, true, true}; \
+    if (train && f16) return {wide_train_kernel<nhl>, false, true, true, false, true}; \
+    if (train) return {wide_kernel<d, f, nhl, false, true, true>, false, true, true}; \
     return {f16 ? wide_kernel<d, f, nhl, true, false, true>                          \
                 : wide_kernel<d, f, nhl, false, false, true>, false, true, true};    \
   }
@@ -188,6 +191,7 @@ struct KernelPlan {
   bool wide = false;       // block-cooperative hidden-128 kernel (4 waves, 128-point block tiles)
   bool xmem = false;       // features from encode_features_kernel (X tiles in xfeat)
   bool mlp = false;        // mlp_train_kernel
+  bool wide_train = false; // wide_train_kernel
   int max_blocks = 0;   // resident blocks on the whole device
 };
 
@@ -357,6 +361,7 @@ bool size_plan(const ModelShape &m, bool f16, bool train, int family, int lds_li
   out.wide = kc.wide;
   out.xmem = kc.xmem;
   out.mlp = kc.mlp;
+  out.wide_train = kc.wide_train;
   out.f16 = f16;
   out.train = train;
   *why = 0;
@@ -374,7 +379,7 @@ bool size_plan(const ModelShape &m, bool f16, bool train, int family, int lds_li
   } else if (out.wide) {
     const FieldLayout fl = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, m.mlp_count, f16, train, 1);
     out.wpb = kWideWaves;
-    out.lds = make_wide_layout(fl, f16, train).total;
+    out.lds = out.wide_train ? wide_train_lds(fl).total : make_wide_layout(fl, f16, train).total;
     out.image_bytes = static_cast<size_t>(fl.dw_off);
   } else {
     // Most waves per block whose LDS plan fits; failing that, move the dW

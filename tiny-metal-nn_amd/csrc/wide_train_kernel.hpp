@@ -1,0 +1,417 @@
+// wide_train_kernel.hpp -- fp16 training kernel of the hidden-width-128 MLP
+// (32 -> 128 x NHL -> M), on the scheme of
+// mlp_train_kernel (mlp_kernel.hpp): transposes on the matrix cores, owned
+// weight-gradient tiles accumulated in registers over all rounds, packed fp16
+// ReLU' factors, 16-byte lane-private LDS parking slots.
+//
+// Two things differ from the 64-wide kernel because a 128-wide layer's
+// operands are 4x larger:
+//  * weights: the split-fp16 forward fragments of one hidden layer (hi + lo,
+//    64 KB) plus the backward copy exceed what LDS can hold for every layer,
+//    so the block stages one layer's fragments at a time from the packed
+//    image (direct global-to-LDS loads, behind barriers);
+//  * activations: the packed fp16 activations of hidden layers 0 .. NHL-2
+//    (the D-layout B operands, 8 KB per tile and layer) go to global memory
+//    in the forward and come back in the backward, where they give both the
+//    ReLU' factors and (transposed on the matrix cores) the dW operands; the
+//    last hidden layer's stay in registers.
+//
+// Per round each of the four waves (one per SIMD) owns a 32-point tile. The
+// backward parks, per layer, every wave's transposed deltas and layer inputs;
+// after a barrier each wave accumulates the dW tiles it owns over all four
+// waves' points in wave order (deterministic, no cross-wave reduction), and
+// the owners write the block's partial row at the end. Numerics as
+// mlp_train_kernel: split-fp16 forward with the bias as the accumulator's
+// initial value, fp16 backward with a power-of-two loss scale, ReLU' from the
+// fp16 activation, bias gradients as MFMAs of an all-ones fragment.
+#pragma once
+
+#include "mlp_kernel.hpp"
+#include "wide_kernel.hpp"
+
+namespace tmnn_hip {
+
+// LDS plan of wide_train_kernel (bytes): one layer's staged weight fragments,
+// the biases of every layer (fp32, image order), the per-wave loss slots,
+// then per wave its parking slots (16 bytes per lane each): [0, 8) delta^T
+// tiles, [8, 16) layer-input^T tiles, 16 the output gradient^T.
+struct WideTrainLds {
+  int32_t bias, loss, park, park_bytes, total;
+};
+
+__host__ __device__ inline WideTrainLds wide_train_lds(const FieldLayout &s) {
+  WideTrainLds m;
+  m.bias = 2 * kWideHP * kWideHP * 2;  // a hidden layer's forward hi + lo fragments
+  m.loss = m.bias + round_up(s.res_off - s.bias_base, 16);
+  m.park = m.loss + 16 * 4;
+  m.park_bytes = (2 * kWideHT + 1) * 64 * 16;
+  m.total = m.park + kWideWaves * m.park_bytes;
+  return m;
+}
+
+template <int NHL>
+__global__ void __launch_bounds__(kWideWaves * 64)
+    __attribute__((amdgpu_waves_per_eu(1, 1))) wide_train_kernel(FieldArgs a) {
+  constexpr int HP = kWideHP;
+  constexpr int HT = HP / 16;  // unit tiles of a hidden layer
+  constexpr int HS = HT / 2;   // K steps over a hidden layer
+  constexpr int INP = 32;
+  constexpr int KT0 = INP / 16;
+  constexpr int XS = KT0 / 2;
+  constexpr int W = kWideWaves;
+  static_assert(NHL >= 2, "at least two hidden layers");
+  constexpr int kJobsOut = HT + 1;        // dW_out tiles (units x outputs) + b_out
+  constexpr int kJobsHid = HT * HT + HT;  // dW_k tiles + b_k tiles
+  constexpr int kJobs0 = KT0 * HT + HT;   // dW_0 tiles + b_0 tiles
+  constexpr int kSlotsOut = (kJobsOut + W - 1) / W;
+  constexpr int kSlotsHid = (kJobsHid + W - 1) / W;
+  constexpr int kSlots0 = (kJobs0 + W - 1) / W;
+  constexpr int kHSlot = HT;       // first layer-input^T slot
+  constexpr int kGSlot = 2 * HT;   // output gradient^T slot
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const FieldLayout s = make_layout(INP, HP, a.IN, a.H, NHL, a.M, a.mlp_count, true, true, 1);
+  const WideTrainLds ml = wide_train_lds(s);
+  copy_to_lds(smem + ml.bias, a.image + s.bias_base, s.res_off - s.bias_base);
+  // parked operands of absent tiles must be finite (they meet zero deltas)
+  for (int e = threadIdx.x; e < W * ml.park_bytes / 16; e += blockDim.x)
+    reinterpret_cast<uint4 *>(smem + ml.park)[e] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int p = lane & 15;
+  const int q = lane >> 4;
+  const bool wgrads = a.mode != kModeInputGrad;
+  unsigned char *park0 = smem + ml.park;
+  unsigned char *pk = park0 + wave * ml.park_bytes;
+  auto opnd = [&](int w, int slot) {
+    return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
+  };
+  auto bias_of = [&](int k) { return reinterpret_cast<const float *>(smem + ml.bias + k * HP * 4); };
+  // one layer's fragments into LDS offset 0 (everyone is done with the last ones)
+  auto stage = [&](int32_t off, int bytes) {
+    __syncthreads();
+    copy_to_lds(smem, a.image + off, bytes);
+    __syncthreads();
+  };
+  half8 sel_lo, sel_hi, ones;
+  selection_fragments(p, q, sel_lo, sel_hi);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = static_cast<_Float16>(1.0f);
+
+  f32x4 accO[kSlotsOut];
+  f32x4 accH[NHL - 1][kSlotsHid];
+  f32x4 acc0[kSlots0];
+#pragma unroll
+  for (int j = 0; j < kSlotsOut; ++j) accO[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < NHL - 1; ++k)
+#pragma unroll
+    for (int j = 0; j < kSlotsHid; ++j) accH[k][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kSlots0; ++j) acc0[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float lane_loss = 0.0f;
+  const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
+  half8 *act_store = reinterpret_cast<half8 *>(a.wide_act);
+  const bool has_target = a.mode != kModeInputGrad && a.target != nullptr;
+  const bool dx_vec = (a.IN & 3) == 0;
+  const int n_rounds = (a.n_tiles + W - 1) / W;
+
+  for (int round = blockIdx.x; round < n_rounds; round += gridDim.x) {
+    const int tile = round * W + wave;
+    const bool have = tile < a.n_tiles;  // waves past the batch park zero deltas
+    int pt[kNT];
+    bool valid[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      pt[nt] = tile * kTilePts + 16 * nt + p;
+      valid[nt] = have && pt[nt] < a.n;
+    }
+    f32x4 X[KT0][kNT];
+#pragma unroll
+    for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+        X[kt][nt] = have ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+    float Tv[kNT][4];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const uint32_t pr = valid[nt] ? static_cast<uint32_t>(pt[nt]) : 0u;
+      const size_t row = static_cast<size_t>(a.tgt_index ? a.tgt_index[pr] : pr) * a.M;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 4 * q + r;
+        const float v = has_target ? a.target[row + (o < a.M ? o : a.M - 1)] : 0.0f;
+        Tv[nt][r] = (valid[nt] && o < a.M) ? v : 0.0f;
+      }
+    }
+    // packed activations of hidden layer k of this tile in global memory
+    auto act_slot = [&](int k, int ks, int nt) {
+      return act_store + ((static_cast<size_t>(k) * a.n_tiles + (have ? tile : 0)) * (HS * kNT) +
+                          ks * kNT + nt) * 64 + lane;
+    };
+
+    // ---- forward, one layer's fragments in LDS at a time
+    f32x4 act[HT][kNT];
+    auto relu = [&]() {
+#pragma unroll
+      for (int mt = 0; mt < HT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) act[mt][nt][r] = relu_f32(act[mt][nt][r]);
+    };
+    {
+      // layer 0: forward hi and lo fragments
+      __syncthreads();
+      copy_to_lds(smem, a.image + s.fwd_off(0), INP * HP * 2);
+      copy_to_lds(smem + INP * HP * 2, a.image + s.fwd_lo_off(0), INP * HP * 2);
+      __syncthreads();
+      half8 bh[XS][kNT], bl[XS][kNT];
+      pack_split_tiles<KT0>(X, bh, bl);
+      mma_split_packed<XS, HT>(smem, smem + INP * HP * 2, bh, bl, bias_of(0), act, lane);
+      relu();
+    }
+    half8 fac[HS][kNT];  // ReLU' factors of the layer whose delta is formed next
+#pragma unroll
+    for (int k = 1; k <= NHL; ++k) {
+      half8 bh[HS][kNT], bl[HS][kNT];
+      pack_split_tiles<HT>(act, bh, bl);
+      if (k < NHL) {
+        if (have)
+#pragma unroll
+          for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) *act_slot(k - 1, ks, nt) = bh[ks][nt];
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_factors(bh[ks][nt]);
+      }
+      const int mout = k == NHL ? 16 : HP;
+      __syncthreads();
+      copy_to_lds(smem, a.image + s.fwd_off(k), HP * mout * 2);
+      copy_to_lds(smem + HP * mout * 2, a.image + s.fwd_lo_off(k), HP * mout * 2);
+      __syncthreads();
+      if (k < NHL) {
+        mma_split_packed<HS, HT>(smem, smem + HP * mout * 2, bh, bl, bias_of(k), act, lane);
+        relu();
+      } else {
+        f32x4 y[1][kNT];
+        mma_split_packed<HS, 1>(smem, smem + HP * mout * 2, bh, bl, bias_of(NHL), y, lane);
+        // loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
+        f32x4 g[2][kNT];
+        output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, g);
+        half8 gb[1][kNT];
+        pack_tiles<2>(g, gb);
+        {
+          half8 gT[2];
+          transpose_tiles<1>(gb, sel_lo, sel_hi, gT);
+          park(pk, kGSlot, lane, gT[0]);
+        }
+        {
+          half8 hT[HT];
+          transpose_tiles<HS>(bh, sel_lo, sel_hi, hT);
+#pragma unroll
+          for (int it = 0; it < HT; ++it) park(pk, kHSlot + it, lane, hT[it]);
+        }
+        // owners: dW_out (units x outputs) and b_out over the round's points
+        __syncthreads();
+        if (wgrads) {
+#pragma unroll 1
+          for (int w = 0; w < W; ++w)  // waves outermost: one wave's operands live
+#pragma unroll
+            for (int j = 0; j < kSlotsOut; ++j) {
+              const int job = wave + W * j;
+              if (job < kJobsOut)
+                accO[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    job < HT ? opnd(w, kHSlot + job) : ones, opnd(w, kGSlot), accO[j], 0, 0, 0);
+            }
+        }
+        // delta of the last hidden layer (backward fragments of the output layer)
+        stage(s.bwd_off(NHL), HP * 32 * 2);
+        mma_packed<1, HT>(smem, gb, act, lane);  // act now holds W_out g (pre-mask)
+      }
+    }
+
+    // ---- hidden layers NHL-1 .. 1: delta_k parked over slots [0, 8), the
+    // layer input h_{k-1} (reloaded, transposed) over [8, 16); owners add
+    // dW_k / b_k; then delta_{k-1} on the staged backward fragments
+#pragma unroll
+    for (int k = NHL - 1; k >= 0; --k) {
+      half8 b[HS][kNT];
+      pack_tiles<HT>(act, b);
+#pragma unroll
+      for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = b[ks][nt] * fac[ks][nt];
+      {
+        half8 dT[HT];
+        transpose_tiles<HS>(b, sel_lo, sel_hi, dT);
+#pragma unroll
+        for (int ut = 0; ut < HT; ++ut) park(pk, ut, lane, dT[ut]);
+      }
+      if (k > 0) {
+        half8 hb[HS][kNT];
+#pragma unroll
+        for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt)
+            hb[ks][nt] = have ? *act_slot(k - 1, ks, nt) : half8{};
+        half8 hT[HT];
+        transpose_tiles<HS>(hb, sel_lo, sel_hi, hT);
+#pragma unroll
+        for (int it = 0; it < HT; ++it) park(pk, kHSlot + it, lane, hT[it]);
+#pragma unroll
+        for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_factors(hb[ks][nt]);
+      } else {
+        // the input features again (L2-resident): not kept live across the round
+        f32x4 X0[KT0][kNT];
+#pragma unroll
+        for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt)
+            X0[kt][nt] = have ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+        half8 bh[XS][kNT], bl[XS][kNT];
+        pack_split_tiles<KT0>(X0, bh, bl);
+        half8 xT[KT0];
+        transpose_tiles<XS>(bh, sel_lo, sel_hi, xT);
+#pragma unroll
+        for (int ft = 0; ft < KT0; ++ft) park(pk, kHSlot + ft, lane, xT[ft]);
+      }
+      __syncthreads();
+      if (wgrads) {
+        // waves outermost (not unrolled): one wave's operands live at a
+        // time; every accumulator still adds the waves in order
+        if (k > 0) {
+#pragma unroll 1
+          for (int w = 0; w < W; ++w)
+#pragma unroll
+            for (int j = 0; j < kSlotsHid; ++j) {
+              const int job = wave + W * j;
+              if (job < kJobsHid) {
+                // job < HT*HT: dW tile (it, ut) = (job / HT, job % HT); else bias tile
+                const int it = job / HT, ut = job < HT * HT ? job % HT : job - HT * HT;
+                accH[k - 1][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    job < HT * HT ? opnd(w, kHSlot + it) : ones, opnd(w, ut), accH[k - 1][j], 0,
+                    0, 0);
+              }
+            }
+        } else {
+#pragma unroll 1
+          for (int w = 0; w < W; ++w)
+#pragma unroll
+            for (int j = 0; j < kSlots0; ++j) {
+              const int job = wave + W * j;
+              if (job < kJobs0) {
+                const int ft = job / HT, ut = job < KT0 * HT ? job % HT : job - KT0 * HT;
+                acc0[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    job < KT0 * HT ? opnd(w, kHSlot + ft) : ones, opnd(w, ut), acc0[j], 0, 0, 0);
+              }
+            }
+        }
+      }
+      if (k > 0) {
+        stage(s.bwd_off(k), HP * HP * 2);
+        mma_packed<HS, HT>(smem, b, act, lane);  // W_k delta_k (pre-mask)
+      } else {
+        stage(s.bwd_off(0), INP * HP * 2);
+        f32x4 dx[KT0][kNT];
+        mma_packed<HS, KT0>(smem, b, dx, lane);
+        if (have) {
+          // rows past the batch exist (the buffer is padded to whole tiles)
+#pragma unroll
+          for (int nt = 0; nt < kNT; ++nt) {
+            float *row = a.dx_out + static_cast<size_t>(pt[nt]) * a.IN;
+#pragma unroll
+            for (int kt = 0; kt < KT0; ++kt) {
+              const int f0 = 16 * kt + 4 * q;
+              f32x4 v = dx[kt][nt];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) v[r] = v[r] * a.inv_loss_scale;
+              if (dx_vec) {
+                if (f0 < a.IN) *reinterpret_cast<f32x4 *>(row + f0) = v;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  if (f0 + r < a.IN) row[f0 + r] = v[r];
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+
+  if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
+  // ---- loss partial of the block (wave order)
+  float v = lane_loss;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  float *lred = reinterpret_cast<float *>(smem + ml.loss);
+  __syncthreads();
+  if (lane == 0) lred[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.0f;
+    for (int w = 0; w < W; ++w) t += lred[w];
+    a.loss_partials[blockIdx.x] = t;
+  }
+  // ---- owners write their tiles of the block's partial row (reference layout)
+  float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
+  const float sc = a.inv_loss_scale;
+  const int H = a.H, IN = a.IN, M = a.M;
+#pragma unroll
+  for (int j = 0; j < kSlotsOut; ++j) {
+    const int job = wave + W * j;
+    if (job < HT) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int u = 16 * job + 4 * q + r;
+        if (u < H && p < M) dst[s.w_off(NHL) + u * M + p] = accO[j][r] * sc;
+      }
+    } else if (job == HT && q == 0 && p < M) {
+      dst[s.b_off(NHL) + p] = accO[j][0] * sc;
+    }
+  }
+#pragma unroll
+  for (int k = 1; k < NHL; ++k)
+#pragma unroll
+    for (int j = 0; j < kSlotsHid; ++j) {
+      const int job = wave + W * j;
+      if (job < HT * HT) {
+        const int it = job / HT, ut = job % HT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * it + 4 * q + r, u = 16 * ut + p;
+          if (i < H && u < H) dst[s.w_off(k) + i * H + u] = accH[k - 1][j][r] * sc;
+        }
+      } else if (job < kJobsHid && q == 0) {
+        const int u = 16 * (job - HT * HT) + p;
+        if (u < H) dst[s.b_off(k) + u] = accH[k - 1][j][0] * sc;
+      }
+    }
+#pragma unroll
+  for (int j = 0; j < kSlots0; ++j) {
+    const int job = wave + W * j;
+    if (job < KT0 * HT) {
+      const int ft = job / HT, ut = job % HT;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int f = 16 * ft + 4 * q + r, u = 16 * ut + p;
+        if (f < IN && u < H) dst[s.w_off(0) + f * H + u] = acc0[j][r] * sc;
+      }
+    } else if (job < kJobs0 && q == 0) {
+      const int u = 16 * (job - KT0 * HT) + p;
+      if (u < H) dst[s.b_off(0) + u] = acc0[j][0] * sc;
+    }
+  }
+}
+
+}  // namespace tmnn_hip
