@@ -23,7 +23,10 @@
 // the owners write the block's partial row at the end. Numerics as
 // mlp_train_kernel: split-fp16 forward with the bias as the accumulator's
 // initial value, fp16 backward with a power-of-two loss scale, ReLU' from the
-// fp16 activation, bias gradients as MFMAs of an all-ones fragment.
+// fp16 activation. Bias gradients are fp32 sums of the parked fp16 delta^T
+// tiles (v_dot2 against ones; the owner of unit tile ut is wave ut % 4, the
+// four lanes of a unit are added at the end in a fixed order), which keeps
+// them out of the MFMA accumulators.
 #pragma once
 
 #include "mlp_kernel.hpp"
@@ -60,9 +63,10 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   constexpr int XS = KT0 / 2;
   constexpr int W = kWideWaves;
   static_assert(NHL >= 2, "at least two hidden layers");
-  constexpr int kJobsOut = HT + 1;        // dW_out tiles (units x outputs) + b_out
-  constexpr int kJobsHid = HT * HT + HT;  // dW_k tiles + b_k tiles
-  constexpr int kJobs0 = KT0 * HT + HT;   // dW_0 tiles + b_0 tiles
+  constexpr int kJobsOut = HT;        // dW_out tiles (units x outputs)
+  constexpr int kJobsHid = HT * HT;   // dW_k tiles
+  constexpr int kJobs0 = KT0 * HT;    // dW_0 tiles
+  constexpr int kBiasTiles = HT / W;  // owned bias unit tiles per layer: ut = wave + W j
   constexpr int kSlotsOut = (kJobsOut + W - 1) / W;
   constexpr int kSlotsHid = (kJobsHid + W - 1) / W;
   constexpr int kSlots0 = (kJobs0 + W - 1) / W;
@@ -95,14 +99,29 @@ __global__ void __launch_bounds__(kWideWaves * 64)
     copy_to_lds(smem, a.image + off, bytes);
     __syncthreads();
   };
-  half8 sel_lo, sel_hi, ones;
+  half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ones[j] = static_cast<_Float16>(1.0f);
 
   f32x4 accO[kSlotsOut];
   f32x4 accH[NHL - 1][kSlotsHid];
   f32x4 acc0[kSlots0];
+  float bsO = 0.0f;                       // output bias (wave 0): lane partial sums
+  float bsH[NHL - 1][kBiasTiles];         // hidden biases of the owned unit tiles
+  float bs0[kBiasTiles];
+#pragma unroll
+  for (int j = 0; j < kBiasTiles; ++j) {
+    bs0[j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NHL - 1; ++k) bsH[k][j] = 0.0f;
+  }
+  const half2v one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  // partial sum += the 8 fp16 values of a parked tile of this lane
+  auto add8 = [&](float acc, half8 v) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_fdot2(half2v{v[2 * j], v[2 * j + 1]}, one2, acc, false);
+    return acc;
+  };
 #pragma unroll
   for (int j = 0; j < kSlotsOut; ++j) accO[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -227,8 +246,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
             for (int j = 0; j < kSlotsOut; ++j) {
               const int job = wave + W * j;
               if (job < kJobsOut)
-                accO[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    job < HT ? opnd(w, kHSlot + job) : ones, opnd(w, kGSlot), accO[j], 0, 0, 0);
+                accO[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(opnd(w, kHSlot + job),
+                                                                 opnd(w, kGSlot), accO[j], 0, 0, 0);
+              if (j == 0 && wave == 0) bsO = add8(bsO, opnd(w, kGSlot));
             }
         }
         // delta of the last hidden layer (backward fragments of the output layer)
@@ -294,26 +314,22 @@ __global__ void __launch_bounds__(kWideWaves * 64)
           for (int w = 0; w < W; ++w)
 #pragma unroll
             for (int j = 0; j < kSlotsHid; ++j) {
-              const int job = wave + W * j;
-              if (job < kJobsHid) {
-                // job < HT*HT: dW tile (it, ut) = (job / HT, job % HT); else bias tile
-                const int it = job / HT, ut = job < HT * HT ? job % HT : job - HT * HT;
+              const int job = wave + W * j;  // dW tile (it, ut) = (job / HT, job % HT)
+              if (job < kJobsHid)
                 accH[k - 1][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    job < HT * HT ? opnd(w, kHSlot + it) : ones, opnd(w, ut), accH[k - 1][j], 0,
-                    0, 0);
-              }
+                    opnd(w, kHSlot + job / HT), opnd(w, job % HT), accH[k - 1][j], 0, 0, 0);
+              if (j < kBiasTiles) bsH[k - 1][j] = add8(bsH[k - 1][j], opnd(w, wave + W * j));
             }
         } else {
 #pragma unroll 1
           for (int w = 0; w < W; ++w)
 #pragma unroll
             for (int j = 0; j < kSlots0; ++j) {
-              const int job = wave + W * j;
-              if (job < kJobs0) {
-                const int ft = job / HT, ut = job < KT0 * HT ? job % HT : job - KT0 * HT;
+              const int job = wave + W * j;  // dW tile (ft, ut) = (job / HT, job % HT)
+              if (job < kJobs0)
                 acc0[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    job < KT0 * HT ? opnd(w, kHSlot + ft) : ones, opnd(w, ut), acc0[j], 0, 0, 0);
-              }
+                    opnd(w, kHSlot + job / HT), opnd(w, job % HT), acc0[j], 0, 0, 0);
+              if (j < kBiasTiles) bs0[j] = add8(bs0[j], opnd(w, wave + W * j));
             }
         }
       }
@@ -376,9 +392,16 @@ __global__ void __launch_bounds__(kWideWaves * 64)
         const int u = 16 * job + 4 * q + r;
         if (u < H && p < M) dst[s.w_off(NHL) + u * M + p] = accO[j][r] * sc;
       }
-    } else if (job == HT && q == 0 && p < M) {
-      dst[s.b_off(NHL) + p] = accO[j][0] * sc;
     }
+  }
+  // bias of unit 16 ut + p: the four lanes p + 16 q, added in a fixed order
+  auto lane_total = [&](float v) {
+    v = v + __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+  };
+  {
+    const float t = lane_total(bsO);
+    if (wave == 0 && q == 0 && p < M) dst[s.b_off(NHL) + p] = t * sc;
   }
 #pragma unroll
   for (int k = 1; k < NHL; ++k)
@@ -392,9 +415,11 @@ __global__ void __launch_bounds__(kWideWaves * 64)
           const int i = 16 * it + 4 * q + r, u = 16 * ut + p;
           if (i < H && u < H) dst[s.w_off(k) + i * H + u] = accH[k - 1][j][r] * sc;
         }
-      } else if (job < kJobsHid && q == 0) {
-        const int u = 16 * (job - HT * HT) + p;
-        if (u < H) dst[s.b_off(k) + u] = accH[k - 1][j][0] * sc;
+      }
+      if (j < kBiasTiles) {
+        const float t = lane_total(bsH[k - 1][j]);
+        const int u = 16 * (wave + W * j) + p;
+        if (q == 0 && u < H) dst[s.b_off(k) + u] = t * sc;
       }
     }
 #pragma unroll
@@ -407,9 +432,11 @@ __global__ void __launch_bounds__(kWideWaves * 64)
         const int f = 16 * ft + 4 * q + r, u = 16 * ut + p;
         if (f < IN && u < H) dst[s.w_off(0) + f * H + u] = acc0[j][r] * sc;
       }
-    } else if (job < kJobs0 && q == 0) {
-      const int u = 16 * (job - KT0 * HT) + p;
-      if (u < H) dst[s.b_off(0) + u] = acc0[j][0] * sc;
+    }
+    if (j < kBiasTiles) {
+      const float t = lane_total(bs0[j]);
+      const int u = 16 * (wave + W * j) + p;
+      if (q == 0 && u < H) dst[s.b_off(0) + u] = t * sc;
     }
   }
 }
