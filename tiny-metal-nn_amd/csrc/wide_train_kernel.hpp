@@ -93,11 +93,52 @@ __global__ void __launch_bounds__(kWideWaves * 64)
     return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
   };
   auto bias_of = [&](int k) { return reinterpret_cast<const float *>(smem + ml.bias + k * HP * 4); };
-  // one layer's fragments into LDS offset 0 (everyone is done with the last ones)
-  auto stage = [&](int32_t off, int bytes) {
+  // Weight stages, double-buffered: a round walks 3 NHL + 1 stages (below),
+  // stage i in buffer (i + par) & 1 of two 32 KB buffers. At each stage
+  // boundary the block waits for its loads and meets at one barrier, which
+  // both publishes stage i and retires every read of the other buffer
+  // (stage i - 1); then the loads of stage i + 1 are issued into that buffer
+  // and run under stage i's products.
+  constexpr int kBuf = HP * HP * 2;
+  constexpr int kStages = 3 * NHL + 1;
+  int par = 0;
+  auto buf = [&](int i) { return smem + ((i + par) & 1) * kBuf; };
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  auto fetch = [&](unsigned char *dst, int32_t off, int bytes) {  // whole 4 KB groups
+    // an opaque image base: the addresses are formed here, not hoisted out
+    // of the round loop into registers held across it
+    const unsigned char *img = a.image;
+    asm volatile("" : "+s"(img));
+    for (int j = 0; j < (bytes >> 12); ++j) {
+      const int c = wave_s + W * j;  // 1 KB chunk of this wave
+      __builtin_amdgcn_global_load_lds(img + off + (c << 10) + lane * 16,
+                                       (__attribute__((address_space(3))) void *)(dst + (c << 10)),
+                                       16, 0, 0);
+    }
+  };
+  auto boundary = [&]() {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads (direct-to-LDS included) landed
     __syncthreads();
-    copy_to_lds(smem, a.image + off, bytes);
-    __syncthreads();
+  };
+  // stage i of a round: 0 F0 (hi | lo), 2k - 1 and 2k the unit tiles [0, 4) and
+  // [4, 8) of F_k (hi | lo, 1 <= k < NHL), 2 NHL - 1 F_out (hi | lo), 3 NHL - k
+  // B_k (NHL >= k >= 0): F forward fragments, B backward fragments
+  auto fetch_stage = [&](int i) {
+    unsigned char *d = buf(i);
+    if (i == 0 || i == kStages) {  // kStages: the next round's stage 0
+      fetch(d, s.fwd_off(0), INP * HP * 2);
+      fetch(d + INP * HP * 2, s.fwd_lo_off(0), INP * HP * 2);
+    } else if (i < 2 * NHL - 1) {
+      const int k = (i + 1) / 2, part = (i + 1) % 2 * (kBuf / 2);
+      fetch(d, s.fwd_off(k) + part, kBuf / 2);
+      fetch(d + kBuf / 2, s.fwd_lo_off(k) + part, kBuf / 2);
+    } else if (i == 2 * NHL - 1) {
+      fetch(d, s.fwd_off(NHL), HP * 16 * 2);
+      fetch(d + HP * 16 * 2, s.fwd_lo_off(NHL), HP * 16 * 2);
+    } else {
+      const int k = 3 * NHL - i;
+      fetch(d, s.bwd_off(k), k == NHL ? HP * 32 * 2 : k == 0 ? INP * HP * 2 : kBuf);
+    }
   };
   half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
@@ -137,6 +178,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   const bool dx_vec = (a.IN & 3) == 0;
   const int n_rounds = (a.n_tiles + W - 1) / W;
 
+  if (static_cast<int>(blockIdx.x) < n_rounds) fetch_stage(0);
   for (int round = blockIdx.x; round < n_rounds; round += gridDim.x) {
     const int tile = round * W + wave;
     const bool have = tile < a.n_tiles;  // waves past the batch park zero deltas
@@ -183,14 +225,12 @@ __global__ void __launch_bounds__(kWideWaves * 64)
           for (int r = 0; r < 4; ++r) act[mt][nt][r] = relu_f32(act[mt][nt][r]);
     };
     {
-      // layer 0: forward hi and lo fragments
-      __syncthreads();
-      copy_to_lds(smem, a.image + s.fwd_off(0), INP * HP * 2);
-      copy_to_lds(smem + INP * HP * 2, a.image + s.fwd_lo_off(0), INP * HP * 2);
-      __syncthreads();
+      // layer 0: forward hi and lo fragments (stage 0)
+      boundary();
+      fetch_stage(1);
       half8 bh[XS][kNT], bl[XS][kNT];
       pack_split_tiles<KT0>(X, bh, bl);
-      mma_split_packed<XS, HT>(smem, smem + INP * HP * 2, bh, bl, bias_of(0), act, lane);
+      mma_split_packed<XS, HT>(buf(0), buf(0) + INP * HP * 2, bh, bl, bias_of(0), act, lane);
       relu();
     }
     half8 fac[HS][kNT];  // ReLU' factors of the layer whose delta is formed next
@@ -199,28 +239,45 @@ __global__ void __launch_bounds__(kWideWaves * 64)
       half8 bh[HS][kNT], bl[HS][kNT];
       pack_split_tiles<HT>(act, bh, bl);
       if (k < NHL) {
-        if (have)
+        // unit tiles [0, 4) on stage 2k - 1, then [4, 8) on stage 2k
+        boundary();
+        fetch_stage(2 * k);
+        if (have)  // after the fetch: the stores retire under the products
 #pragma unroll
           for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
             for (int nt = 0; nt < kNT; ++nt) *act_slot(k - 1, ks, nt) = bh[ks][nt];
+        {
+          f32x4 part[HT / 2][kNT];
+          mma_split_packed<HS, HT / 2>(buf(2 * k - 1), buf(2 * k - 1) + kBuf / 2, bh, bl,
+                                       bias_of(k), part, lane);
+#pragma unroll
+          for (int mt = 0; mt < HT / 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) act[mt][nt] = part[mt][nt];
+        }
+        boundary();
+        fetch_stage(2 * k + 1);
+        {
+          f32x4 part[HT / 2][kNT];
+          mma_split_packed<HS, HT / 2>(buf(2 * k), buf(2 * k) + kBuf / 2, bh, bl,
+                                       bias_of(k) + HP / 2, part, lane);
+#pragma unroll
+          for (int mt = 0; mt < HT / 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) act[HT / 2 + mt][nt] = part[mt][nt];
+        }
+        relu();
       } else {
 #pragma unroll
         for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
           for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_factors(bh[ks][nt]);
-      }
-      const int mout = k == NHL ? 16 : HP;
-      __syncthreads();
-      copy_to_lds(smem, a.image + s.fwd_off(k), HP * mout * 2);
-      copy_to_lds(smem + HP * mout * 2, a.image + s.fwd_lo_off(k), HP * mout * 2);
-      __syncthreads();
-      if (k < NHL) {
-        mma_split_packed<HS, HT>(smem, smem + HP * mout * 2, bh, bl, bias_of(k), act, lane);
-        relu();
-      } else {
+        boundary();  // stage 2 NHL - 1: F_out
+        fetch_stage(2 * NHL);
         f32x4 y[1][kNT];
-        mma_split_packed<HS, 1>(smem, smem + HP * mout * 2, bh, bl, bias_of(NHL), y, lane);
+        mma_split_packed<HS, 1>(buf(2 * NHL - 1), buf(2 * NHL - 1) + HP * 16 * 2, bh, bl,
+                                bias_of(NHL), y, lane);
         // loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
         f32x4 g[2][kNT];
         output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, g);
@@ -237,8 +294,10 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
           for (int it = 0; it < HT; ++it) park(pk, kHSlot + it, lane, hT[it]);
         }
-        // owners: dW_out (units x outputs) and b_out over the round's points
-        __syncthreads();
+        // owners: dW_out (units x outputs) and b_out over the round's points;
+        // the boundary publishes the parks and stage 2 NHL (B_out)
+        boundary();
+        fetch_stage(2 * NHL + 1);
         if (wgrads) {
 #pragma unroll 1
           for (int w = 0; w < W; ++w)  // waves outermost: one wave's operands live
@@ -252,8 +311,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
             }
         }
         // delta of the last hidden layer (backward fragments of the output layer)
-        stage(s.bwd_off(NHL), HP * 32 * 2);
-        mma_packed<1, HT>(smem, gb, act, lane);  // act now holds W_out g (pre-mask)
+        mma_packed<1, HT>(buf(2 * NHL), gb, act, lane);  // act now holds W_out g (pre-mask)
       }
     }
 
@@ -264,6 +322,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
     for (int k = NHL - 1; k >= 0; --k) {
       half8 b[HS][kNT];
       pack_tiles<HT>(act, b);
+      __syncthreads();  // every wave is done with the last layer's parked operands
 #pragma unroll
       for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
@@ -305,7 +364,13 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
         for (int ft = 0; ft < KT0; ++ft) park(pk, kHSlot + ft, lane, xT[ft]);
       }
-      __syncthreads();
+      // stage 3 NHL - k (B_k) and the parks published; the next stage is
+      // B_{k-1}, or the next round's F0
+      boundary();
+      if (k > 0)
+        fetch_stage(3 * NHL - k + 1);
+      else if (round + static_cast<int>(gridDim.x) < n_rounds)
+        fetch_stage(kStages);
       if (wgrads) {
         // waves outermost (not unrolled): one wave's operands live at a
         // time; every accumulator still adds the waves in order
@@ -334,12 +399,10 @@ __global__ void __launch_bounds__(kWideWaves * 64)
         }
       }
       if (k > 0) {
-        stage(s.bwd_off(k), HP * HP * 2);
-        mma_packed<HS, HT>(smem, b, act, lane);  // W_k delta_k (pre-mask)
+        mma_packed<HS, HT>(buf(3 * NHL - k), b, act, lane);  // W_k delta_k (pre-mask)
       } else {
-        stage(s.bwd_off(0), INP * HP * 2);
         f32x4 dx[KT0][kNT];
-        mma_packed<HS, KT0>(smem, b, dx, lane);
+        mma_packed<HS, KT0>(buf(3 * NHL), b, dx, lane);
         if (have) {
           // rows past the batch exist (the buffer is padded to whole tiles)
 #pragma unroll
@@ -363,6 +426,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
         }
       }
     }
+    par ^= kStages & 1;  // the next round's stage 0 is this round's stage kStages
   }
 
   if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
