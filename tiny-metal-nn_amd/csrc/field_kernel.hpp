@@ -244,15 +244,25 @@ __device__ __forceinline__ void layer_mma(const unsigned char *frag,
 
 // fp16 split of two D-layout tiles: hi = fp16(v), lo = fp16(v - hi). hi*hi
 // products are exact in the fp32 accumulator and hi + lo carries ~22 bits.
+// v - hi is exact in fp32, so it is formed as fma(hi, m1, v) with m1 = -1
+// held opaque in a scalar register: the compiler then selects v_fma_mix,
+// which reads hi straight out of the packed pair (one v_cvt_pk per pair for
+// hi, no separate fp16 -> fp32 conversions), with bit-identical results.
 __device__ __forceinline__ void pack8_split(f32x4 a, f32x4 b, half8 &hi, half8 &lo) {
+  float m1 = -1.0f;
+  asm volatile("" : "+s"(m1));  // emits nothing; keeps the fma from folding into a subtraction
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const _Float16 ha = static_cast<_Float16>(a[r]);
-    const _Float16 hb = static_cast<_Float16>(b[r]);
-    hi[r] = ha;
-    hi[r + 4] = hb;
-    lo[r] = static_cast<_Float16>(a[r] - static_cast<float>(ha));
-    lo[r + 4] = static_cast<_Float16>(b[r] - static_cast<float>(hb));
+  for (int r = 0; r < 4; r += 2) {
+    const half2v ha = __builtin_convertvector(f32x2{a[r], a[r + 1]}, half2v);
+    const half2v hb = __builtin_convertvector(f32x2{b[r], b[r + 1]}, half2v);
+    hi[r] = ha[0];
+    hi[r + 1] = ha[1];
+    hi[r + 4] = hb[0];
+    hi[r + 5] = hb[1];
+    lo[r] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(ha[0]), m1, a[r]));
+    lo[r + 1] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(ha[1]), m1, a[r + 1]));
+    lo[r + 4] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(hb[0]), m1, b[r]));
+    lo[r + 5] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(hb[1]), m1, b[r + 1]));
   }
 }
 

@@ -50,17 +50,19 @@ __host__ __device__ constexpr int mlp_waves(int INP, int NHL) {
 }
 
 // LDS plan of mlp_train_kernel (bytes): the packed weight image, the per-wave
-// loss slots, then per wave its parking slots (16 bytes per lane each):
-// [0, KT0) input features, KT0 + k * HT + t hidden layer k (then delta_k),
-// KT0 + NHL * HT the output gradient.
+// loss slots, one slot of fp16 ones (the bias jobs' operand), then per wave
+// its parking slots (16 bytes per lane each): [0, KT0) input features,
+// KT0 + k * HT + t hidden layer k (then delta_k), KT0 + NHL * HT the output
+// gradient.
 struct MlpLds {
-  int32_t loss, park, park_bytes, total;
+  int32_t loss, ones, park, park_bytes, total;
 };
 
 __host__ __device__ inline MlpLds mlp_lds(const FieldLayout &s, int waves) {
   MlpLds m;
   m.loss = s.dw_off;
-  m.park = m.loss + 16 * 4;
+  m.ones = m.loss + 16 * 4;
+  m.park = m.ones + 64 * 16;
   m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + 1) * 64 * 16;
   m.total = m.park + waves * m.park_bytes;
   return m;
@@ -192,6 +194,18 @@ __device__ __forceinline__ half8 relu_factors(half8 h) {
 // max(x, x)); -0 maps to +0
 __device__ __forceinline__ float relu_f32(float x) { return __builtin_elementwise_maximum(x, 0.0f); }
 
+// Scheduling hint for an owner's run of W products: the LDS reads of four
+// products' operands, then those four MFMAs, and so on, so the reads are in
+// flight together instead of one read, one wait, one product at a time.
+template <int W>
+__device__ __forceinline__ void owner_schedule() {
+#pragma unroll
+  for (int g = 0; g < W / 4; ++g) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+  }
+}
+
 template <int HP, int INP, int NHL, int W = mlp_waves(INP, NHL)>
 __global__ void __launch_bounds__(W * 64)
     __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) mlp_train_kernel(FieldArgs a) {
@@ -216,6 +230,9 @@ __global__ void __launch_bounds__(W * 64)
   // parked operands of absent tiles must be finite (they meet zero deltas)
   for (int e = threadIdx.x; e < W * ml.park_bytes / 16; e += blockDim.x)
     reinterpret_cast<uint4 *>(smem + ml.park)[e] = make_uint4(0u, 0u, 0u, 0u);
+  if (threadIdx.x < 64)
+    reinterpret_cast<uint4 *>(smem + ml.ones)[threadIdx.x] =
+        make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);  // fp16 1.0 pairs
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -231,10 +248,14 @@ __global__ void __launch_bounds__(W * 64)
   auto opnd = [&](int w, int slot) {
     return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
   };
-  half8 sel_lo, sel_hi, ones;
+  // wave w's slot, or the ones slot for a bias job: a select of the address,
+  // so an owner's loads and MFMAs form one branch-free run
+  auto opnd_or_ones = [&](bool ones, int w, int slot) {
+    const int off = ones ? ml.ones : ml.park + w * ml.park_bytes + slot * 64 * 16;
+    return *reinterpret_cast<const half8 *>(smem + off + lane * 16);
+  };
+  half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ones[j] = static_cast<_Float16>(1.0f);
 
   f32x4 accO[kSlotsOut];
   f32x4 accH[NHL > 1 ? NHL - 1 : 1][kSlotsHid];
@@ -400,12 +421,17 @@ __global__ void __launch_bounds__(W * 64)
       for (int j = 0; j < kSlotsOut; ++j) {
         const int job = wave + W * j;
         if (job < kJobsOut) {
+          half8 oa[W], ob[W];  // every operand requested before the first product
+#pragma unroll
+          for (int w = 0; w < W; ++w) {
+            oa[w] = opnd_or_ones(job >= HT, w, hslot(NHL - 1, job));
+            ob[w] = opnd(w, kGSlot);
+          }
           f32x4 acc = accO[j];
 #pragma unroll
-          for (int w = 0; w < W; ++w)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                job < HT ? opnd(w, hslot(NHL - 1, job)) : ones, opnd(w, kGSlot), acc, 0, 0, 0);
+          for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
           accO[j] = acc;
+          owner_schedule<W>();
         }
       }
     }
@@ -463,12 +489,17 @@ __global__ void __launch_bounds__(W * 64)
             if (job < kJobsHid) {
               // job < HT*HT: dW tile (it, ut) = (job / HT, job % HT); else bias tile
               const int it = job / HT, ut = job < HT * HT ? job % HT : job - HT * HT;
+              half8 oa[W], ob[W];
+#pragma unroll
+              for (int w = 0; w < W; ++w) {
+                oa[w] = opnd_or_ones(job >= HT * HT, w, hslot(k - 1, it));
+                ob[w] = opnd(w, hslot(k, ut));
+              }
               f32x4 acc = accH[k - 1][j];
 #pragma unroll
-              for (int w = 0; w < W; ++w)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    job < HT * HT ? opnd(w, hslot(k - 1, it)) : ones, opnd(w, hslot(k, ut)), acc, 0, 0, 0);
+              for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
               accH[k - 1][j] = acc;
+              owner_schedule<W>();
             }
           }
         } else {
@@ -477,12 +508,17 @@ __global__ void __launch_bounds__(W * 64)
             const int job = wave + W * j;
             if (job < kJobs0) {
               const int ft = job / HT, ut = job < KT0 * HT ? job % HT : job - KT0 * HT;
+              half8 oa[W], ob[W];
+#pragma unroll
+              for (int w = 0; w < W; ++w) {
+                oa[w] = opnd_or_ones(job >= KT0 * HT, w, ft);
+                ob[w] = opnd(w, hslot(0, ut));
+              }
               f32x4 acc = acc0[j];
 #pragma unroll
-              for (int w = 0; w < W; ++w)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    job < KT0 * HT ? opnd(w, ft) : ones, opnd(w, hslot(0, ut)), acc, 0, 0, 0);
+              for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
               acc0[j] = acc;
+              owner_schedule<W>();
             }
           }
         }
