@@ -1,9 +1,11 @@
-// sort.hip -- stable LSD radix sort of the batch by Morton code on the
-// trainer's stream, replacing the reference's per-step host std::sort
+// sort.hip -- stable radix sort of the batch by Morton code on the trainer's
+// stream, replacing the reference's per-step host std::sort
 // (src/tiny_metal_nn/runtime/morton_sort.h:60-110).
 //
-// RB-bit digits (10 for 2D's 20-bit codes: 2 passes; 8 for 3D's 30-bit and
-// 4D's 32-bit codes: 4 passes), three kernels per pass:
+// 3D's 30-bit and 4D's 32-bit codes: LSD with 8-bit digits (4 passes). 2D's
+// 20-bit codes: one MSD pass on the top 10 bits, then bucket_sort_kernel
+// sorts each of the 1024 buckets by the low 10 bits in one block (one launch
+// instead of a second three-kernel pass). Three kernels per radix pass:
 //   hist   -- each block counts the digits of its 2048-key chunk (LDS atomics)
 //             into hist[digit][block]; the first pass computes the Morton
 //             codes from the positions itself;
@@ -122,49 +124,42 @@ __global__ void __launch_bounds__(kSortThreads)
   if (t == 0) totals[d] = total;
 }
 
-template <int RB, bool FIRST>
-__global__ void __launch_bounds__(kSortThreads)
-    radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const float *pos,
-                         int dims, int n, int shift, int blocks, const uint32_t * /*hist*/,
-                         const uint32_t *pre, const uint32_t *totals, uint32_t *keys_out,
-                         uint32_t *vals_out) {
-  constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
-  __shared__ uint32_t s_keys[kChunk];
-  __shared__ uint32_t s_vals[kChunk];
-  __shared__ uint16_t wcnt[kSortWaves][kBins];  // per-wave counts, then offsets (< kChunk)
-  __shared__ uint32_t lstart[kBins];            // start of the digit run within the chunk
-  __shared__ uint32_t glob[kBins];              // global slot of chunk index 0 of the run
-  __shared__ uint32_t wsum[kSortWaves];
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = t >> 6;
-  const int base = blockIdx.x * kChunk;
-  const int nblk = std::min(kChunk, n - base);
-  for (int i = t; i < kSortWaves * kBins / 2; i += kSortThreads)
-    reinterpret_cast<uint32_t *>(&wcnt[0][0])[i] = 0u;
-  __syncthreads();
+// LDS of one chunk's stable ranking (radix_scatter_kernel, bucket_sort_kernel).
+template <int RB>
+struct ChunkLds {
+  uint32_t keys[kChunk];
+  uint32_t vals[kChunk];
+  uint16_t wcnt[kSortWaves][1 << RB];  // per-wave counts, then offsets (< kChunk)
+  uint32_t lstart[1 << RB];            // start of the digit run within the chunk
+  uint32_t glob[1 << RB];              // output slot of chunk index 0 of the run
+  uint32_t wsum[kSortWaves];
+};
 
-  // wave w ranks chunk keys [w * kWaveKeys, (w + 1) * kWaveKeys), 64 per
-  // round in input order, against its own counters (no barriers): piw = keys
-  // of the same digit before it in the wave. All loads are issued first.
-  uint32_t key[kKeysPerThread], val[kKeysPerThread], piw[kKeysPerThread];
-#pragma unroll
-  for (int r = 0; r < kKeysPerThread; ++r) {
-    const int li = wave * kWaveKeys + r * 64 + lane;
-    const bool valid = li < nblk;
-    const size_t gi = static_cast<size_t>(base + (valid ? li : 0));
-    if constexpr (FIRST) {
-      key[r] = valid ? load_key<true>(nullptr, pos, dims, gi) : 0u;
-      val[r] = static_cast<uint32_t>(gi);
-    } else {
-      key[r] = valid ? keys_in[gi] : 0u;
-      val[r] = valid ? vals_in[gi] : 0u;
-    }
-  }
+// Chunk element of key slot r of this thread: wave w holds the contiguous
+// chunk elements [w * kWaveKeys, (w + 1) * kWaveKeys), 64 per slot.
+__device__ __forceinline__ int chunk_index(int r) {
+  return (threadIdx.x >> 6) * kWaveKeys + r * 64 + (threadIdx.x & 63);
+}
+
+// Clears the per-wave digit counters (the caller's barrier publishes it).
+template <int RB>
+__device__ __forceinline__ void clear_counts(ChunkLds<RB> &L) {
+  for (int i = threadIdx.x; i < kSortWaves * (1 << RB) / 2; i += kSortThreads)
+    reinterpret_cast<uint32_t *>(&L.wcnt[0][0])[i] = 0u;
+}
+
+// Every wave ranks its keys, 64 per round in input order, against its own
+// counters (no barriers): piw = keys of the same digit before it in the wave.
+template <int RB>
+__device__ __forceinline__ void rank_in_waves(ChunkLds<RB> &L, const uint32_t (&key)[kKeysPerThread],
+                                              int nblk, int shift,
+                                              uint32_t (&piw)[kKeysPerThread]) {
+  constexpr int kBins = 1 << RB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
   for (int r = 0; r < kKeysPerThread; ++r) {
-    const bool valid = wave * kWaveKeys + r * 64 + lane < nblk;
+    const bool valid = chunk_index(r) < nblk;
     const uint32_t d = (key[r] >> shift) & (kBins - 1);
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -176,62 +171,209 @@ __global__ void __launch_bounds__(kSortThreads)
     const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt_mask));
     // every lane reads the wave's running count before the leader advances
     // it (the LDS operations of one wave complete in program order)
-    const uint32_t c = valid ? wcnt[wave][d] : 0u;
+    const uint32_t c = valid ? L.wcnt[wave][d] : 0u;
     piw[r] = c + rank;
-    if (valid && rank == 0u) wcnt[wave][d] = static_cast<uint16_t>(c + __popcll(peers));
+    if (valid && rank == 0u) L.wcnt[wave][d] = static_cast<uint16_t>(c + __popcll(peers));
   }
-  __syncthreads();
+}
 
-  // thread t owns digits [t*BPT, (t+1)*BPT): offsets across waves, the
-  // chunk's count, the run's start in the chunk and its global slot
-  // (exclusive scan of the digit totals plus this block's prefix in the digit)
-  uint32_t cnt[BPT], tot[BPT], sc = 0, st = 0;
+// After the ranking's barrier: thread t owns digits [t*BPT, (t+1)*BPT); turns
+// their per-wave counts into offsets across the waves and returns the
+// chunk's count of each in cnt.
+template <int RB>
+__device__ __forceinline__ void wave_offsets(ChunkLds<RB> &L,
+                                             uint32_t (&cnt)[(1 << RB) / kSortThreads]) {
+  constexpr int BPT = (1 << RB) / kSortThreads;
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
-    const int dd = t * BPT + j;
+    const int dd = threadIdx.x * BPT + j;
     uint32_t acc = 0;
 #pragma unroll
     for (int w = 0; w < kSortWaves; ++w) {
-      const uint32_t c = wcnt[w][dd];
-      wcnt[w][dd] = static_cast<uint16_t>(acc);
+      const uint32_t c = L.wcnt[w][dd];
+      L.wcnt[w][dd] = static_cast<uint16_t>(acc);
       acc += c;
     }
     cnt[j] = acc;
-    tot[j] = totals[dd];
-    sc += acc;
+  }
+}
+
+// Sorts the chunk into L.keys / L.vals by digit, input order within a digit
+// (after the barrier that published lstart and the wave offsets).
+template <int RB>
+__device__ __forceinline__ void place_chunk(ChunkLds<RB> &L, const uint32_t (&key)[kKeysPerThread],
+                                            const uint32_t (&val)[kKeysPerThread],
+                                            const uint32_t (&piw)[kKeysPerThread], int nblk,
+                                            int shift) {
+  constexpr int kBins = 1 << RB;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int r = 0; r < kKeysPerThread; ++r) {
+    if (chunk_index(r) < nblk) {
+      const uint32_t d = (key[r] >> shift) & (kBins - 1);
+      const uint32_t p = L.lstart[d] + L.wcnt[wave][d] + piw[r];
+      L.keys[p] = key[r];
+      L.vals[p] = val[r];
+    }
+  }
+}
+
+// Writes the sorted chunk out (after the barrier that follows place_chunk):
+// consecutive threads write consecutive slots of a digit run.
+template <int RB>
+__device__ __forceinline__ void write_chunk(const ChunkLds<RB> &L, int nblk, int shift,
+                                            uint32_t *keys_out, uint32_t *vals_out) {
+  constexpr int kBins = 1 << RB;
+  for (int j = threadIdx.x; j < nblk; j += kSortThreads) {
+    const uint32_t k = L.keys[j];
+    const uint32_t dst = L.glob[(k >> shift) & (kBins - 1)] + static_cast<uint32_t>(j);
+    keys_out[dst] = k;
+    vals_out[dst] = L.vals[j];
+  }
+}
+
+template <int RB, bool FIRST>
+__global__ void __launch_bounds__(kSortThreads)
+    radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const float *pos,
+                         int dims, int n, int shift, int blocks, const uint32_t * /*hist*/,
+                         const uint32_t *pre, const uint32_t *totals, uint32_t *keys_out,
+                         uint32_t *vals_out) {
+  constexpr int BPT = (1 << RB) / kSortThreads;
+  __shared__ ChunkLds<RB> L;
+  const int t = threadIdx.x;
+  const int base = blockIdx.x * kChunk;
+  const int nblk = std::min(kChunk, n - base);
+  clear_counts(L);
+  __syncthreads();
+
+  // all loads are issued before the ranking
+  uint32_t key[kKeysPerThread], val[kKeysPerThread], piw[kKeysPerThread];
+#pragma unroll
+  for (int r = 0; r < kKeysPerThread; ++r) {
+    const int li = chunk_index(r);
+    const bool valid = li < nblk;
+    const size_t gi = static_cast<size_t>(base + (valid ? li : 0));
+    if constexpr (FIRST) {
+      key[r] = valid ? load_key<true>(nullptr, pos, dims, gi) : 0u;
+      val[r] = static_cast<uint32_t>(gi);
+    } else {
+      key[r] = valid ? keys_in[gi] : 0u;
+      val[r] = valid ? vals_in[gi] : 0u;
+    }
+  }
+  rank_in_waves(L, key, nblk, shift, piw);
+  __syncthreads();
+
+  // the chunk's count of each owned digit, the run's start in the chunk and
+  // its global slot (exclusive scan of the digit totals plus this block's
+  // prefix in the digit)
+  uint32_t cnt[BPT], tot[BPT], sc = 0, st = 0;
+  wave_offsets(L, cnt);
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    tot[j] = totals[t * BPT + j];
+    sc += cnt[j];
     st += tot[j];
   }
   uint32_t all = 0;
-  uint32_t lb = block_excl_scan(sc, wsum, &all);
-  uint32_t gb = block_excl_scan(st, wsum, &all);
+  uint32_t lb = block_excl_scan(sc, L.wsum, &all);
+  uint32_t gb = block_excl_scan(st, L.wsum, &all);
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
     const int dd = t * BPT + j;
-    lstart[dd] = lb;
-    glob[dd] = gb + pre[static_cast<size_t>(dd) * blocks + blockIdx.x] - lb;  // modulo 2^32
+    L.lstart[dd] = lb;
+    L.glob[dd] = gb + pre[static_cast<size_t>(dd) * blocks + blockIdx.x] - lb;  // modulo 2^32
     lb += cnt[j];
     gb += tot[j];
   }
   __syncthreads();
+  place_chunk(L, key, val, piw, nblk, shift);
+  __syncthreads();
+  write_chunk(L, nblk, shift, keys_out, vals_out);
+}
 
-  // sort the chunk in LDS (input order within each digit)
+// Second pass of the 2D sort, after an MSD pass on the top RB bits: block b
+// sorts bucket b (the keys whose top digit is b, contiguous and in input
+// order) stably by the low RB bits, in place of a full LSD pass. A bucket
+// that fits one chunk is ranked and written at once; a larger one takes a
+// digit histogram of the whole bucket, then its chunks in order, each
+// written at the running offsets of its digits (stable across chunks).
+template <int RB>
+__global__ void __launch_bounds__(kSortThreads)
+    bucket_sort_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const uint32_t *totals,
+                       uint32_t *keys_out, uint32_t *vals_out) {
+  constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
+  __shared__ ChunkLds<RB> L;
+  __shared__ uint32_t offs[kBins];  // running output offset of each digit in the bucket
+  const int t = threadIdx.x;
+  const int b = blockIdx.x;
+  // bucket start: the totals of the buckets before it
+  uint32_t s = 0;
+  for (int i = t; i < b; i += kSortThreads) s += totals[i];
+  uint32_t start = 0;
+  block_excl_scan(s, L.wsum, &start);
+  const int size = static_cast<int>(totals[b]);
+  if (size == 0) return;  // uniform
+  const bool one_chunk = size <= kChunk;
+  if (!one_chunk) {
+    // digit histogram of the whole bucket, then its exclusive scan
+    for (int i = t; i < kBins; i += kSortThreads) offs[i] = 0u;
+    __syncthreads();
+    for (int i = t; i < size; i += kSortThreads)
+      atomicAdd(&offs[keys_in[start + i] & (kBins - 1)], 1u);
+    __syncthreads();
+    uint32_t c[BPT], sum = 0;
 #pragma unroll
-  for (int r = 0; r < kKeysPerThread; ++r) {
-    if (wave * kWaveKeys + r * 64 + lane < nblk) {
-      const uint32_t d = (key[r] >> shift) & (kBins - 1);
-      const uint32_t p = lstart[d] + wcnt[wave][d] + piw[r];
-      s_keys[p] = key[r];
-      s_vals[p] = val[r];
+    for (int j = 0; j < BPT; ++j) {
+      c[j] = offs[t * BPT + j];
+      sum += c[j];
+    }
+    uint32_t all = 0;
+    uint32_t run = block_excl_scan(sum, L.wsum, &all);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      offs[t * BPT + j] = run;
+      run += c[j];
     }
   }
-  __syncthreads();
-
-  // consecutive threads write consecutive slots of a digit run
-  for (int j = t; j < nblk; j += kSortThreads) {
-    const uint32_t k = s_keys[j];
-    const uint32_t dst = glob[(k >> shift) & (kBins - 1)] + static_cast<uint32_t>(j);
-    keys_out[dst] = k;
-    vals_out[dst] = s_vals[j];
+  for (int base = 0; base < size; base += kChunk) {
+    const int nblk = std::min(kChunk, size - base);
+    clear_counts(L);
+    __syncthreads();
+    uint32_t key[kKeysPerThread], val[kKeysPerThread], piw[kKeysPerThread];
+#pragma unroll
+    for (int r = 0; r < kKeysPerThread; ++r) {
+      const int li = chunk_index(r);
+      const bool valid = li < nblk;
+      const size_t gi = static_cast<size_t>(start) + base + (valid ? li : 0);
+      key[r] = valid ? keys_in[gi] : 0u;
+      val[r] = valid ? vals_in[gi] : 0u;
+    }
+    rank_in_waves(L, key, nblk, 0, piw);
+    __syncthreads();
+    uint32_t cnt[BPT], sc = 0;
+    wave_offsets(L, cnt);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) sc += cnt[j];
+    uint32_t all = 0;
+    uint32_t lb = block_excl_scan(sc, L.wsum, &all);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int dd = t * BPT + j;
+      L.lstart[dd] = lb;
+      if (one_chunk) {
+        L.glob[dd] = start;  // the sorted chunk is the sorted bucket
+      } else {
+        L.glob[dd] = start + offs[dd] - lb;  // modulo 2^32
+        offs[dd] += cnt[j];
+      }
+      lb += cnt[j];
+    }
+    __syncthreads();
+    place_chunk(L, key, val, piw, nblk, 0);
+    __syncthreads();
+    write_chunk(L, nblk, 0, keys_out, vals_out);
+    __syncthreads();  // L is reused by the next chunk
   }
 }
 
@@ -311,8 +453,22 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
   if (digit_bits(end_bit) == 8)
     return run_passes<8>(hist, pre, totals, pos, dims, keys0, keys1, vals0, vals1, n, end_bit,
                          stream, keys_sorted, vals_sorted);
-  return run_passes<10>(hist, pre, totals, pos, dims, keys0, keys1, vals0, vals1, n, end_bit,
-                        stream, keys_sorted, vals_sorted);
+  // 2D: an MSD pass on the top 10 bits (codes computed from the positions),
+  // then one block per top digit sorts its bucket by the low 10 bits
+  hipLaunchKernelGGL((radix_hist_kernel<10, true>), dim3(blocks), dim3(kSortThreads), 0, stream,
+                     nullptr, pos, dims, n, 10, blocks, hist);
+  hipLaunchKernelGGL(radix_scan_kernel, dim3(1 << 10), dim3(kSortThreads), 0, stream, hist,
+                     blocks, pre, totals);
+  hipLaunchKernelGGL((radix_scatter_kernel<10, true>), dim3(blocks), dim3(kSortThreads), 0,
+                     stream, nullptr, nullptr, pos, dims, n, 10, blocks, hist, pre, totals, keys1,
+                     vals1);
+  hipLaunchKernelGGL((bucket_sort_kernel<10>), dim3(1 << 10), dim3(kSortThreads), 0, stream, keys1,
+                     vals1, totals, keys0, vals0);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  *keys_sorted = keys0;
+  *vals_sorted = vals0;
+  return hipSuccess;
 }
 
 }  // namespace tmnn_hip
