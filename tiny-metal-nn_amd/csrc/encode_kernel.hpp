@@ -125,7 +125,8 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeA
 #pragma unroll
         for (int f = 0; f < F; ++f) o[lv * F + f] = (valid && l < a.L) ? feat[f] : 0.0f;
       }
-      *reinterpret_cast<f32x4 *>(a.xfeat + xtile_offset(i, q0 + g, a.KT0)) = o;
+      // streamed out (non-temporal): the table keeps the caches
+      __builtin_nontemporal_store(o, reinterpret_cast<f32x4 *>(a.xfeat + xtile_offset(i, q0 + g, a.KT0)));
     }
   }
 }
