@@ -138,26 +138,51 @@ __device__ __forceinline__ void mma_split_packed(const unsigned char *frag_hi,
                                                  const half8 (&bl)[KS][kNT], const float *bias,
                                                  f32x4 (&out)[MT][kNT], int lane) {
   const int q = lane >> 4;
+  // unit tiles in pairs (one alone if MT is odd): four independent
+  // accumulator chains interleaved; each chain keeps its own product order
+  constexpr int MP = MT >= 2 ? 2 : 1;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + 16 * mt + 4 * q);
-    f32x4 acc[kNT];
+  for (int m0 = 0; m0 < MT; m0 += MP) {
+    constexpr int kM = MP;
+    f32x4 acc[kM][kNT];
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) acc[nt] = bv;
+    for (int u = 0; u < kM; ++u) {
+      const int mt = m0 + u < MT ? m0 + u : MT - 1;
+      const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + 16 * mt + 4 * q);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int off = ((mt * KS + ks) * 64 + lane) * 16;
-      const half8 ah = *reinterpret_cast<const half8 *>(frag_hi + off);
-      const half8 al = *reinterpret_cast<const half8 *>(frag_lo + off);
-#pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) {
-        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[ks][nt], acc[nt], 0, 0, 0);
-        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[ks][nt], acc[nt], 0, 0, 0);
-        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[ks][nt], acc[nt], 0, 0, 0);
-      }
+      for (int nt = 0; nt < kNT; ++nt) acc[u][nt] = bv;
     }
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) out[mt][nt] = acc[nt];
+    for (int ks = 0; ks < KS; ++ks) {
+      half8 ah[kM], al[kM];
+#pragma unroll
+      for (int u = 0; u < kM; ++u) {
+        const int mt = m0 + u < MT ? m0 + u : MT - 1;
+        const int off = ((mt * KS + ks) * 64 + lane) * 16;
+        ah[u] = *reinterpret_cast<const half8 *>(frag_hi + off);
+        al[u] = *reinterpret_cast<const half8 *>(frag_lo + off);
+      }
+#pragma unroll
+      for (int u = 0; u < kM; ++u)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          acc[u][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[u], bh[ks][nt], acc[u][nt], 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < kM; ++u)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          acc[u][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u], bl[ks][nt], acc[u][nt], 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < kM; ++u)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          acc[u][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u], bh[ks][nt], acc[u][nt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kM; ++u)
+      if (m0 + u < MT)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) out[m0 + u][nt] = acc[u][nt];
   }
 }
 
