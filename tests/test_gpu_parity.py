@@ -399,8 +399,9 @@ def _compact_2d(code3):
     return out
 
 
-@pytest.mark.parametrize("d,n", [(2, 1), (2, 2), (2, 2048), (2, 2049), (2, 4097), (2, 70000),
-                                 (2, 1 << 18), (3, 12345), (3, 1 << 20), (4, 9000), (4, 300001)])
+@pytest.mark.parametrize("d,n", [(2, 1), (2, 2), (2, 1536), (2, 1537), (2, 2048), (2, 2049),
+                                 (2, 3073), (2, 4097), (2, 70000), (2, 1 << 18), (3, 12345),
+                                 (3, 1 << 20), (4, 9000), (4, 300001)])
 def test_morton_sort_matches_oracle_codes_and_stable_order(oracle, d, n):
     """morton_sort.h: same codes as the oracle (the reference's quantisation),
     and the permutation is the stable argsort of those codes."""

@@ -28,9 +28,11 @@ namespace tmnn_hip {
 namespace {
 
 constexpr int kSortThreads = 256;
+// keys per thread (a chunk = 256 x KPT keys per block): 8 for the 3D/4D LSD
+// passes; 6 for 2D, whose 2^18-point batches gain from more, smaller chunks
 constexpr int kKeysPerThread = 8;
-constexpr int kChunk = kSortThreads * kKeysPerThread;  // keys per block
-constexpr int kWaveKeys = 64 * kKeysPerThread;         // keys per wave in the scatter
+constexpr int kKeysPerThread2D = 6;
+constexpr int chunk_keys(int kpt) { return kSortThreads * kpt; }
 constexpr int kSortWaves = kSortThreads / 64;
 
 // Inclusive scan of v over the 64 lanes of a wave.
@@ -71,7 +73,7 @@ __device__ __forceinline__ uint32_t load_key(const uint32_t *keys, const float *
   return keys[i];
 }
 
-template <int RB, bool FIRST>
+template <int RB, bool FIRST, int KPT>
 __global__ void __launch_bounds__(kSortThreads)
     radix_hist_kernel(const uint32_t *keys, const float *pos, int dims, int n, int shift,
                       int blocks, uint32_t *hist) {
@@ -81,9 +83,9 @@ __global__ void __launch_bounds__(kSortThreads)
 #pragma unroll
   for (int j = 0; j < BPT; ++j) cnt[t + kSortThreads * j] = 0u;
   __syncthreads();
-  const int base = blockIdx.x * kChunk;
+  const int base = blockIdx.x * chunk_keys(KPT);
 #pragma unroll
-  for (int r = 0; r < kKeysPerThread; ++r) {
+  for (int r = 0; r < KPT; ++r) {
     const int i = base + r * kSortThreads + t;
     if (i < n) {
       const uint32_t key = load_key<FIRST>(keys, pos, dims, static_cast<size_t>(i));
@@ -125,41 +127,41 @@ __global__ void __launch_bounds__(kSortThreads)
 }
 
 // LDS of one chunk's stable ranking (radix_scatter_kernel, bucket_sort_kernel).
-template <int RB>
+template <int RB, int KPT>
 struct ChunkLds {
-  uint32_t keys[kChunk];
-  uint32_t vals[kChunk];
-  uint16_t wcnt[kSortWaves][1 << RB];  // per-wave counts, then offsets (< kChunk)
+  uint32_t keys[chunk_keys(KPT)];
+  uint32_t vals[chunk_keys(KPT)];
+  uint16_t wcnt[kSortWaves][1 << RB];  // per-wave counts, then offsets (< the chunk)
   uint32_t lstart[1 << RB];            // start of the digit run within the chunk
   uint32_t glob[1 << RB];              // output slot of chunk index 0 of the run
   uint32_t wsum[kSortWaves];
 };
 
 // Chunk element of key slot r of this thread: wave w holds the contiguous
-// chunk elements [w * kWaveKeys, (w + 1) * kWaveKeys), 64 per slot.
+// chunk elements [w * 64 KPT, (w + 1) * 64 KPT), 64 per slot.
+template <int KPT>
 __device__ __forceinline__ int chunk_index(int r) {
-  return (threadIdx.x >> 6) * kWaveKeys + r * 64 + (threadIdx.x & 63);
+  return (threadIdx.x >> 6) * (64 * KPT) + r * 64 + (threadIdx.x & 63);
 }
 
 // Clears the per-wave digit counters (the caller's barrier publishes it).
-template <int RB>
-__device__ __forceinline__ void clear_counts(ChunkLds<RB> &L) {
+template <int RB, int KPT>
+__device__ __forceinline__ void clear_counts(ChunkLds<RB, KPT> &L) {
   for (int i = threadIdx.x; i < kSortWaves * (1 << RB) / 2; i += kSortThreads)
     reinterpret_cast<uint32_t *>(&L.wcnt[0][0])[i] = 0u;
 }
 
 // Every wave ranks its keys, 64 per round in input order, against its own
 // counters (no barriers): piw = keys of the same digit before it in the wave.
-template <int RB>
-__device__ __forceinline__ void rank_in_waves(ChunkLds<RB> &L, const uint32_t (&key)[kKeysPerThread],
-                                              int nblk, int shift,
-                                              uint32_t (&piw)[kKeysPerThread]) {
+template <int RB, int KPT>
+__device__ __forceinline__ void rank_in_waves(ChunkLds<RB, KPT> &L, const uint32_t (&key)[KPT],
+                                              int nblk, int shift, uint32_t (&piw)[KPT]) {
   constexpr int kBins = 1 << RB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
-  for (int r = 0; r < kKeysPerThread; ++r) {
-    const bool valid = chunk_index(r) < nblk;
+  for (int r = 0; r < KPT; ++r) {
+    const bool valid = chunk_index<KPT>(r) < nblk;
     const uint32_t d = (key[r] >> shift) & (kBins - 1);
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -180,8 +182,8 @@ __device__ __forceinline__ void rank_in_waves(ChunkLds<RB> &L, const uint32_t (&
 // After the ranking's barrier: thread t owns digits [t*BPT, (t+1)*BPT); turns
 // their per-wave counts into offsets across the waves and returns the
 // chunk's count of each in cnt.
-template <int RB>
-__device__ __forceinline__ void wave_offsets(ChunkLds<RB> &L,
+template <int RB, int KPT>
+__device__ __forceinline__ void wave_offsets(ChunkLds<RB, KPT> &L,
                                              uint32_t (&cnt)[(1 << RB) / kSortThreads]) {
   constexpr int BPT = (1 << RB) / kSortThreads;
 #pragma unroll
@@ -200,16 +202,15 @@ __device__ __forceinline__ void wave_offsets(ChunkLds<RB> &L,
 
 // Sorts the chunk into L.keys / L.vals by digit, input order within a digit
 // (after the barrier that published lstart and the wave offsets).
-template <int RB>
-__device__ __forceinline__ void place_chunk(ChunkLds<RB> &L, const uint32_t (&key)[kKeysPerThread],
-                                            const uint32_t (&val)[kKeysPerThread],
-                                            const uint32_t (&piw)[kKeysPerThread], int nblk,
-                                            int shift) {
+template <int RB, int KPT>
+__device__ __forceinline__ void place_chunk(ChunkLds<RB, KPT> &L, const uint32_t (&key)[KPT],
+                                            const uint32_t (&val)[KPT], const uint32_t (&piw)[KPT],
+                                            int nblk, int shift) {
   constexpr int kBins = 1 << RB;
   const int wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int r = 0; r < kKeysPerThread; ++r) {
-    if (chunk_index(r) < nblk) {
+  for (int r = 0; r < KPT; ++r) {
+    if (chunk_index<KPT>(r) < nblk) {
       const uint32_t d = (key[r] >> shift) & (kBins - 1);
       const uint32_t p = L.lstart[d] + L.wcnt[wave][d] + piw[r];
       L.keys[p] = key[r];
@@ -220,8 +221,8 @@ __device__ __forceinline__ void place_chunk(ChunkLds<RB> &L, const uint32_t (&ke
 
 // Writes the sorted chunk out (after the barrier that follows place_chunk):
 // consecutive threads write consecutive slots of a digit run.
-template <int RB>
-__device__ __forceinline__ void write_chunk(const ChunkLds<RB> &L, int nblk, int shift,
+template <int RB, int KPT>
+__device__ __forceinline__ void write_chunk(const ChunkLds<RB, KPT> &L, int nblk, int shift,
                                             uint32_t *keys_out, uint32_t *vals_out) {
   constexpr int kBins = 1 << RB;
   for (int j = threadIdx.x; j < nblk; j += kSortThreads) {
@@ -232,25 +233,25 @@ __device__ __forceinline__ void write_chunk(const ChunkLds<RB> &L, int nblk, int
   }
 }
 
-template <int RB, bool FIRST>
+template <int RB, bool FIRST, int KPT>
 __global__ void __launch_bounds__(kSortThreads)
     radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const float *pos,
                          int dims, int n, int shift, int blocks, const uint32_t * /*hist*/,
                          const uint32_t *pre, const uint32_t *totals, uint32_t *keys_out,
                          uint32_t *vals_out) {
   constexpr int BPT = (1 << RB) / kSortThreads;
-  __shared__ ChunkLds<RB> L;
+  __shared__ ChunkLds<RB, KPT> L;
   const int t = threadIdx.x;
-  const int base = blockIdx.x * kChunk;
-  const int nblk = std::min(kChunk, n - base);
+  const int base = blockIdx.x * chunk_keys(KPT);
+  const int nblk = std::min(chunk_keys(KPT), n - base);
   clear_counts(L);
   __syncthreads();
 
   // all loads are issued before the ranking
-  uint32_t key[kKeysPerThread], val[kKeysPerThread], piw[kKeysPerThread];
+  uint32_t key[KPT], val[KPT], piw[KPT];
 #pragma unroll
-  for (int r = 0; r < kKeysPerThread; ++r) {
-    const int li = chunk_index(r);
+  for (int r = 0; r < KPT; ++r) {
+    const int li = chunk_index<KPT>(r);
     const bool valid = li < nblk;
     const size_t gi = static_cast<size_t>(base + (valid ? li : 0));
     if constexpr (FIRST) {
@@ -298,12 +299,13 @@ __global__ void __launch_bounds__(kSortThreads)
 // that fits one chunk is ranked and written at once; a larger one takes a
 // digit histogram of the whole bucket, then its chunks in order, each
 // written at the running offsets of its digits (stable across chunks).
-template <int RB>
+template <int RB, int KPT>
 __global__ void __launch_bounds__(kSortThreads)
     bucket_sort_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const uint32_t *totals,
                        uint32_t *keys_out, uint32_t *vals_out) {
   constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
-  __shared__ ChunkLds<RB> L;
+  constexpr int kChunk = chunk_keys(KPT);
+  __shared__ ChunkLds<RB, KPT> L;
   __shared__ uint32_t offs[kBins];  // running output offset of each digit in the bucket
   const int t = threadIdx.x;
   const int b = blockIdx.x;
@@ -340,10 +342,10 @@ __global__ void __launch_bounds__(kSortThreads)
     const int nblk = std::min(kChunk, size - base);
     clear_counts(L);
     __syncthreads();
-    uint32_t key[kKeysPerThread], val[kKeysPerThread], piw[kKeysPerThread];
+    uint32_t key[KPT], val[KPT], piw[KPT];
 #pragma unroll
-    for (int r = 0; r < kKeysPerThread; ++r) {
-      const int li = chunk_index(r);
+    for (int r = 0; r < KPT; ++r) {
+      const int li = chunk_index<KPT>(r);
       const bool valid = li < nblk;
       const size_t gi = static_cast<size_t>(start) + base + (valid ? li : 0);
       key[r] = valid ? keys_in[gi] : 0u;
@@ -377,7 +379,7 @@ __global__ void __launch_bounds__(kSortThreads)
   }
 }
 
-int sort_blocks(int n) { return (n + kChunk - 1) / kChunk; }
+int sort_blocks(int n, int kpt) { return (n + chunk_keys(kpt) - 1) / chunk_keys(kpt); }
 
 // digit width per code width: two 10-bit passes for 2D's 20-bit codes; 8-bit
 // digits (4 passes) for 3D/4D, where wider digits measured slower per pass
@@ -389,27 +391,27 @@ hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const flo
                       int dims, uint32_t *keys0, uint32_t *keys1, uint32_t *vals0,
                       uint32_t *vals1, int n, int end_bit, hipStream_t stream,
                       const uint32_t **keys_sorted, const uint32_t **vals_sorted) {
-  const int blocks = sort_blocks(n);
+  const int blocks = sort_blocks(n, kKeysPerThread);
   uint32_t *kin = keys0, *kout = keys1, *vin = nullptr, *vout = vals1;
   uint32_t *vspare = vals0;
   const int passes = std::max(1, (end_bit + RB - 1) / RB);
   for (int pass = 0; pass < passes; ++pass) {
     const int shift = RB * pass;
     if (pass == 0) {
-      hipLaunchKernelGGL((radix_hist_kernel<RB, true>), dim3(blocks), dim3(kSortThreads), 0, stream,
+      hipLaunchKernelGGL((radix_hist_kernel<RB, true, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0, stream,
                          nullptr, pos, dims, n, shift, blocks, hist);
     } else {
-      hipLaunchKernelGGL((radix_hist_kernel<RB, false>), dim3(blocks), dim3(kSortThreads), 0,
+      hipLaunchKernelGGL((radix_hist_kernel<RB, false, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
                          stream, kin, nullptr, dims, n, shift, blocks, hist);
     }
     hipLaunchKernelGGL(radix_scan_kernel, dim3(1 << RB), dim3(kSortThreads), 0, stream, hist,
                        blocks, pre, totals);
     if (pass == 0) {
-      hipLaunchKernelGGL((radix_scatter_kernel<RB, true>), dim3(blocks), dim3(kSortThreads), 0,
+      hipLaunchKernelGGL((radix_scatter_kernel<RB, true, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
                          stream, nullptr, nullptr, pos, dims, n, shift, blocks, hist, pre, totals,
                          kout, vout);
     } else {
-      hipLaunchKernelGGL((radix_scatter_kernel<RB, false>), dim3(blocks), dim3(kSortThreads), 0,
+      hipLaunchKernelGGL((radix_scatter_kernel<RB, false, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
                          stream, kin, vin, nullptr, dims, n, shift, blocks, hist, pre, totals,
                          kout, vout);
     }
@@ -431,7 +433,8 @@ hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const flo
 hipError_t morton_sort_temp_bytes(int n, size_t *bytes) {
   // hist[kBins][G] + pre[kBins][G] + totals[kBins] at the widest digit
   const size_t bins = size_t(1) << 10;
-  *bytes = (2 * bins * std::max(1, sort_blocks(n)) + bins) * sizeof(uint32_t);
+  const int blocks = std::max(sort_blocks(n, kKeysPerThread), sort_blocks(n, kKeysPerThread2D));
+  *bytes = (2 * bins * std::max(1, blocks) + bins) * sizeof(uint32_t);
   return hipSuccess;
 }
 
@@ -445,8 +448,8 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
   // 2D codes interleave x and y only (the lifted z = 0 bits are all zero,
   // which leaves the order unchanged): 20 bits; 3D 30 bits; 4D 32 bits.
   const int end_bit = dims == 2 ? 20 : (dims == 3 ? 30 : 32);
-  const int blocks = sort_blocks(n);
   const size_t bins = size_t(1) << digit_bits(end_bit);
+  const int blocks = sort_blocks(n, digit_bits(end_bit) == 8 ? kKeysPerThread : kKeysPerThread2D);
   uint32_t *hist = static_cast<uint32_t *>(tmp);
   uint32_t *pre = hist + bins * blocks;
   uint32_t *totals = pre + bins * blocks;
@@ -455,15 +458,16 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
                          stream, keys_sorted, vals_sorted);
   // 2D: an MSD pass on the top 10 bits (codes computed from the positions),
   // then one block per top digit sorts its bucket by the low 10 bits
-  hipLaunchKernelGGL((radix_hist_kernel<10, true>), dim3(blocks), dim3(kSortThreads), 0, stream,
-                     nullptr, pos, dims, n, 10, blocks, hist);
+  constexpr int K2 = kKeysPerThread2D;
+  hipLaunchKernelGGL((radix_hist_kernel<10, true, K2>), dim3(blocks), dim3(kSortThreads), 0,
+                     stream, nullptr, pos, dims, n, 10, blocks, hist);
   hipLaunchKernelGGL(radix_scan_kernel, dim3(1 << 10), dim3(kSortThreads), 0, stream, hist,
                      blocks, pre, totals);
-  hipLaunchKernelGGL((radix_scatter_kernel<10, true>), dim3(blocks), dim3(kSortThreads), 0,
+  hipLaunchKernelGGL((radix_scatter_kernel<10, true, K2>), dim3(blocks), dim3(kSortThreads), 0,
                      stream, nullptr, nullptr, pos, dims, n, 10, blocks, hist, pre, totals, keys1,
                      vals1);
-  hipLaunchKernelGGL((bucket_sort_kernel<10>), dim3(1 << 10), dim3(kSortThreads), 0, stream, keys1,
-                     vals1, totals, keys0, vals0);
+  hipLaunchKernelGGL((bucket_sort_kernel<10, K2>), dim3(1 << 10), dim3(kSortThreads), 0, stream,
+                     keys1, vals1, totals, keys0, vals0);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   *keys_sorted = keys0;
