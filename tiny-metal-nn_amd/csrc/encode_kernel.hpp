@@ -60,7 +60,10 @@ template <int D, int F>
 __global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeArgs a) {
   constexpr int C = 1 << D;        // corners per level
   constexpr int LPQ = 4 / F;       // levels per feature quad
-  constexpr int QG = C >= 32 ? 1 : 32 / C;  // quads per group: QG * 4 * C floats in flight
+  // quads per group (QG * 4 * C floats in flight): 2D takes 4 (32 gathers,
+  // 74 registers: six waves per SIMD hold a whole 2^18 batch at once), 3D and
+  // 4D 32 / C
+  constexpr int QG = D == 2 ? 4 : (C >= 32 ? 1 : 32 / C);
   const int i = blockIdx.x * kEncodeThreads + threadIdx.x;
   if (i >= a.n_pad) return;
   const bool valid = i < a.n;
