@@ -609,12 +609,27 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *per
   e.pos_out = pos_out;
   e.table = tr->params.as<float>();
   e.xfeat = tr->xfeat.as<float>();
-  // level-major for large tables (the scatter's rule) when the positions are
-  // read in place; through a sort permutation every level would re-read them
-  // at random (measured slower than point-major)
-  const bool by_level = level_major(tr) && perm == nullptr;
-  const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads, by_level ? e.L : 1);
   hipStream_t st = tr->ctx->stream;
+  // level-major for large tables (the scatter's rule), reading the positions
+  // in place: through a sort permutation they are first gathered into sorted
+  // order in pos_out (which the scatter reads anyway), since every level
+  // re-reading them through the permutation at random measured slower than
+  // point-major
+  bool by_level = level_major(tr);
+  if (by_level && perm != nullptr) {
+    if (pos_out == nullptr) {
+      by_level = false;
+    } else {
+      const size_t elems = static_cast<size_t>(n) * tr->d.spatial_dims;
+      hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<uint32_t>((elems + 255) / 256)),
+                         dim3(256), 0, st, pos, nullptr, perm, n, tr->d.spatial_dims, 0,
+                         pos_out, nullptr);
+      e.pos = pos_out;
+      e.perm = nullptr;
+      e.pos_out = nullptr;
+    }
+  }
+  const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads, by_level ? e.L : 1);
 #define TMNN_ENCODE(d, f)                                                                     \
   if (by_level)                                                                               \
     hipLaunchKernelGGL((encode_level_kernel<d, f>), grid, dim3(kEncodeThreads), 0, st, e);    \
