@@ -587,10 +587,18 @@ int ensure_image(tmnn_trainer *tr, KernelPlan &plan) {
 // Input features of n points at pos as X tiles in tr->xfeat; with perm,
 // point i is pos[perm[i]] and its position is also written to pos_out[i].
 // Hash-grid kernels walk the levels one at a time (level-major) when a
-// level's slice of the table exceeds 8 MB, else all levels per point.
+// level's slice of the table exceeds 8 MB (the scatter) or 2 MB (the
+// encode), else all levels per point.
 bool level_major(const tmnn_trainer *tr) {
   return (static_cast<size_t>(tr->d.features_per_level) * 4u << tr->d.log2_hashmap_size) >
          (8u << 20);
+}
+
+// The encode goes level-major from 2 MB slices on (C3's 4 MB levels: 450 ->
+// 345 us; its scatter measured slower level-major there, so it keeps 8 MB).
+bool encode_level_major(const tmnn_trainer *tr) {
+  return (static_cast<size_t>(tr->d.features_per_level) * 4u << tr->d.log2_hashmap_size) >
+         (2u << 20);
 }
 
 int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *perm = nullptr,
@@ -615,7 +623,7 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *per
   // order in pos_out (which the scatter reads anyway), since every level
   // re-reading them through the permutation at random measured slower than
   // point-major
-  bool by_level = level_major(tr);
+  bool by_level = encode_level_major(tr);
   if (by_level && perm != nullptr) {
     if (pos_out == nullptr) {
       by_level = false;
