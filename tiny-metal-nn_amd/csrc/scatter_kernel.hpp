@@ -113,7 +113,8 @@ __device__ __forceinline__ bool grads_fit(const float *d) {
   return ok;
 }
 
-// One thread per point, all levels in turn: the thread reads its dx row with
+// One thread per point (or per point and share of its levels, blockIdx.y),
+// its levels in turn: the thread reads its dx row with
 // 16-byte loads (coalesced across the wave) and the lanes of a wave still
 // hold consecutive Morton-sorted points at the same level, which keeps the
 // run merging. FITS: every lane's d passed grads_fit (plain conversion).
@@ -185,7 +186,12 @@ __global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterAr
   for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(ii) * D + k];
   const float *row = a.dx + static_cast<size_t>(ii) * a.IN;
   // the levels of one 16-byte dx load (4 features: 4 / F levels) at a time
-  for (int fq = 0; fq * 4 < a.IN; ++fq) {
+  // blockIdx.y picks this thread's share of the quads (the launch may split
+  // a point's levels over several threads)
+  const int nq = (a.IN + 3) / 4;
+  const int per = (nq + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
+  const int q1 = min(nq, static_cast<int>(blockIdx.y) * per + per);
+  for (int fq = static_cast<int>(blockIdx.y) * per; fq < q1; ++fq) {
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (fq * 4 + 3 < a.IN && (a.IN & 3) == 0) {
       v = *reinterpret_cast<const f32x4 *>(row + fq * 4);
