@@ -16,12 +16,13 @@ One step = Morton sort -> hash-grid encode kernel -> MLP train kernel
 (dW / loss reductions, Adam, weight image for the next step), all on the
 library's HIP stream, inputs resident in HBM before the timed region starts.
 
-The K timed steps run as a caller runs them, without instrumentation (a HIP
-event pair on the stream costs ~3.5 us, ~23 us per step at seven phase
-boundaries). The same K steps are then run again with HIP events at the phase
-boundaries on the library's stream; that profiled pass gives the per-kernel
-durations behind the roofline fractions (`kernel_rooflines`, the slowest
-kernel is `roofline`) and `phase_us_per_step`.
+Inside the timed region the library brackets the phases of one step in
+every K/10 with HIP events on its own stream (`profile_every`); those sampled
+steps give the per-kernel durations behind the roofline fractions
+(`kernel_rooflines`, the slowest kernel is `roofline`) and
+`phase_us_per_step`. A HIP event pair costs ~3.5 us of stream time, so
+instrumenting every step would add ~23 us to a 0.13 ms step; sampling adds
+~2 us per sampled step, ~0.2 us per step on average.
 
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
 fp32, 2^16 points per call) and the CPU restatement of the reference math
@@ -187,13 +188,15 @@ def run_other_workload(args, which: str) -> int:
            "mi355x": {"precision": "fp16", "hash_adam": "lazy", "morton_sort": True}}
     gen = torch.Generator(device=dev).manual_seed(7)
     batches = [workload_batch(torch, which, n, gen, dev) for _ in range(2)]
-    loss_dev = torch.zeros(2 * args.steps + args.warmup + 1, device=dev)
+    loss_dev = torch.zeros(args.steps + args.warmup + 1, device=dev)
     tr = Trainer.from_config(cfg, n_input=d, n_output=m)
     for i in range(args.warmup):
         x, y = batches[i % 2]
         tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[i].data_ptr())
     tr.synchronize()
-    # timed steps without phase events, then the same count profiled
+    # timed steps, phase events on one in `every` (as the C2 line)
+    every = max(1, args.steps // 10)
+    tr.set_training_step_profiling(True, every)
     t0 = time.perf_counter()
     for i in range(args.steps):
         x, y = batches[i % 2]
@@ -201,12 +204,6 @@ def run_other_workload(args, which: str) -> int:
                                 loss_dev[args.warmup + i].data_ptr())
     tr.synchronize()
     el = time.perf_counter() - t0
-    tr.set_training_step_profiling(True)
-    for i in range(args.steps):
-        x, y = batches[i % 2]
-        tr.training_step_device(x.data_ptr(), y.data_ptr(), n,
-                                loss_dev[args.warmup + args.steps + i].data_ptr())
-    tr.synchronize()
     prof = tr.training_step_profile()
     tr.set_training_step_profiling(False)
     out = torch.empty(n, m, device=dev)
@@ -233,7 +230,7 @@ def run_other_workload(args, which: str) -> int:
         "forward_samples_per_s": round(n / fwd, 1), "forward_ms": round(fwd * 1e3, 4),
         "phase_us_per_step": {k: round(prof[k] / steps_prof, 2) for k in prof if k.startswith("gpu_")},
         "loss_first_last": [round(float(losses[0]), 6),
-                            round(float(losses[args.warmup + 2 * args.steps - 1]), 6)]}), flush=True)
+                            round(float(losses[args.warmup + args.steps - 1]), 6)]}), flush=True)
     return 0
 
 
@@ -365,7 +362,7 @@ def main() -> int:
     nb = 4
     xs = [torch.rand(B_TRAIN, 2, device=dev, generator=gen) for _ in range(nb)]
     ys = [sample_bilinear(torch, img, x) for x in xs]
-    loss_dev = torch.zeros(2 * args.steps + args.warmup + 1, device=dev)
+    loss_dev = torch.zeros(args.steps + args.warmup + 1, device=dev)
     torch.cuda.synchronize()
 
     tr = Trainer.from_config(C2_CONFIG, n_input=2, n_output=3)
@@ -382,8 +379,10 @@ def main() -> int:
     torch.cuda.synchronize()
     print(f"# warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
-    # timed region: the K steps exactly as a caller runs them (no phase events:
-    # an event pair costs ~3.5 us of stream time, ~23 us over a step's seven)
+    # timed region: phase events on one step in `every` (the kernel durations),
+    # the rest run exactly as a caller runs them
+    every = max(1, args.steps // 10)
+    tr.set_training_step_profiling(True, every)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -392,21 +391,11 @@ def main() -> int:
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     elapsed = t1 - t0
-    # profiled pass: the same K steps again (continuing the run) with HIP events
-    # at the phase boundaries on the trainer's stream -> per-kernel durations
-    tr.set_training_step_profiling(True)
-    torch.cuda.synchronize()
-    tp = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + args.steps + i)
-    tr.synchronize()
-    torch.cuda.synchronize()
-    profiled_ms = (time.perf_counter() - tp) * 1e3 / args.steps
     prof = tr.training_step_profile()
     tr.set_training_step_profiling(False)
     losses = loss_dev.cpu().numpy()
     first_loss = float(losses[0])
-    last_loss = float(losses[args.warmup + 2 * args.steps - 1])
+    last_loss = float(losses[args.warmup + args.steps - 1])
     if not (math.isfinite(last_loss) and last_loss < first_loss):
         print(f"bench.py: training did not progress (loss {first_loss} -> {last_loss})",
               file=sys.stderr)
@@ -463,7 +452,8 @@ def main() -> int:
         "infer_samples_per_s": round(infer_sps, 1),
         "infer_config": "C1 (configs[0]): same field, fp32, 2^16 points per call",
         "phase_us_per_step": phases,
-        "profiled_pass_ms_per_step": round(profiled_ms, 4),
+        "profile_every": every,
+        "profiled_steps": int(prof["steps"]),
         "loss_first_last": [round(first_loss, 6), round(last_loss, 6)],
         "roofline": roofline,
         "kernel_rooflines": per_kernel,

@@ -298,10 +298,11 @@ int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding,
 /* ---- step profiling ------------------------------------------------------------ */
 /* Opt-in GPU timing of the fused step's phases, the GPU-timestamp fields of
  * TrainingStepProfile (trainer.h:89-133; set_training_step_profiling,
- * trainer.h:214-217,422-431). While enabled, every training step brackets
+ * trainer.h:214-217,422-431). While enabled, profiled training steps bracket
  * each phase with HIP events on the trainer's stream. The profile holds the
- * sums over all steps since profiling was (re-)enabled; reading it waits for
- * the stream. gpu_*_us are GPU execution microseconds between events. */
+ * sums over the profiled steps since profiling was (re-)enabled; reading it
+ * waits for the stream. gpu_*_us are GPU execution microseconds between
+ * events (each event pair also costs a few microseconds of stream time). */
 typedef struct tmnn_step_profile {
   uint32_t steps;             /* profiled steps summed below */
   uint32_t batch_size;        /* points of the last profiled step */
@@ -314,6 +315,9 @@ typedef struct tmnn_step_profile {
   double gpu_encode_us;       /* hash-grid encode forward (features of the batch) */
 } tmnn_step_profile;
 
+/* enabled: 0 off; k >= 1 profiles one training step in k (the first after
+ * enabling, then every k-th; 1 = every step, the reference's on). Resets the
+ * sums. Negative: TMNN_ERR_INVALID_ARGUMENT. */
 int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled);
 int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
 

@@ -566,3 +566,27 @@ def test_fused_step_keeps_the_training_image_current(name, precision):
         cur, rep = tr.debug_train_image()
     assert cur.size > 0
     assert np.array_equal(cur, rep)
+
+
+def test_step_profiling_samples_one_step_in_k():
+    """TrainingStepProfile with an interval: one training step in k carries
+    the phase events (the first after enabling, then every k-th); 1 is every
+    step, 0 off; a negative interval is an argument error."""
+    _say("step profiling interval")
+    d, enc, net, m_out = GEOMS["small"]
+    rng = np.random.default_rng(9)
+    pos = rng.random((3000, d), dtype=np.float32)
+    tgt = rng.random((3000, m_out), dtype=np.float32)
+    with make_trainer(d, m_out, enc, net) as tr:
+        for every, steps, want in ((3, 7, 3), (1, 4, 4), (5, 5, 1)):
+            tr.set_training_step_profiling(True, every)
+            for _ in range(steps):
+                tr.training_step(pos, tgt)
+            prof = tr.training_step_profile()
+            assert prof["steps"] == want, (every, prof)
+            assert prof["gpu_total_us"] > 0.0
+        tr.set_training_step_profiling(False)
+        tr.training_step(pos, tgt)
+        assert tr.training_step_profile()["steps"] == 0
+        with pytest.raises(ValueError):
+            tr.set_training_step_profiling(True, 0)

@@ -235,9 +235,11 @@ struct tmnn_trainer {
   uint64_t weights_version = 0;  // bumped whenever the parameters change
 
   // Step profiling: one set of phase events per profiled step, summed and
-  // recycled when the profile is read.
+  // recycled when the profile is read. prof_every: 0 off, k >= 1 one training
+  // step in k (the first, then every k-th); prof_seen counts steps since on.
   static constexpr int kProfEvents = 7;  // sort | encode | fwd/bwd | scatter | reduce | adam |
-  bool profiling = false;
+  int32_t prof_every = 0;
+  uint64_t prof_seen = 0;
   std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
   size_t prof_used = 0;
   int prof_cur = -1;  // event set of the step being enqueued, or -1
@@ -290,7 +292,8 @@ bool desc_ok(const tmnn_model_desc *d, std::string &why) {
 // Claims the next event set for a profiled step (prof_cur = -1 when off).
 int prof_begin_step(tmnn_trainer *tr) {
   tr->prof_cur = -1;
-  if (!tr->profiling) return TMNN_OK;
+  if (tr->prof_every <= 0) return TMNN_OK;
+  if (tr->prof_seen++ % static_cast<uint64_t>(tr->prof_every) != 0) return TMNN_OK;
   if (tr->prof_used == tr->prof_events.size()) {
     std::array<hipEvent_t, tmnn_trainer::kProfEvents> set{};
     for (hipEvent_t &e : set) TMNN_HIP_TRY(hipEventCreate(&e));
@@ -1676,11 +1679,13 @@ int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding, float lr_network
 
 int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled) {
   if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (enabled < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "profiling interval must be >= 0");
   TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
   const int rc = prof_collect(tr);  // drop what an earlier window recorded
   if (rc != TMNN_OK) return rc;
   tr->prof_acc = tmnn_step_profile{};
-  tr->profiling = enabled != 0;
+  tr->prof_every = enabled;
+  tr->prof_seen = 0;
   return TMNN_OK;
 }
 

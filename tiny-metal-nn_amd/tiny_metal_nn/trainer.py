@@ -309,10 +309,13 @@ class Trainer:
         _lib.check(self._lib.tmnn_set_learning_rate(self._h, float(lr), float(lr)))
 
     # ---- step profiling (TrainingStepProfile GPU timestamps) -------------------
-    def set_training_step_profiling(self, enabled: bool) -> None:
-        """Enable/disable per-phase GPU event timing of fused steps; resets the sums."""
+    def set_training_step_profiling(self, enabled: bool, every: int = 1) -> None:
+        """Enable/disable per-phase GPU event timing of fused steps (one step in
+        `every` when enabled); resets the sums."""
         self._check_open()
-        _lib.check(self._lib.tmnn_set_step_profiling(self._h, 1 if enabled else 0))
+        if every < 1:
+            raise ValueError("every must be >= 1")
+        _lib.check(self._lib.tmnn_set_step_profiling(self._h, int(every) if enabled else 0))
 
     def training_step_profile(self) -> dict:
         """Per-phase GPU microseconds summed over the profiled steps."""
