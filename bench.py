@@ -328,6 +328,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--profile-every", type=int, default=None, metavar="K",
+                    help="phase events on one timed step in K (0: none)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches): the "
                          "known-size reference for FETCH_SIZE / WRITE_SIZE counters")
@@ -381,8 +383,8 @@ def main() -> int:
 
     # timed region: phase events on one step in `every` (the kernel durations),
     # the rest run exactly as a caller runs them
-    every = max(1, args.steps // 10)
-    tr.set_training_step_profiling(True, every)
+    every = max(1, args.steps // 10) if args.profile_every is None else args.profile_every
+    tr.set_training_step_profiling(every > 0, max(every, 1))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -421,8 +423,8 @@ def main() -> int:
     tr.close()
 
     steps_prof = max(1, prof["steps"])
-    per_kernel = kernel_rooflines(prof)
-    roofline = max(per_kernel, key=lambda r: r["kernel_avg_us"])
+    per_kernel = kernel_rooflines(prof) if prof["steps"] else []
+    roofline = max(per_kernel, key=lambda r: r["kernel_avg_us"]) if per_kernel else None
     phases = {k: round(prof[k] / steps_prof, 2) for k in
               ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",
                "gpu_adam_us", "gpu_total_us")}

@@ -295,6 +295,114 @@ int tmnn_reset_optimizer(tmnn_trainer *tr);
 int tmnn_set_learning_rate(tmnn_trainer *tr, float lr_encoding,
                            float lr_network);
 
+/* ---- runtime authority: RuntimeAuthority (detail/runtime_authority.h:
+ * 110-119) and ITrainerRuntime::batch_plan (trainer.h:186) ----------------- */
+
+/* RuntimeBufferRole (runtime_authority.h:68-79), same numbering. */
+#define TMNN_BUFFER_CONFIG_WEIGHTS 0
+#define TMNN_BUFFER_HASH_WEIGHTS 1
+#define TMNN_BUFFER_MLP_WEIGHTS 2
+#define TMNN_BUFFER_GRAD_HASH 3
+#define TMNN_BUFFER_GRAD_MLP 4
+#define TMNN_BUFFER_TRAIN_PARAMS 5
+#define TMNN_BUFFER_ADAM_PARAMS 6
+#define TMNN_BUFFER_FUSED_WEIGHTS 7
+#define TMNN_BUFFER_FUSED_FIRST_MOMENT 8
+#define TMNN_BUFFER_FUSED_SECOND_MOMENT 9
+
+/* StorageVisibility / ResourceLifetime (runtime_authority.h:21-31). */
+#define TMNN_STORAGE_CPU_VISIBLE 0
+#define TMNN_STORAGE_GPU_ONLY 1
+#define TMNN_LIFETIME_PERSISTENT 0
+#define TMNN_LIFETIME_TRANSIENT 1
+#define TMNN_LIFETIME_STAGING 2
+
+/* Element encoding of a buffer view. I32_PACKED_PAIR: the int32 fixed-point
+ * hash gradients of F == 2 tables, where each entry's two words hold one
+ * 64-bit sum: word 0 is feature 0's int32 sum and feature 1's sum is
+ * word 1 + (word 0 < 0 ? 1 : 0) (two's complement, wrapping).
+ * tmnn_debug_get_gradients returns the unpacked reference layout. */
+#define TMNN_ELEM_F32 0
+#define TMNN_ELEM_I32 1
+#define TMNN_ELEM_I32_PACKED_PAIR 2
+#define TMNN_ELEM_OPAQUE 3
+
+/* RuntimeBufferView (runtime_authority.h:81-93): gpu_buffer + offset is the
+ * role's first byte (device_ptr, for convenience). Device memory only
+ * (cpu_data is always null in this library): read it with hipMemcpy on the
+ * trainer's device, after tmnn_synchronize. The pointers stay valid until the
+ * trainer is destroyed. */
+typedef struct tmnn_buffer_view {
+  uint32_t struct_size;       /* sizeof(tmnn_buffer_view), set by the caller */
+  int32_t role;               /* TMNN_BUFFER_* */
+  void *gpu_buffer;           /* base of the allocation (NULL: no such buffer) */
+  uint64_t offset;            /* byte offset of the role's data in it */
+  uint64_t bytes;             /* 0: no such buffer (RuntimeBufferView::valid() false) */
+  void *device_ptr;           /* gpu_buffer + offset */
+  int32_t element_kind;       /* TMNN_ELEM_* */
+  int32_t visibility;         /* TMNN_STORAGE_* */
+  int32_t lifetime;           /* TMNN_LIFETIME_* */
+} tmnn_buffer_view;
+
+/* ParameterLayout (runtime_authority.h:33-43). This library passes the step
+ * parameters and Adam's hyper-parameters as kernel launch arguments, so the
+ * TrainParams / AdamParams / config-header float counts are 0. */
+typedef struct tmnn_parameter_layout_t {
+  uint32_t struct_size;
+  uint32_t hash_grid_float_count;
+  uint32_t mlp_weight_float_count;
+  uint32_t train_params_float_count;
+  uint32_t train_params_idx_n;
+  uint32_t train_params_idx_unsigned_mode;
+  uint32_t train_params_idx_loss_scale;
+  uint32_t train_params_idx_num_active_levels;
+  uint32_t adam_params_float_count;
+  uint32_t config_header_float_count;
+  uint32_t config_tail_float_count;
+  uint32_t target_dims;
+  uint32_t reduction_terms;
+  int32_t fused_adam;
+} tmnn_parameter_layout_t;
+
+/* TrainerBatchPlan (runtime_authority.h:45-56). max_batch_size is the
+ * configured batch_size (no 65536 cap in this library); one step lane. */
+typedef struct tmnn_batch_plan_t {
+  uint32_t struct_size;
+  uint32_t max_batch_size;
+  uint32_t lane_count;
+  uint32_t input_dims;
+  uint32_t target_dims;
+  uint32_t reduction_terms;
+  uint64_t positions_bytes_per_lane;
+  uint64_t targets_bytes_per_lane;
+  uint64_t reduction_bytes_per_lane;
+  uint32_t threadgroup_size;       /* threads per block of the training kernel */
+  uint32_t points_per_threadgroup; /* points one block takes per round */
+} tmnn_batch_plan_t;
+
+/* RuntimeStoragePolicy (runtime_authority.h:58-66). */
+typedef struct tmnn_storage_policy_t {
+  uint32_t struct_size;
+  int32_t parameter_weights;  /* TMNN_STORAGE_* */
+  int32_t gradients;
+  int32_t optimizer_state;
+  int32_t control_buffers;
+  int32_t step_inputs;        /* TMNN_LIFETIME_* */
+  int32_t step_targets;
+  int32_t step_reduction;
+  int32_t requires_staging_uploads;
+} tmnn_storage_policy_t;
+
+/* RuntimeAuthority::buffer(role) (default_trainer.cpp:263-297). out->struct_size
+ * must be set. Unknown roles: TMNN_ERR_INVALID_ARGUMENT. */
+int tmnn_runtime_buffer(tmnn_trainer *tr, int32_t role, tmnn_buffer_view *out);
+/* RuntimeAuthority::parameter_layout (default_trainer.cpp:258-260). */
+int tmnn_parameter_layout(tmnn_trainer *tr, tmnn_parameter_layout_t *out);
+/* RuntimeAuthority::storage_policy (default_trainer.cpp:261-263). */
+int tmnn_storage_policy(tmnn_trainer *tr, tmnn_storage_policy_t *out);
+/* ITrainerRuntime::batch_plan (trainer.h:186; default_trainer.cpp:1531-1533). */
+int tmnn_batch_plan(tmnn_trainer *tr, tmnn_batch_plan_t *out);
+
 /* ---- step profiling ------------------------------------------------------------ */
 /* Opt-in GPU timing of the fused step's phases, the GPU-timestamp fields of
  * TrainingStepProfile (trainer.h:89-133; set_training_step_profiling,
@@ -328,6 +436,19 @@ int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
 int tmnn_debug_encode(tmnn_trainer *tr, const float *positions, int32_t n,
                       float *features, uint32_t *corner_index,
                       float *corner_weight);
+
+/* The training step's own encode (the feature-tile kernels the step launches,
+ * point- or level-major by the table size, reading the batch through the
+ * step's Morton permutation when `sorted` and the trainer sorts): features
+ * [N][L*F] fp32 in the step's point order, i.e. row j belongs to input row
+ * perm_out[j] (identity when unsorted). sorted_pos_out [N][spatial_dims]
+ * receives the positions the encode wrote for the backward scatter (nullable),
+ * *padding_nonzero the count of nonzero padding floats in the feature tiles
+ * (padding features and points; 0 when correct; nullable). Host memory.
+ * No counterpart in the reference (its training kernel encodes inline). */
+int tmnn_debug_encode_tiles(tmnn_trainer *tr, const float *positions, int32_t n,
+                            int32_t sorted, float *features, uint32_t *perm_out,
+                            float *sorted_pos_out, uint64_t *padding_nonzero);
 
 /* Accumulated gradients in reference layout: int32 fixed-point hash grads
  * [L][T][F] (scale 65536) and fp32 MLP grads. Either pointer may be null. */

@@ -85,6 +85,8 @@ def test_canonicalize_defaults():
     ({"encoding": {"interpolation": "Nearest"}}, "Linear"),
     ({"encoding": {"n_levels": "many"}}, "n_levels"),
     ({"bogus": 1}, "bogus"),
+    ({"mi355x": {"weight_decay": -1.0}}, "weight_decay"),
+    ({"mi355x": {"grad_clip": -0.5}}, "grad_clip"),
 ])
 def test_canonicalize_rejects(bad, frag):
     from tiny_metal_nn import ConfigError, canonicalize_model_config
@@ -118,6 +120,43 @@ def test_model_desc_from_config():
     assert d.lr_encoding == pytest.approx(1e-2) and d.lr_network == pytest.approx(1e-2)
     assert d.loss_kind == _lib.LOSS_RELATIVE_L2 and d.batch_size == 262144
     assert d.precision == _lib.PRECISION_FP16 and d.hash_adam_mode == _lib.HASH_ADAM_DENSE
+    c = canonicalize_model_config(3, 1, {"optimizer": {"l1_reg": 1e-4, "l2_reg": 1e-3},
+                                         "mi355x": {"grad_clip": 0.5, "weight_decay": 0.01}})
+    d = model_desc(c)
+    assert d.l1_reg == pytest.approx(1e-4) and d.l2_reg == pytest.approx(1e-3)
+    assert d.grad_clip == pytest.approx(0.5) and d.weight_decay == pytest.approx(0.01)
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every descriptor struct of include/tmnn_hip.h has the size and field
+    offsets the ctypes binding assumes (compiled with the host C compiler)."""
+    import shutil
+    import subprocess
+    from tiny_metal_nn import _lib
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    structs = {"tmnn_model_desc": _lib.ModelDesc, "tmnn_device_caps": _lib.DeviceCaps,
+               "tmnn_network_plan": _lib.NetworkPlan, "tmnn_step_result": _lib.StepResult,
+               "tmnn_inspection": _lib.Inspection, "tmnn_step_profile": _lib.StepProfile,
+               "tmnn_buffer_view": _lib.BufferView, "tmnn_parameter_layout_t": _lib.ParameterLayout,
+               "tmnn_batch_plan_t": _lib.BatchPlan, "tmnn_storage_policy_t": _lib.StoragePolicy}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tmnn_hip.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                         check=True).stdout.splitlines())
+    for cname, cls in structs.items():
+        assert int(got[cname]) == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert int(got[f"{cname}.{field}"]) == getattr(cls, field).offset, (cname, field)
 
 
 def test_call_guard_releases_and_rejects_concurrent_entry():

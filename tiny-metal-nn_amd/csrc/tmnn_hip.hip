@@ -296,7 +296,10 @@ int prof_begin_step(tmnn_trainer *tr) {
   if (tr->prof_seen++ % static_cast<uint64_t>(tr->prof_every) != 0) return TMNN_OK;
   if (tr->prof_used == tr->prof_events.size()) {
     std::array<hipEvent_t, tmnn_trainer::kProfEvents> set{};
-    for (hipEvent_t &e : set) TMNN_HIP_TRY(hipEventCreate(&e));
+    // timing-only events: no system-scope fence (cache writeback and
+    // invalidate) at each record; prof_collect synchronizes the stream first
+    for (hipEvent_t &e : set)
+      TMNN_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     tr->prof_events.push_back(set);
   }
   tr->prof_cur = static_cast<int>(tr->prof_used++);
@@ -950,17 +953,29 @@ int zero_device(tmnn_trainer *tr, void *ptr, size_t bytes) {
   return TMNN_OK;
 }
 
+// Releases the event set claimed for a step that failed before its last
+// event was recorded (prof_collect would otherwise read unrecorded events).
+void prof_abort(tmnn_trainer *tr) {
+  if (tr->prof_cur >= 0) tr->prof_used = static_cast<size_t>(tr->prof_cur);
+  tr->prof_cur = -1;
+}
+
 int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, int n,
                       float *d_loss) {
   int rc = prof_begin_step(tr);
   if (rc != TMNN_OK) return rc;
   float *loss = d_loss ? d_loss : tr->loss_out.as<float>();
   const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false, loss, false);
-  if (blocks < 0) return blocks;
-  if ((rc = prof_mark(tr, 5)) != TMNN_OK) return rc;
+  if (blocks < 0) {
+    prof_abort(tr);
+    return blocks;
+  }
   // dW reduction, loss and Adam in one kernel (the reduce phase reads ~0)
-  if ((rc = run_finish(tr, blocks, n, loss)) != TMNN_OK) return rc;
-  if ((rc = prof_mark(tr, 6)) != TMNN_OK) return rc;
+  if ((rc = prof_mark(tr, 5)) != TMNN_OK || (rc = run_finish(tr, blocks, n, loss)) != TMNN_OK ||
+      (rc = prof_mark(tr, 6)) != TMNN_OK) {
+    prof_abort(tr);
+    return rc;
+  }
   if (tr->prof_cur >= 0) tr->prof_acc.batch_size = static_cast<uint32_t>(n);
   tr->prof_cur = -1;
   ++tr->step;
@@ -1735,6 +1750,175 @@ int tmnn_debug_encode(tmnn_trainer *tr, const float *positions, int32_t n, float
     TMNN_HIP_TRY(hipMemcpyAsync(corner_weight, tr->dbg_c.ptr, n * L * C * sizeof(float),
                                 hipMemcpyDeviceToHost, st));
   TMNN_HIP_TRY(hipStreamSynchronize(st));
+  return TMNN_OK;
+}
+
+// DefaultAuthority::parameter_layout (default_trainer.cpp:241-260): counts of
+// the fused parameter buffer and the step's per-launch control data. The
+// kernels of this library take the step parameters (N, loss scale, active
+// levels) and Adam's hyper-parameters as launch arguments, so the reference's
+// TrainParams / AdamParams device buffers have no counterpart (float counts 0,
+// TrainParamsLayout indices as the reference's defaults, schema.h:29-35).
+int tmnn_parameter_layout(tmnn_trainer *tr, tmnn_parameter_layout_t *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (out->struct_size != sizeof(tmnn_parameter_layout_t))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_parameter_layout_t.struct_size mismatch");
+  std::memset(out, 0, sizeof *out);
+  out->struct_size = sizeof *out;
+  out->hash_grid_float_count = tr->hash_count;
+  out->mlp_weight_float_count = tr->mlp_count;
+  out->train_params_float_count = 0;
+  out->train_params_idx_n = 0;
+  out->train_params_idx_unsigned_mode = 1;
+  out->train_params_idx_loss_scale = 2;
+  out->train_params_idx_num_active_levels = 3;
+  out->adam_params_float_count = 0;
+  out->config_header_float_count = 0;
+  out->config_tail_float_count = 0;
+  out->target_dims = static_cast<uint32_t>(tr->d.num_outputs);
+  out->reduction_terms = 1;  // one loss partial per training block
+  out->fused_adam = 1;       // Adam runs inside the step's last kernel
+  return TMNN_OK;
+}
+
+// DefaultRuntime::batch_plan (default_trainer.cpp:2333-2360): one step lane
+// (the trainer's stream runs one step at a time), no 65536 cap, and the
+// training kernel's block geometry.
+int tmnn_batch_plan(tmnn_trainer *tr, tmnn_batch_plan_t *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (out->struct_size != sizeof(tmnn_batch_plan_t))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_batch_plan_t.struct_size mismatch");
+  std::memset(out, 0, sizeof *out);
+  out->struct_size = sizeof *out;
+  const uint64_t B = static_cast<uint64_t>(tr->d.batch_size);
+  out->max_batch_size = static_cast<uint32_t>(B);
+  out->lane_count = 1;
+  out->input_dims = static_cast<uint32_t>(tr->d.spatial_dims);
+  out->target_dims = static_cast<uint32_t>(tr->d.num_outputs);
+  out->reduction_terms = 1;
+  out->positions_bytes_per_lane = B * out->input_dims * sizeof(float);
+  out->targets_bytes_per_lane = B * out->target_dims * sizeof(float);
+  out->reduction_bytes_per_lane = static_cast<uint64_t>(tr->train_plan.max_blocks) * sizeof(float);
+  const int tile = tr->train_plan.wide ? kWideWaves * kTilePts : kTilePts;
+  out->threadgroup_size = static_cast<uint32_t>(64 * tr->train_plan.wpb);
+  out->points_per_threadgroup =
+      static_cast<uint32_t>(tr->train_plan.wide ? tile : kTilePts * tr->train_plan.wpb);
+  return TMNN_OK;
+}
+
+// RuntimeStoragePolicy (runtime_authority.h:57-66): every buffer is device
+// memory (hipMalloc); host access goes through explicit copies.
+int tmnn_storage_policy(tmnn_trainer *tr, tmnn_storage_policy_t *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (out->struct_size != sizeof(tmnn_storage_policy_t))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_storage_policy_t.struct_size mismatch");
+  std::memset(out, 0, sizeof *out);
+  out->struct_size = sizeof *out;
+  out->parameter_weights = TMNN_STORAGE_GPU_ONLY;
+  out->gradients = TMNN_STORAGE_GPU_ONLY;
+  out->optimizer_state = TMNN_STORAGE_GPU_ONLY;
+  out->control_buffers = TMNN_STORAGE_GPU_ONLY;
+  out->step_inputs = TMNN_LIFETIME_TRANSIENT;
+  out->step_targets = TMNN_LIFETIME_TRANSIENT;
+  out->step_reduction = TMNN_LIFETIME_TRANSIENT;
+  out->requires_staging_uploads = 1;
+  return TMNN_OK;
+}
+
+// DefaultAuthority::buffer(role) (default_trainer.cpp:263-297): the device
+// range holding a role's data. Roles whose data this library passes as
+// launch arguments (TrainParams, AdamParams) return an empty view, as the
+// reference does for a buffer it does not have (RuntimeBufferView::valid()
+// is false). ConfigWeights is the training kernel's packed weight image (its
+// layout is this library's, not the reference's 8-float header + MLP copy).
+int tmnn_runtime_buffer(tmnn_trainer *tr, int32_t role, tmnn_buffer_view *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (out->struct_size != sizeof(tmnn_buffer_view))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_buffer_view.struct_size mismatch");
+  std::memset(out, 0, sizeof *out);
+  out->struct_size = sizeof *out;
+  out->role = role;
+  out->visibility = TMNN_STORAGE_GPU_ONLY;
+  out->lifetime = TMNN_LIFETIME_PERSISTENT;
+  const uint64_t hb = static_cast<uint64_t>(tr->hash_count) * sizeof(float);
+  const uint64_t mb = static_cast<uint64_t>(tr->mlp_count) * sizeof(float);
+  auto set = [&](void *base, uint64_t off, uint64_t bytes, int32_t elem) {
+    out->gpu_buffer = base;
+    out->offset = off;
+    out->bytes = bytes;
+    out->element_kind = elem;
+    out->device_ptr = base ? static_cast<uint8_t *>(base) + off : nullptr;
+  };
+  switch (role) {
+    case TMNN_BUFFER_CONFIG_WEIGHTS:
+      set(tr->train_plan.image, 0, tr->train_plan.image_bytes, TMNN_ELEM_OPAQUE);
+      break;
+    case TMNN_BUFFER_HASH_WEIGHTS: set(tr->params.ptr, 0, hb, TMNN_ELEM_F32); break;
+    case TMNN_BUFFER_MLP_WEIGHTS: set(tr->params.ptr, hb, mb, TMNN_ELEM_F32); break;
+    case TMNN_BUFFER_GRAD_HASH:
+      set(tr->grad_hash.ptr, 0, static_cast<uint64_t>(tr->hash_count) * sizeof(int32_t),
+          tr->d.features_per_level == 2 ? TMNN_ELEM_I32_PACKED_PAIR : TMNN_ELEM_I32);
+      break;
+    case TMNN_BUFFER_GRAD_MLP: set(tr->grad_mlp.ptr, 0, mb, TMNN_ELEM_F32); break;
+    case TMNN_BUFFER_TRAIN_PARAMS:
+    case TMNN_BUFFER_ADAM_PARAMS:
+      set(nullptr, 0, 0, TMNN_ELEM_F32);
+      break;
+    case TMNN_BUFFER_FUSED_WEIGHTS: set(tr->params.ptr, 0, hb + mb, TMNN_ELEM_F32); break;
+    case TMNN_BUFFER_FUSED_FIRST_MOMENT: set(tr->m.ptr, 0, hb + mb, TMNN_ELEM_F32); break;
+    case TMNN_BUFFER_FUSED_SECOND_MOMENT: set(tr->v.ptr, 0, hb + mb, TMNN_ELEM_F32); break;
+    default: return fail(TMNN_ERR_INVALID_ARGUMENT, "unknown RuntimeBufferRole");
+  }
+  return TMNN_OK;
+}
+
+int tmnn_debug_encode_tiles(tmnn_trainer *tr, const float *positions, int32_t n, int32_t sorted,
+                            float *features, uint32_t *perm_out, float *sorted_pos_out,
+                            uint64_t *padding_nonzero) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "N must be non-negative");
+  if (n == 0) return TMNN_OK;
+  if (!positions || !features) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  int rc = ensure_batch(tr, n);
+  if (rc != TMNN_OK) return rc;
+  const size_t D = tr->d.spatial_dims;
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, positions, n * D * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const float *pos = tr->in_pos.as<float>(), *unused = nullptr;
+  const uint32_t *perm = nullptr;
+  if (sorted) {
+    rc = sort_batch(tr, tr->in_pos.as<float>(), nullptr, 0, n, &pos, &unused, &perm, false);
+    if (rc != TMNN_OK) return rc;
+  }
+  float *pos_out = perm ? tr->s_pos.as<float>() : nullptr;
+  if ((rc = launch_encode(tr, pos, n, perm, pos_out)) != TMNN_OK) return rc;
+  const int n_pad = (n + kTilePts - 1) / kTilePts * kTilePts;
+  const int KT0 = tr->INP / 16;
+  std::vector<float> tiles(static_cast<size_t>(n_pad) * tr->INP);
+  TMNN_HIP_TRY(hipMemcpyAsync(tiles.data(), tr->xfeat.ptr, tiles.size() * sizeof(float),
+                              hipMemcpyDeviceToHost, st));
+  if (perm_out && perm)
+    TMNN_HIP_TRY(hipMemcpyAsync(perm_out, perm, n * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  if (sorted_pos_out && perm)
+    TMNN_HIP_TRY(hipMemcpyAsync(sorted_pos_out, pos_out, n * D * sizeof(float),
+                                hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  if (perm_out && !perm)
+    for (int i = 0; i < n; ++i) perm_out[i] = static_cast<uint32_t>(i);
+  if (sorted_pos_out && !perm)
+    std::memcpy(sorted_pos_out, positions, n * D * sizeof(float));
+  uint64_t pad = 0;
+  for (int i = 0; i < n_pad; ++i)
+    for (int f = 0; f < tr->INP; ++f) {
+      const float x = tiles[xtile_offset(i, f / 4, KT0) + f % 4];
+      if (i < n && f < tr->IN)
+        features[static_cast<size_t>(i) * tr->IN + f] = x;
+      else if (x != 0.0f)
+        ++pad;
+    }
+  if (padding_nonzero) *padding_nonzero = pad;
   return TMNN_OK;
 }
 

@@ -133,6 +133,52 @@ class StepProfile(ctypes.Structure):
     ]
 
 
+# RuntimeBufferRole (runtime_authority.h:68-79), same numbering
+BUFFER_ROLES = {"ConfigWeights": 0, "HashWeights": 1, "MlpWeights": 2, "GradHash": 3,
+                "GradMlp": 4, "TrainParams": 5, "AdamParams": 6, "FusedWeights": 7,
+                "FusedFirstMoment": 8, "FusedSecondMoment": 9}
+ELEMENT_KINDS = {0: "f32", 1: "i32", 2: "i32_packed_pair", 3: "opaque"}
+STORAGE = {0: "CpuVisible", 1: "GpuOnly"}
+LIFETIMES = {0: "Persistent", 1: "Transient", 2: "Staging"}
+
+
+class BufferView(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("role", ctypes.c_int32),
+        ("gpu_buffer", ctypes.c_void_p),
+        ("offset", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+        ("device_ptr", ctypes.c_void_p),
+        ("element_kind", ctypes.c_int32),
+        ("visibility", ctypes.c_int32),
+        ("lifetime", ctypes.c_int32),
+    ]
+
+
+class ParameterLayout(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_uint32) for k in (
+        "struct_size", "hash_grid_float_count", "mlp_weight_float_count",
+        "train_params_float_count", "train_params_idx_n", "train_params_idx_unsigned_mode",
+        "train_params_idx_loss_scale", "train_params_idx_num_active_levels",
+        "adam_params_float_count", "config_header_float_count", "config_tail_float_count",
+        "target_dims", "reduction_terms")] + [("fused_adam", ctypes.c_int32)]
+
+
+class BatchPlan(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_uint32) for k in (
+        "struct_size", "max_batch_size", "lane_count", "input_dims", "target_dims",
+        "reduction_terms")] + [(k, ctypes.c_uint64) for k in (
+            "positions_bytes_per_lane", "targets_bytes_per_lane", "reduction_bytes_per_lane")] + [
+        (k, ctypes.c_uint32) for k in ("threadgroup_size", "points_per_threadgroup")]
+
+
+class StoragePolicy(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32)] + [(k, ctypes.c_int32) for k in (
+        "parameter_weights", "gradients", "optimizer_state", "control_buffers", "step_inputs",
+        "step_targets", "step_reduction", "requires_staging_uploads")]
+
+
 _V = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _U32 = ctypes.c_uint32
@@ -178,7 +224,13 @@ SIGNATURES = {
     "tmnn_set_learning_rate": (ctypes.c_int, [_V, _F, _F]),
     "tmnn_set_step_profiling": (ctypes.c_int, [_V, _I32]),
     "tmnn_get_step_profile": (ctypes.c_int, [_V, ctypes.POINTER(StepProfile)]),
+    "tmnn_runtime_buffer": (ctypes.c_int, [_V, _I32, ctypes.POINTER(BufferView)]),
+    "tmnn_parameter_layout": (ctypes.c_int, [_V, ctypes.POINTER(ParameterLayout)]),
+    "tmnn_storage_policy": (ctypes.c_int, [_V, ctypes.POINTER(StoragePolicy)]),
+    "tmnn_batch_plan": (ctypes.c_int, [_V, ctypes.POINTER(BatchPlan)]),
     "tmnn_debug_encode": (ctypes.c_int, [_V, _V, _I32, _V, _V, _V]),
+    "tmnn_debug_encode_tiles": (ctypes.c_int, [_V, _V, _I32, _I32, _V, _V, _V,
+                                               ctypes.POINTER(ctypes.c_uint64)]),
     "tmnn_debug_get_gradients": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
     "tmnn_debug_get_active_mask": (ctypes.c_int, [_V, _V, _SZ]),
     "tmnn_debug_morton_sort": (ctypes.c_int, [_V, _V, _I32, _V, _V]),

@@ -192,12 +192,16 @@ def canonicalize_model_config(n_input: int, n_output: int, config: dict) -> dict
         errors.append("batch_size: must be >= 1")
 
     mi = config.get("mi355x", {}) or {}
-    _known(mi, {"precision", "hash_adam", "morton_sort", "grad_clip", "family"}, "mi355x", errors)
+    _known(mi, {"precision", "hash_adam", "morton_sort", "grad_clip", "weight_decay", "family"},
+           "mi355x", errors)
     m = {
         "precision": _get(mi, "precision", "fp32", str, "mi355x", errors),
         "hash_adam": _get(mi, "hash_adam", "lazy", str, "mi355x", errors),
         "morton_sort": _get(mi, "morton_sort", True, bool, "mi355x", errors),
         "grad_clip": _get(mi, "grad_clip", 0.0, float, "mi355x", errors),
+        # decoupled (AdamW) decay of the adapters' training configs
+        # (extension/training_adapter.h:43; adam_kernel_msl.h:85-88)
+        "weight_decay": _get(mi, "weight_decay", 0.0, float, "mi355x", errors),
         # NetworkFactoryOptions::forced_family (network_planning.h:146-158)
         "family": _get(mi, "family", "auto", str, "mi355x", errors),
     }
@@ -207,6 +211,9 @@ def canonicalize_model_config(n_input: int, n_output: int, config: dict) -> dict
         errors.append("mi355x.precision: must be 'fp32' or 'fp16'")
     if m["hash_adam"] not in ("lazy", "dense"):
         errors.append("mi355x.hash_adam: must be 'lazy' or 'dense'")
+    for k in ("grad_clip", "weight_decay"):
+        if isinstance(m[k], float) and m[k] < 0.0:
+            errors.append(f"mi355x.{k}: must be >= 0")
 
     if errors:
         raise ConfigError("; ".join(errors))
@@ -246,6 +253,7 @@ def model_desc(canonical: dict) -> _lib.ModelDesc:
     d.l1_reg = o["l1_reg"]
     d.l2_reg = o["l2_reg"]
     d.grad_clip = m["grad_clip"]
+    d.weight_decay = m.get("weight_decay", 0.0)
     d.batch_size = c["batch_size"]
     d.precision = _lib.PRECISION_FP16 if m["precision"] == "fp16" else _lib.PRECISION_FP32
     d.hash_adam_mode = _lib.HASH_ADAM_DENSE if m["hash_adam"] == "dense" else _lib.HASH_ADAM_LAZY

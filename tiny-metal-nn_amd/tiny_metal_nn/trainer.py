@@ -199,10 +199,10 @@ class Trainer:
     def training_step_device(self, input_ptr: int, target_ptr: int, n: int,
                              loss_ptr: int = 0) -> None:
         """Enqueue one step on device-resident data (no host synchronization)."""
-        self._check_open()
-        _lib.check(self._lib.tmnn_training_step_device(
-            self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(target_ptr), int(n),
-            ctypes.c_void_p(loss_ptr) if loss_ptr else None))
+        with self._enter("training_step_device"):
+            _lib.check(self._lib.tmnn_training_step_device(
+                self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(target_ptr), int(n),
+                ctypes.c_void_p(loss_ptr) if loss_ptr else None))
 
     def inference(self, input) -> np.ndarray:
         """Evaluate at N positions; returns a fresh (N, n_output) float32 array."""
@@ -228,13 +228,13 @@ class Trainer:
         return out, jac
 
     def inference_device(self, input_ptr: int, output_ptr: int, n: int) -> None:
-        self._check_open()
-        _lib.check(self._lib.tmnn_inference_device(
-            self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(output_ptr), int(n)))
+        with self._enter("inference_device"):
+            _lib.check(self._lib.tmnn_inference_device(
+                self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(output_ptr), int(n)))
 
     def synchronize(self) -> None:
-        self._check_open()
-        _lib.check(self._lib.tmnn_synchronize(self._h))
+        with self._enter("synchronize"):
+            _lib.check(self._lib.tmnn_synchronize(self._h))
 
     # ---- split / accumulate path -------------------------------------------
     def forward_for_training(self, input) -> np.ndarray:
@@ -247,8 +247,8 @@ class Trainer:
         return out[: written.value // self.n_output]
 
     def zero_gradients(self) -> None:
-        self._check_open()
-        _lib.check(self._lib.tmnn_zero_gradients(self._h))
+        with self._enter("zero_gradients"):
+            _lib.check(self._lib.tmnn_zero_gradients(self._h))
 
     def backward_accumulate(self, input, d_output) -> None:
         x = _as_f32_2d(input, "input", self.n_input)
@@ -259,19 +259,18 @@ class Trainer:
             _lib.check(self._lib.tmnn_backward_accumulate(self._h, _ptr(x), _ptr(g), x.shape[0]))
 
     def adam_step(self) -> None:
-        self._check_open()
-        _lib.check(self._lib.tmnn_adam_step(self._h))
+        with self._enter("adam_step"):
+            _lib.check(self._lib.tmnn_adam_step(self._h))
 
     # ---- state ---------------------------------------------------------------
     def get_weights(self) -> tuple[np.ndarray, np.ndarray]:
-        self._check_open()
         hw = np.empty(self.hash_param_count, np.float32)
         mw = np.empty(self.mlp_param_count, np.float32)
-        _lib.check(self._lib.tmnn_get_weights(self._h, _ptr(hw), hw.size, _ptr(mw), mw.size))
+        with self._enter("get_weights"):
+            _lib.check(self._lib.tmnn_get_weights(self._h, _ptr(hw), hw.size, _ptr(mw), mw.size))
         return hw, mw
 
     def set_initial_weights(self, hash_weights=None, mlp_weights=None) -> None:
-        self._check_open()
         hp, hn, mp, mn = None, 0, None, 0
         if hash_weights is not None:
             hash_weights = np.ascontiguousarray(hash_weights, np.float32).ravel()
@@ -279,50 +278,98 @@ class Trainer:
         if mlp_weights is not None:
             mlp_weights = np.ascontiguousarray(mlp_weights, np.float32).ravel()
             mp, mn = _ptr(mlp_weights), mlp_weights.size
-        _lib.check(self._lib.tmnn_set_initial_weights(self._h, hp, hn, mp, mn))
+        with self._enter("set_initial_weights"):
+            _lib.check(self._lib.tmnn_set_initial_weights(self._h, hp, hn, mp, mn))
 
     def export_optimizer_state(self) -> OptimizerStateBlob:
-        self._check_open()
         n = ctypes.c_size_t()
         ver, st = ctypes.c_uint32(), ctypes.c_uint32()
-        _lib.check(self._lib.tmnn_export_optimizer_state(self._h, ctypes.byref(ver),
-                                                         ctypes.byref(st), None, 0,
-                                                         ctypes.byref(n)))
-        buf = (ctypes.c_uint8 * n.value)()
-        _lib.check(self._lib.tmnn_export_optimizer_state(self._h, ctypes.byref(ver),
-                                                         ctypes.byref(st), buf, n.value,
-                                                         ctypes.byref(n)))
+        with self._enter("export_optimizer_state"):
+            _lib.check(self._lib.tmnn_export_optimizer_state(self._h, ctypes.byref(ver),
+                                                             ctypes.byref(st), None, 0,
+                                                             ctypes.byref(n)))
+            buf = (ctypes.c_uint8 * n.value)()
+            _lib.check(self._lib.tmnn_export_optimizer_state(self._h, ctypes.byref(ver),
+                                                             ctypes.byref(st), buf, n.value,
+                                                             ctypes.byref(n)))
         return OptimizerStateBlob(ver.value, st.value, bytes(buf))
 
     def import_optimizer_state(self, blob: OptimizerStateBlob) -> None:
-        self._check_open()
         data = (ctypes.c_uint8 * len(blob.payload)).from_buffer_copy(blob.payload)
-        _lib.check(self._lib.tmnn_import_optimizer_state(self._h, blob.version, blob.step,
-                                                         data, len(blob.payload)))
+        with self._enter("import_optimizer_state"):
+            _lib.check(self._lib.tmnn_import_optimizer_state(self._h, blob.version, blob.step,
+                                                             data, len(blob.payload)))
 
     def reset_optimizer(self) -> None:
-        self._check_open()
-        _lib.check(self._lib.tmnn_reset_optimizer(self._h))
+        with self._enter("reset_optimizer"):
+            _lib.check(self._lib.tmnn_reset_optimizer(self._h))
 
     def set_learning_rate(self, lr: float) -> None:
-        self._check_open()
-        _lib.check(self._lib.tmnn_set_learning_rate(self._h, float(lr), float(lr)))
+        with self._enter("set_learning_rate"):
+            _lib.check(self._lib.tmnn_set_learning_rate(self._h, float(lr), float(lr)))
 
     # ---- step profiling (TrainingStepProfile GPU timestamps) -------------------
     def set_training_step_profiling(self, enabled: bool, every: int = 1) -> None:
         """Enable/disable per-phase GPU event timing of fused steps (one step in
         `every` when enabled); resets the sums."""
-        self._check_open()
         if every < 1:
             raise ValueError("every must be >= 1")
-        _lib.check(self._lib.tmnn_set_step_profiling(self._h, int(every) if enabled else 0))
+        with self._enter("set_training_step_profiling"):
+            _lib.check(self._lib.tmnn_set_step_profiling(self._h, int(every) if enabled else 0))
 
     def training_step_profile(self) -> dict:
         """Per-phase GPU microseconds summed over the profiled steps."""
-        self._check_open()
         p = _lib.StepProfile()
-        _lib.check(self._lib.tmnn_get_step_profile(self._h, ctypes.byref(p)))
+        with self._enter("training_step_profile"):
+            _lib.check(self._lib.tmnn_get_step_profile(self._h, ctypes.byref(p)))
         return {k: getattr(p, k) for k, _ in _lib.StepProfile._fields_}
+
+    # ---- runtime authority (RuntimeAuthority / batch_plan) ----------------------
+    def runtime_buffer(self, role: str) -> dict:
+        """RuntimeAuthority::buffer(role): the device range of a buffer role
+        (pointer, offset, bytes, element kind); bytes == 0 for roles this
+        library passes as launch arguments."""
+        self._check_open()
+        if role not in _lib.BUFFER_ROLES:
+            raise ValueError(f"unknown RuntimeBufferRole {role!r}")
+        v = _lib.BufferView()
+        v.struct_size = ctypes.sizeof(v)
+        _lib.check(self._lib.tmnn_runtime_buffer(self._h, _lib.BUFFER_ROLES[role], ctypes.byref(v)))
+        return {"role": role, "gpu_buffer": v.gpu_buffer or 0, "offset": v.offset,
+                "bytes": v.bytes, "device_ptr": v.device_ptr or 0,
+                "element_kind": _lib.ELEMENT_KINDS[v.element_kind],
+                "visibility": _lib.STORAGE[v.visibility],
+                "lifetime": _lib.LIFETIMES[v.lifetime], "valid": bool(v.gpu_buffer and v.bytes)}
+
+    def parameter_layout(self) -> dict:
+        """RuntimeAuthority::parameter_layout."""
+        self._check_open()
+        p = _lib.ParameterLayout()
+        p.struct_size = ctypes.sizeof(p)
+        _lib.check(self._lib.tmnn_parameter_layout(self._h, ctypes.byref(p)))
+        return {k: getattr(p, k) for k, _ in _lib.ParameterLayout._fields_ if k != "struct_size"}
+
+    def storage_policy(self) -> dict:
+        """RuntimeAuthority::storage_policy."""
+        self._check_open()
+        p = _lib.StoragePolicy()
+        p.struct_size = ctypes.sizeof(p)
+        _lib.check(self._lib.tmnn_storage_policy(self._h, ctypes.byref(p)))
+        out = {k: getattr(p, k) for k, _ in _lib.StoragePolicy._fields_ if k != "struct_size"}
+        for k in ("parameter_weights", "gradients", "optimizer_state", "control_buffers"):
+            out[k] = _lib.STORAGE[out[k]]
+        for k in ("step_inputs", "step_targets", "step_reduction"):
+            out[k] = _lib.LIFETIMES[out[k]]
+        out["requires_staging_uploads"] = bool(out["requires_staging_uploads"])
+        return out
+
+    def batch_plan(self) -> dict:
+        """ITrainerRuntime::batch_plan (TrainerBatchPlan)."""
+        self._check_open()
+        p = _lib.BatchPlan()
+        p.struct_size = ctypes.sizeof(p)
+        _lib.check(self._lib.tmnn_batch_plan(self._h, ctypes.byref(p)))
+        return {k: getattr(p, k) for k, _ in _lib.BatchPlan._fields_ if k != "struct_size"}
 
     # ---- inspection hooks (parity tests) --------------------------------------
     def debug_encode(self, positions, with_corners: bool = False):
@@ -338,6 +385,23 @@ class Trainer:
             self._h, _ptr(x), n, _ptr(feats), _ptr(idx) if with_corners else None,
             _ptr(w) if with_corners else None))
         return (feats, idx, w) if with_corners else feats
+
+    def debug_encode_tiles(self, positions, sorted: bool = True):
+        """The training step's own encode kernels: (features [N][L*F] in the
+        step's point order, perm (row j is input row perm[j]), the sorted
+        positions the encode wrote, count of nonzero padding floats)."""
+        x = _as_f32_2d(positions, "positions", self.n_input)
+        e = self.config["encoding"]
+        n = x.shape[0]
+        feats = np.empty((n, e["n_levels"] * e["n_features_per_level"]), np.float32)
+        perm = np.empty(n, np.uint32)
+        spos = np.empty((n, self.n_input), np.float32)
+        pad = ctypes.c_uint64(0)
+        with self._enter("debug_encode_tiles"):
+            _lib.check(self._lib.tmnn_debug_encode_tiles(self._h, _ptr(x), n, 1 if sorted else 0,
+                                                         _ptr(feats), _ptr(perm), _ptr(spos),
+                                                         ctypes.byref(pad)))
+        return feats, perm, spos, pad.value
 
     def debug_gradients(self) -> tuple[np.ndarray, np.ndarray]:
         self._check_open()
