@@ -228,6 +228,31 @@ int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input,
                               const float *d_target, int32_t n,
                               float *d_loss_out);
 
+/* Bytes of the per-device scratch behind tmnn_training_step_device_noalloc. */
+#define TMNN_NOALLOC_SCRATCH_BYTES (80u << 20)
+
+/* Allocation-free variant of tmnn_training_step_device. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, same result, same kernels; it calls no
+ * hipMalloc / hipFree / hipEventCreate: the step's batch-sized buffers (sort
+ * keys and values, radix histograms, sorted positions and targets, feature
+ * tiles, input-feature gradients) live in a fixed device scratch of
+ * TMNN_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, instead
+ * of trainer buffers grown on demand. Trainer state (parameters, moments,
+ * gradients, visit flags, dW partial rows) was allocated by
+ * tmnn_trainer_create. The scratch needs about
+ * (16 + 4 * (spatial_dims + num_outputs) + 4 * (input_padded + L * F)) bytes
+ * per point (each region rounded to 256 bytes, plus the radix histograms):
+ * the C2 image-fit step (2D, 16x2 features, 3 outputs) fits 2^18 points.
+ * Larger batches return TMNN_ERR_INVALID_ARGUMENT; hidden width 128 returns
+ * TMNN_ERR_UNSUPPORTED. Steps are not profiled. Every call on one GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (trainers on different
+ * streams) race. */
+int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
+                                      const float *d_target, int32_t n,
+                                      float *d_loss_out);
+
 /* FieldEvaluator::evaluate / Trainer::inference (evaluator.h:22-59;
  * default_trainer.cpp:321-465): fp32, unsorted, no batch cap.
  * positions [N][spatial_dims] -> output [N][num_outputs], host memory. */

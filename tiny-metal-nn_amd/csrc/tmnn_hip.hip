@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -34,6 +35,17 @@
 
 using namespace tmnn_hip;
 
+// Device scratch of the allocation-free training step
+// (tmnn_training_step_device_noalloc): the step's batch-sized buffers --
+// sort keys and values, radix histograms, sorted positions and targets, the
+// feature tiles and the input-feature gradients -- for batches up to
+// TMNN_NOALLOC_SCRATCH_BYTES. Each GPU the library runs on holds its own copy
+// until the process ends; host code reaches it only through the device
+// address hipGetSymbolAddress returns for the current device (tmnn_context).
+// Every kernel of the step writes its region before reading it, so nothing
+// in it needs clearing; calls that overlap on one GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[TMNN_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 constexpr uint32_t kAbiVersion = 2u;
@@ -41,6 +53,10 @@ constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr uint32_t kOptimizerBlobVersion = 1u;  // detail/checkpoint_contract.h:14
 
 thread_local std::string g_last_error;
+
+// Device address of `scratch` per device ordinal, looked up once per device.
+std::mutex g_scratch_mu;
+std::vector<unsigned char *> g_scratch_dev;
 
 int fail(int code, const std::string &msg) {
   g_last_error = msg;
@@ -154,14 +170,16 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
 struct DevBuf {
   void *ptr = nullptr;
   size_t bytes = 0;
+  bool borrowed = false;  // ptr is a region of the device scratch (never freed or grown)
   DevBuf() = default;
   DevBuf(const DevBuf &) = delete;
   DevBuf &operator=(const DevBuf &) = delete;
   ~DevBuf() {
-    if (ptr) (void)hipFree(ptr);
+    if (ptr && !borrowed) (void)hipFree(ptr);
   }
   hipError_t ensure(size_t want) {
     if (want <= bytes) return hipSuccess;
+    if (borrowed) return hipErrorInvalidValue;  // a scratch region never grows
     if (ptr) {
       (void)hipFree(ptr);
       ptr = nullptr;
@@ -203,6 +221,7 @@ struct tmnn_context {
   int cu_count = 0;
   uint64_t mem_bytes = 0;
   std::string name;
+  unsigned char *scratch = nullptr;  // this device's copy of the step scratch (device address)
 };
 
 struct tmnn_trainer {
@@ -243,6 +262,7 @@ struct tmnn_trainer {
   std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
   size_t prof_used = 0;
   int prof_cur = -1;  // event set of the step being enqueued, or -1
+  bool prof_suspended = false;  // allocation-free steps record no events
   tmnn_step_profile prof_acc{};
 
   ~tmnn_trainer() {
@@ -292,7 +312,7 @@ bool desc_ok(const tmnn_model_desc *d, std::string &why) {
 // Claims the next event set for a profiled step (prof_cur = -1 when off).
 int prof_begin_step(tmnn_trainer *tr) {
   tr->prof_cur = -1;
-  if (tr->prof_every <= 0) return TMNN_OK;
+  if (tr->prof_every <= 0 || tr->prof_suspended) return TMNN_OK;
   if (tr->prof_seen++ % static_cast<uint64_t>(tr->prof_every) != 0) return TMNN_OK;
   if (tr->prof_used == tr->prof_events.size()) {
     std::array<hipEvent_t, tmnn_trainer::kProfEvents> set{};
@@ -1081,6 +1101,17 @@ int tmnn_context_create(int32_t device, tmnn_context **out) {
   ctx->mem_bytes = prop.totalGlobalMem;
   ctx->name = prop.gcnArchName;
   TMNN_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+  {
+    // this device's copy of the step scratch, with the device current
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev.size() < static_cast<size_t>(count)) g_scratch_dev.resize(count, nullptr);
+    if (!g_scratch_dev[device]) {
+      void *p = nullptr;
+      TMNN_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      g_scratch_dev[device] = static_cast<unsigned char *>(p);
+    }
+    ctx->scratch = g_scratch_dev[device];
+  }
   *out = ctx.release();
   return TMNN_OK;
 }
@@ -1350,6 +1381,64 @@ int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input, const floa
   const int rc = ensure_batch(tr, bn);
   if (rc != TMNN_OK) return rc;
   return train_step_device(tr, d_input, d_target, bn, d_loss_out);
+}
+
+int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
+                                      const float *d_target, int32_t n, float *d_loss_out) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
+  if (!d_input || !d_target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
+  if (!tr->ctx->scratch) return fail(TMNN_ERR_RUNTIME, "device scratch address unknown");
+  if (tr->train_plan.wide)
+    return fail(TMNN_ERR_UNSUPPORTED,
+                "the allocation-free step does not run hidden width 128 (its activation "
+                "buffers exceed the scratch): use tmnn_training_step_device");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int bn = std::min(n, tr->d.batch_size);
+  // carve the scratch: [keys0 | keys1 | vals0 | vals1 | sort tmp | s_pos | s_tgt | xfeat | dx]
+  const size_t D = tr->d.spatial_dims, M = tr->d.num_outputs;
+  const size_t n_pad = static_cast<size_t>((bn + kTilePts - 1) / kTilePts) * kTilePts;
+  size_t sort_bytes = 0;
+  TMNN_HIP_TRY(morton_sort_temp_bytes(bn, &sort_bytes));
+  DevBuf *bufs[] = {&tr->keys0, &tr->keys1, &tr->vals0, &tr->vals1, &tr->sort_tmp,
+                    &tr->s_pos, &tr->s_tgt, &tr->xfeat, &tr->dx};
+  const size_t want[] = {bn * sizeof(uint32_t), bn * sizeof(uint32_t), bn * sizeof(uint32_t),
+                         bn * sizeof(uint32_t), std::max<size_t>(sort_bytes, 256),
+                         bn * D * sizeof(float), bn * M * sizeof(float),
+                         n_pad * tr->INP * sizeof(float), n_pad * tr->IN * sizeof(float)};
+  constexpr int kRegions = sizeof(want) / sizeof(want[0]);
+  size_t off[kRegions], total = 0;
+  for (int r = 0; r < kRegions; ++r) {
+    off[r] = total;
+    total += (want[r] + 255) / 256 * 256;
+  }
+  if (total > TMNN_NOALLOC_SCRATCH_BYTES)
+    return fail(TMNN_ERR_INVALID_ARGUMENT,
+                "training_step_device_noalloc: a batch of " + std::to_string(bn) +
+                    " points needs " + std::to_string(total) + " bytes of scratch, above the " +
+                    std::to_string(static_cast<size_t>(TMNN_NOALLOC_SCRATCH_BYTES)) +
+                    "-byte maximum");
+  // lend the regions to the step's buffers for this call, then give them back
+  struct Saved {
+    void *ptr;
+    size_t bytes;
+    bool borrowed;
+  } saved[kRegions];
+  for (int r = 0; r < kRegions; ++r) {
+    saved[r] = {bufs[r]->ptr, bufs[r]->bytes, bufs[r]->borrowed};
+    bufs[r]->ptr = tr->ctx->scratch + off[r];
+    bufs[r]->bytes = want[r];
+    bufs[r]->borrowed = true;
+  }
+  tr->prof_suspended = true;
+  const int rc = train_step_device(tr, d_input, d_target, bn, d_loss_out);
+  tr->prof_suspended = false;
+  for (int r = 0; r < kRegions; ++r) {
+    bufs[r]->ptr = saved[r].ptr;
+    bufs[r]->bytes = saved[r].bytes;
+    bufs[r]->borrowed = saved[r].borrowed;
+  }
+  return rc;
 }
 
 int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions, float *d_output,

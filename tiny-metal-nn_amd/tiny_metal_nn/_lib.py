@@ -206,6 +206,7 @@ SIGNATURES = {
                                          ctypes.POINTER(NetworkPlan)]),
     "tmnn_training_step": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(StepResult)]),
     "tmnn_training_step_device": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
+    "tmnn_training_step_device_noalloc": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
     "tmnn_inference": (ctypes.c_int, [_V, _V, _V, _I32]),
     "tmnn_inference_device": (ctypes.c_int, [_V, _V, _V, _I32]),
     "tmnn_evaluate_with_gradient": (ctypes.c_int, [_V, _V, _V, _V, _I32]),

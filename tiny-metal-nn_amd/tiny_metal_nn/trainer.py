@@ -204,6 +204,16 @@ class Trainer:
                 self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(target_ptr), int(n),
                 ctypes.c_void_p(loss_ptr) if loss_ptr else None))
 
+    def training_step_device_noalloc(self, input_ptr: int, target_ptr: int, n: int,
+                                     loss_ptr: int = 0) -> None:
+        """training_step_device without any device allocation: the step's
+        batch buffers live in the library's fixed per-GPU scratch (batches up
+        to its size; calls overlapping on one GPU race)."""
+        with self._enter("training_step_device_noalloc"):
+            _lib.check(self._lib.tmnn_training_step_device_noalloc(
+                self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(target_ptr), int(n),
+                ctypes.c_void_p(loss_ptr) if loss_ptr else None))
+
     def inference(self, input) -> np.ndarray:
         """Evaluate at N positions; returns a fresh (N, n_output) float32 array."""
         x = _as_f32_2d(input, "input", self.n_input)
