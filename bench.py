@@ -17,12 +17,13 @@ One step = Morton sort -> hash-grid encode kernel -> MLP train kernel
 library's HIP stream, inputs resident in HBM before the timed region starts.
 
 Inside the timed region the library brackets the phases of one step in
-every K/10 with HIP events on its own stream (`profile_every`); those sampled
-steps give the per-kernel durations behind the roofline fractions
-(`kernel_rooflines`, the slowest kernel is `roofline`) and
-`phase_us_per_step`. A HIP event pair costs ~3.5 us of stream time, so
-instrumenting every step would add ~23 us to a 0.13 ms step; sampling adds
-~2 us per sampled step, ~0.2 us per step on average.
+every K/5 (five sampled steps) with timing-only HIP events on its own stream
+(`profile_every`); those sampled steps give the per-kernel durations behind
+the roofline fractions (`kernel_rooflines`, the slowest kernel is
+`roofline`) and `phase_us_per_step`. The seven events of a sampled step cost
+~12 us of stream time (measured: 0.1409 ms/step with events on every step,
+0.1286 ms without), so five samples add ~60 us to the timed region: 3 us per
+step at K = 20, 0.3 us at K = 200 (`profile_overhead_us_per_step`).
 
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
 fp32, 2^16 points per call) and the CPU restatement of the reference math
@@ -55,6 +56,7 @@ B_TRAIN = 1 << 18
 B_INFER = 1 << 16
 IMG = 1024
 HBM_PEAK_GBS = 8000.0
+EVENT_COST_US = 12.3  # stream time of one sampled step's seven phase events (measured)
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 C2_CONFIG = {
@@ -127,6 +129,31 @@ def kernel_rooflines(prof: dict) -> list[dict]:
     return out
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def infer_roofline(prof: dict) -> dict | None:
+    """C1 forward kernel (field_forward_kernel, fp32 MFMA, inline encode):
+    algorithmic FLOPs 2 * (32*64 + 64*64 + 64*3) = 12,672 per point against
+    the fp32 dense MFMA peak, and algorithmic bytes per point (position 8 B,
+    4 corners x 16 levels x 2 features x 4 B of gathers, 12 B of outputs =
+    532 B) against the HBM peak, per launch of 2^16 points over the sampled
+    calls' average kernel duration."""
+    if not prof.get("infer_calls"):
+        return None
+    us = prof["gpu_infer_us"] / prof["infer_calls"]
+    flops = 2 * (32 * 64 + 64 * 64 + 64 * 3) * B_INFER
+    bytes_ = (8 + 4 * 16 * 2 * 4 + 12) * B_INFER
+    tf = flops / (us * 1e-6) / 1e12
+    gbs = bytes_ / (us * 1e-6) / 1e9
+    return {"bound": "mfma", "achieved": round(tf, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None, "kernel": "field_forward_kernel<64, 32, false, 18>",
+            "kernel_avg_us": round(us, 2), "work_per_launch": flops,
+            "gather_GBps": round(gbs, 1), "gather_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "sampled_calls": int(prof["infer_calls"])}
+
+
 OTHER_WORKLOADS = {
     # D, levels, feats, log2T, base, scale, hidden, hidden layers, outputs, loss, batch
     "c3": (3, 16, 2, 19, 16.0, 1.381913, 64, 1, 16, "L2", 1 << 20),
@@ -195,7 +222,7 @@ def run_other_workload(args, which: str) -> int:
         tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[i].data_ptr())
     tr.synchronize()
     # timed steps, phase events on one in `every` (as the C2 line)
-    every = max(1, args.steps // 10)
+    every = max(1, args.steps // 5)
     tr.set_training_step_profiling(True, every)
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -267,17 +294,29 @@ def sample_bilinear(torch, img, pos):
     return out.view(3, -1).t().contiguous()
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds: float = 12.0) -> dict:
     """The CPU restatement of the reference math (oracle/, compiled -O3,
-    OpenMP over points) running the same C2 training step on this host, on a
-    bounded sample: batches of 2^16 points (the reference's per-step cap)
-    until `seconds` have elapsed (at least 2 steps)."""
+    OpenMP over points) running the same C2 training step (B = 2^18, the GPU
+    line's batch) on this host's cores, on a bounded sample: all threads for
+    about `seconds` * 2/3 of steps, then one thread for the rest (the 1-core
+    figure); each leg runs at least one whole step."""
     sys.path.insert(0, str(REPO / "tests"))
     from oracle_binding import Oracle  # the checker's binding; CPU baseline only
 
     o = Oracle()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    threads = max(1, min(threads, os.cpu_count() or 1))
+    nproc = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
+    threads = max(1, min(threads, nproc))
     e = C2_CONFIG["encoding"]
     m = o.model(2, e["n_levels"], e["n_features_per_level"], e["log2_hashmap_size"],
                 e["base_resolution"], e["per_level_scale"], 64, 2, 3, "RelativeL2")
@@ -286,20 +325,32 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
     params = np.concatenate([hw, mw])
     m1, m2 = np.zeros_like(params), np.zeros_like(params)
     rng = np.random.default_rng(0)
-    n = 1 << 16
+    n = B_TRAIN
     pos = rng.random((n, 2), dtype=np.float32)
     tgt = rng.random((n, 3), dtype=np.float32)
-    o.training_step(m, adam, 0, params, m1, m2, pos, tgt, threads=threads)  # warm
-    steps, t0 = 0, time.perf_counter()
-    while True:
-        o.training_step(m, adam, steps + 1, params, m1, m2, pos, tgt, threads=threads)
-        steps += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and steps >= 2) or el >= 2.5 * seconds:
-            break
-    return {"value": n * steps / el, "unit": "samples/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} C2 training steps of 2^16 points (reference batch cap) "
-                      f"in {el:.1f} s on {threads} host threads (oracle/, -O3, OpenMP)"}
+    step = 0
+
+    def leg(nthreads: int, budget: float):
+        nonlocal step
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            o.training_step(m, adam, step, params, m1, m2, pos, tgt, threads=nthreads)
+            step += 1
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return steps, el
+
+    o.training_step(m, adam, step, params, m1, m2, pos, tgt, threads=threads)  # warm
+    step += 1
+    s_all, t_all = leg(threads, seconds * 2 / 3)
+    s_one, t_one = leg(1, seconds / 3)
+    return {"value": n * s_all / t_all, "unit": "samples/s", "cores": threads, "kind": "port",
+            "one_core_value": n * s_one / t_one, "cpu_model": _cpu_model(), "nproc": nproc,
+            "batch": n,
+            "sample": f"C2 training steps of 2^18 points (the GPU line's batch): {s_all} in "
+                      f"{t_all:.1f} s on {threads} threads, {s_one} in {t_one:.1f} s on 1 thread "
+                      f"(oracle/, -O3, OpenMP over points; {_cpu_model()}, nproc {nproc})"}
 
 
 def traffic_from_profiles(key: str) -> float | None:
@@ -383,7 +434,7 @@ def main() -> int:
 
     # timed region: phase events on one step in `every` (the kernel durations),
     # the rest run exactly as a caller runs them
-    every = max(1, args.steps // 10) if args.profile_every is None else args.profile_every
+    every = max(1, args.steps // 5) if args.profile_every is None else args.profile_every
     tr.set_training_step_profiling(every > 0, max(every, 1))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -414,13 +465,18 @@ def main() -> int:
     tr.synchronize()
     torch.cuda.synchronize()
     iters = max(50, args.steps)
+    # five calls of the timed loop carry an event pair around the kernel
+    tr.set_training_step_profiling(True, max(1, iters // 5))
     t2 = time.perf_counter()
     for _ in range(iters):
         tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
     tr.synchronize()
     torch.cuda.synchronize()
     infer_sps = B_INFER * iters / (time.perf_counter() - t2)
+    iprof = tr.training_step_profile()
+    tr.set_training_step_profiling(False)
     tr.close()
+    infer_roof = infer_roofline(iprof)
 
     steps_prof = max(1, prof["steps"])
     per_kernel = kernel_rooflines(prof) if prof["steps"] else []
@@ -453,9 +509,11 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "infer_samples_per_s": round(infer_sps, 1),
         "infer_config": "C1 (configs[0]): same field, fp32, 2^16 points per call",
+        "infer_roofline": infer_roof,
         "phase_us_per_step": phases,
         "profile_every": every,
         "profiled_steps": int(prof["steps"]),
+        "profile_overhead_us_per_step": round(EVENT_COST_US * prof["steps"] / args.steps, 2),
         "loss_first_last": [round(first_loss, 6), round(last_loss, 6)],
         "roofline": roofline,
         "kernel_rooflines": per_kernel,

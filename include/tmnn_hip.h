@@ -446,11 +446,14 @@ typedef struct tmnn_step_profile {
   double gpu_adam_us;         /* fused Adam pass (+ mask/grad clearing) */
   double gpu_total_us;        /* first event to last event, summed */
   double gpu_encode_us;       /* hash-grid encode forward (features of the batch) */
+  uint32_t infer_calls;       /* profiled inference calls summed below */
+  double gpu_infer_us;        /* the inference forward kernel (tmnn_inference[_device]) */
 } tmnn_step_profile;
 
 /* enabled: 0 off; k >= 1 profiles one training step in k (the first after
- * enabling, then every k-th; 1 = every step, the reference's on). Resets the
- * sums. Negative: TMNN_ERR_INVALID_ARGUMENT. */
+ * enabling, then every k-th; 1 = every step, the reference's on), and one
+ * inference call in k the same way. Resets the sums. Negative:
+ * TMNN_ERR_INVALID_ARGUMENT. */
 int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled);
 int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
 

@@ -264,12 +264,20 @@ struct tmnn_trainer {
   int prof_cur = -1;  // event set of the step being enqueued, or -1
   bool prof_suspended = false;  // allocation-free steps record no events
   tmnn_step_profile prof_acc{};
+  // inference calls while profiling is on: one event pair around the
+  // forward kernel of one call in prof_every
+  uint64_t prof_infer_seen = 0;
+  std::vector<std::array<hipEvent_t, 2>> infer_events;
+  size_t infer_used = 0;
 
   ~tmnn_trainer() {
     for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan, &grad_plan})
       if (p->image) (void)hipFree(p->image);
     for (auto &set : prof_events)
       for (hipEvent_t e : set)
+        if (e) (void)hipEventDestroy(e);
+    for (auto &pair : infer_events)
+      for (hipEvent_t e : pair)
         if (e) (void)hipEventDestroy(e);
   }
 };
@@ -333,10 +341,33 @@ int prof_mark(tmnn_trainer *tr, int k) {
   return TMNN_OK;
 }
 
-// Folds every recorded step into prof_acc and recycles the event sets.
+// Claims an event pair for a profiled inference call (nullptr when this
+// call is not sampled).
+int prof_infer_begin(tmnn_trainer *tr, std::array<hipEvent_t, 2> **pair) {
+  *pair = nullptr;
+  if (tr->prof_every <= 0 || tr->prof_suspended) return TMNN_OK;
+  if (tr->prof_infer_seen++ % static_cast<uint64_t>(tr->prof_every) != 0) return TMNN_OK;
+  if (tr->infer_used == tr->infer_events.size()) {
+    std::array<hipEvent_t, 2> ev{};
+    for (hipEvent_t &e : ev) TMNN_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+    tr->infer_events.push_back(ev);
+  }
+  *pair = &tr->infer_events[tr->infer_used];
+  return TMNN_OK;
+}
+
+// Folds every recorded step and inference call into prof_acc and recycles
+// the event sets.
 int prof_collect(tmnn_trainer *tr) {
-  if (tr->prof_used == 0) return TMNN_OK;
+  if (tr->prof_used == 0 && tr->infer_used == 0) return TMNN_OK;
   TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  for (size_t i = 0; i < tr->infer_used; ++i) {
+    float ms = 0.0f;
+    TMNN_HIP_TRY(hipEventElapsedTime(&ms, tr->infer_events[i][0], tr->infer_events[i][1]));
+    tr->prof_acc.gpu_infer_us += 1e3 * ms;
+    tr->prof_acc.infer_calls += 1;
+  }
+  tr->infer_used = 0;
   for (size_t i = 0; i < tr->prof_used; ++i) {
     const auto &e = tr->prof_events[i];
     float ms[tmnn_trainer::kProfEvents - 1];
@@ -1453,8 +1484,19 @@ int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions, float *d_o
   a.mode = kModeForward;
   a.pos = d_positions;
   a.out = d_output;
+  std::array<hipEvent_t, 2> *ev = nullptr;
+  int rc = prof_infer_begin(tr, &ev);
+  if (rc != TMNN_OK) return rc;
+  // the image repack (after weight changes) stays outside the timed pair
+  if ((rc = ensure_image(tr, tr->infer_plan)) != TMNN_OK) return rc;
+  if (ev) TMNN_HIP_TRY(hipEventRecord((*ev)[0], tr->ctx->stream));
   const int blocks = launch_field(tr, tr->infer_plan, a, n);
-  return blocks < 0 ? blocks : TMNN_OK;
+  if (blocks < 0) return blocks;
+  if (ev) {
+    TMNN_HIP_TRY(hipEventRecord((*ev)[1], tr->ctx->stream));
+    ++tr->infer_used;
+  }
+  return TMNN_OK;
 }
 
 int tmnn_inference(tmnn_trainer *tr, const float *positions, float *output, int32_t n) {
@@ -1790,6 +1832,7 @@ int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled) {
   tr->prof_acc = tmnn_step_profile{};
   tr->prof_every = enabled;
   tr->prof_seen = 0;
+  tr->prof_infer_seen = 0;
   return TMNN_OK;
 }
 

@@ -130,6 +130,8 @@ class StepProfile(ctypes.Structure):
         ("gpu_adam_us", ctypes.c_double),
         ("gpu_total_us", ctypes.c_double),
         ("gpu_encode_us", ctypes.c_double),
+        ("infer_calls", ctypes.c_uint32),
+        ("gpu_infer_us", ctypes.c_double),
     ]
 
 
