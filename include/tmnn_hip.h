@@ -245,10 +245,10 @@ int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input,
  * (16 + 4 * (spatial_dims + num_outputs) + 4 * (input_padded + L * F)) bytes
  * per point (each region rounded to 256 bytes, plus the radix histograms):
  * the C2 image-fit step (2D, 16x2 features, 3 outputs) fits 2^18 points.
- * Larger batches return TMNN_ERR_INVALID_ARGUMENT; hidden width 128 returns
- * TMNN_ERR_UNSUPPORTED. Steps are not profiled. Every call on one GPU shares
- * that GPU's scratch: calls that overlap on one GPU (trainers on different
- * streams) race. */
+ * Larger batches return TMNN_ERR_INVALID_ARGUMENT; hidden width 128 and the
+ * layer-wise (Tiled) path return TMNN_ERR_UNSUPPORTED. Steps are not
+ * profiled. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (trainers on different streams) race. */
 int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
                                       const float *d_target, int32_t n,
                                       float *d_loss_out);

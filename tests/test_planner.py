@@ -87,14 +87,37 @@ def test_no_gpu_context():
     assert p["selected_family"] is None and p["reasons"] == ["NoGPUContext"]
 
 
-def test_width_128_only_fully_fused():
+def test_width_128_fused_or_layerwise_tiled():
+    """Width 128: the instantiated fp16 shapes run fully fused; Tiled (forced,
+    or for fp32 whose operands exceed one CU's LDS) runs the layer-wise path."""
     c = cfg(network__n_neurons=128, network__n_hidden_layers=4,
             encoding__base_resolution=8.0, encoding__per_level_scale=1.4)
     assert plan_network(c, 4, 4)["selected_family"] == "FullyFused"
     p = plan_network(copy.deepcopy(c) | {"mi355x": {"precision": "fp16", "family": "Tiled"}}, 4, 4)
-    assert p["selected_family"] is None and "HiddenDimUnsupported" in p["reasons"]
+    assert p["selected_family"] == "Tiled" and "ForcedTiled" in p["reasons"]
     p = plan_network(copy.deepcopy(c) | {"mi355x": {"precision": "fp32"}}, 4, 4)
-    assert p["selected_family"] is None and "HiddenDimUnsupported" in p["reasons"]
+    assert p["selected_family"] == "Tiled" and not p["fused_train"]
+    assert "ThreadgroupMemoryExceeded" in p["reasons"]
+
+
+@pytest.mark.parametrize("n_in,neurons,layers,levels,feats,n_out,reason", [
+    (3, 256, 2, 16, 2, 1, "HiddenDimUnsupported"),
+    (3, 512, 8, 16, 2, 4, "HiddenDimUnsupported"),
+    (2, 64, 2, 32, 4, 3, "NoFusedInstance"),      # 128 input features
+    (3, 64, 2, 16, 2, 32, "UnsupportedOutputDims"),
+    (3, 128, 2, 16, 4, 2, "NoFusedInstance"),     # width 128 with 64 input features
+])
+def test_every_kernel_spec_shape_has_a_tiled_plan(n_in, neurons, layers, levels, feats, n_out,
+                                                  reason):
+    """KernelSpec bounds (kernel_spec.cpp:12-44: hidden <= 512, <= 8 layers,
+    <= 32 levels x <= 4 features, any outputs): shapes no fused kernel holds
+    fall back to Tiled (the layer-wise path) with the reason recorded."""
+    c = cfg(network__n_neurons=neurons, network__n_hidden_layers=layers, encoding__n_levels=levels,
+            encoding__n_features_per_level=feats)
+    p = plan_network(c, n_in, n_out)
+    assert p["selected_family"] == "Tiled" and not p["fused_train"]
+    assert reason in p["reasons"]
+    assert "Tiled" in p["candidate_families"] and "SafeDebug" in p["candidate_families"]
 
 
 def test_fingerprint_tracks_the_shape():

@@ -26,6 +26,7 @@
 #include "encode_kernel.hpp"
 #include "field_kernel.hpp"
 #include "grad_kernel.hpp"
+#include "layer_kernels.hpp"
 #include "mlp_kernel.hpp"
 #include "scatter_kernel.hpp"
 #include "sort.hpp"
@@ -210,7 +211,8 @@ struct KernelPlan {
   bool xmem = false;       // features from encode_features_kernel (X tiles in xfeat)
   bool mlp = false;        // mlp_train_kernel
   bool wide_train = false; // wide_train_kernel
-  int max_blocks = 0;   // resident blocks on the whole device
+  bool layerwise = false;  // layer-wise path (layer_kernels.hpp): one product per layer
+  int max_blocks = 0;   // resident blocks on the whole device (layer-wise: batch chunks)
 };
 
 }  // namespace
@@ -245,6 +247,7 @@ struct tmnn_trainer {
   DevBuf dx;  // [batch][IN] input-feature gradients between the two train kernels
   DevBuf xfeat;  // input features of the batch as X tiles (encode_kernel.hpp)
   DevBuf wide_mask, wide_act;  // hidden-128 kernel: per-tile ReLU bits and fp16 activations
+  DevBuf lw_act, lw_y, lw_g, lw_d;  // layer-wise path: activations, outputs, d_out, deltas
   DevBuf dbg_a, dbg_b, dbg_c;
 
   KernelPlan train_plan, fwd_plan, infer_plan;
@@ -397,9 +400,12 @@ ModelShape shape_of(const tmnn_model_desc &d) {
   m.F = d.features_per_level;
   m.L = d.num_levels;
   m.IN = d.num_levels * d.features_per_level;
-  m.INP = m.IN <= 32 ? 32 : 64;
+  m.INP = m.IN <= 32 ? 32 : (m.IN <= 64 ? 64 : 128);
   m.H = d.hidden_dim;
-  m.HP = d.hidden_dim <= 32 ? 32 : (d.hidden_dim <= 64 ? 64 : kWideHP);
+  m.HP = d.hidden_dim <= 32 ? 32
+                            : (d.hidden_dim <= 64 ? 64
+                                                  : (d.hidden_dim <= kWideHP ? kWideHP
+                                                                             : round_up(d.hidden_dim, 16)));
   m.NHL = d.num_hidden_layers;
   m.M = d.num_outputs;
   m.mlp_count = make_layout(m.INP, m.HP, m.IN, m.H, m.NHL, m.M, 0, false, false, 1).mlp_count();
@@ -410,8 +416,45 @@ ModelShape shape_of(const tmnn_model_desc &d) {
 // family's kernel for the shape, waves per block, LDS bytes against
 // lds_limit. Returns false with *why when the family has no kernel or its
 // LDS plan does not fit.
+// Batch chunks (partial dW rows) of the layer-wise path: at most 64, and at
+// most 64 MiB of partial rows.
+int lw_max_chunks(int mlp_count) {
+  const int by_mem = static_cast<int>((64u << 20) / (4u * static_cast<unsigned>(std::max(1, mlp_count))));
+  return std::max(1, std::min(64, by_mem));
+}
+
+bool size_plan_fused(const ModelShape &m, bool f16, bool train, int family, int lds_limit,
+                     KernelPlan &out, int *why);
+
+// The family's plan; TILED and SAFE_DEBUG fall back to the layer-wise path
+// (layer_kernels.hpp) for shapes no MFMA kernel is instantiated for or whose
+// LDS plan does not fit, so every KernelSpec shape has a non-fused plan.
 bool size_plan(const ModelShape &m, bool f16, bool train, int family, int lds_limit,
                KernelPlan &out, int *why) {
+  if (size_plan_fused(m, f16, train, family, lds_limit, out, why)) return true;
+  if (family == TMNN_FAMILY_FULLY_FUSED) return false;
+  out = KernelPlan{};
+  out.f16 = f16;
+  out.train = train;
+  out.layerwise = true;
+  out.xmem = true;
+  out.wpb = 4;
+  out.max_blocks = lw_max_chunks(m.mlp_count);
+  *why = 0;
+  return true;
+}
+
+bool size_plan_fused(const ModelShape &m, bool f16, bool train, int family, int lds_limit,
+                     KernelPlan &out, int *why) {
+  *why = 0;
+  if (m.M > 16) {  // the MFMA kernels hold the outputs in one 16-wide tile
+    *why = TMNN_PLAN_UNSUPPORTED_OUTPUT_DIMS;
+    return false;
+  }
+  if (m.INP > 64 || m.HP > kWideHP) {
+    *why = m.HP > kWideHP ? TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED : TMNN_PLAN_NO_FUSED_INSTANCE;
+    return false;
+  }
   const KernelChoice kc = select_kernel(m.HP, m.INP, f16, train, m.D, m.F, m.NHL, family);
   out.fn = kc.fn;
   out.reg_dw = kc.reg_dw;
@@ -506,17 +549,16 @@ void plan_network_impl(const tmnn_device_caps &caps, const tmnn_model_desc &d,
     reason(TMNN_PLAN_NO_GPU_CONTEXT);
     return;
   }
-  if (d.spatial_dims < 2 || d.spatial_dims > 4 || d.num_levels * d.features_per_level > 64) {
+  if (d.spatial_dims < 2 || d.spatial_dims > 4 || d.num_levels < 1 || d.num_levels > 32 ||
+      d.num_levels * d.features_per_level > 128) {
     reason(TMNN_PLAN_UNSUPPORTED_INPUT_DIMS);
     return;
   }
-  if (d.num_outputs < 1 || d.num_outputs > 16) {
+  if (d.num_outputs < 1) {
     reason(TMNN_PLAN_UNSUPPORTED_OUTPUT_DIMS);
     return;
   }
-  if (d.hidden_dim < 1 || d.hidden_dim > kWideHP ||
-      (d.hidden_dim > 64 && (d.num_levels * d.features_per_level > 32 ||
-                             d.precision != TMNN_PRECISION_FP16))) {
+  if (d.hidden_dim < 1 || d.hidden_dim > 512) {
     reason(TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED);
     return;
   }
@@ -530,11 +572,16 @@ void plan_network_impl(const tmnn_device_caps &caps, const tmnn_model_desc &d,
     const bool ff16 = f == TMNN_FAMILY_SAFE_DEBUG ? false : f16;
     int why = 0, why_eval = 0;
     fam[f].train = size_plan(m, ff16, true, f, caps.lds_bytes_per_cu, fam[f].tp, &why);
+    if (f == TMNN_FAMILY_FULLY_FUSED && fam[f].train && m.HP == kWideHP && !ff16) {
+      // width-128 fp32 training: the layer's fp32 weight and gradient
+      // operands do not fit one CU's LDS next to the activations (the fused
+      // width-128 kernels train in fp16 only)
+      fam[f].train = false;
+      why = TMNN_PLAN_THREADGROUP_MEMORY_EXCEEDED;
+    }
     KernelPlan ep;
     fam[f].eval = size_plan(m, false, false, f, caps.lds_bytes_per_cu, ep, &why_eval);
     if (f == TMNN_FAMILY_FULLY_FUSED && !fam[f].train && why) reason(why);
-    if (f == TMNN_FAMILY_TILED && !fam[f].train && why == TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED)
-      reason(why);
     if (fam[f].train && fam[f].eval) p.candidate_families |= 1u << f;
   }
   int sel = -1;
@@ -573,6 +620,7 @@ int plan_kernel(tmnn_trainer *tr, bool f16, bool train, KernelPlan &out) {
     return fail(TMNN_ERR_UNSUPPORTED,
                 why == TMNN_PLAN_THREADGROUP_MEMORY_EXCEEDED ? "model does not fit in LDS"
                                                              : "no kernel for this geometry");
+  if (out.layerwise) return TMNN_OK;  // no packed image, plain launches
   TMNN_HIP_TRY(hipMalloc(&out.image, out.image_bytes));
   TMNN_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(out.fn),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, out.lds));
@@ -607,7 +655,7 @@ FieldArgs base_args(const tmnn_trainer *tr) {
 
 // Rebuild a plan's packed LDS image if the weights changed since it was made.
 int ensure_image(tmnn_trainer *tr, KernelPlan &plan) {
-  if (plan.packed_version == tr->weights_version) return TMNN_OK;
+  if (plan.layerwise || plan.packed_version == tr->weights_version) return TMNN_OK;
   PackArgs p{};
   p.s = make_layout(tr->INP, tr->HP, tr->IN, tr->d.hidden_dim, tr->d.num_hidden_layers,
                     tr->d.num_outputs, static_cast<int>(tr->mlp_count), plan.f16, plan.train, 1);
@@ -719,9 +767,14 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *per
 // Launches a plan's field kernel over n points; XMEM plans first encode a.pos
 // into tr->xfeat (unless reuse_x: the features of these points are there
 // already), with profile mark prof_after_encode (if >= 0) in between.
+int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
+                     int prof_after_encode, bool reuse_x, const uint32_t *perm, float *pos_out);
+
 int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
                  int prof_after_encode = -1, bool reuse_x = false,
                  const uint32_t *perm = nullptr, float *pos_out = nullptr) {
+  if (plan.layerwise)
+    return launch_layerwise(tr, plan, a, n, prof_after_encode, reuse_x, perm, pos_out);
   int rc = ensure_image(tr, plan);
   if (rc != TMNN_OK) return rc;
   if (plan.xmem) {
@@ -744,6 +797,161 @@ int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
                      tr->ctx->stream, a);
   TMNN_HIP_TRY(hipGetLastError());
   return blocks;
+}
+
+// The layer-wise path (layer_kernels.hpp) over n points: encode (unless
+// reuse_x: the features and, in kModeInputGrad, the forward activations of
+// these points are in place), one product per layer forward, and for the
+// training modes the output gradient, the weight-gradient partial rows (one
+// per batch chunk; returns their count) and the input-feature gradients into
+// a.dx_out. fp32 throughout (the loss scale of the fp16 kernels is not needed).
+int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
+                     int prof_after_encode, bool reuse_x, const uint32_t *perm, float *pos_out) {
+  int rc;
+  const bool fwd_only = a.mode == kModeForward;
+  if (!reuse_x && (rc = launch_encode(tr, a.pos, n, perm, pos_out)) != TMNN_OK) return rc;
+  if (prof_after_encode >= 0 && (rc = prof_mark(tr, prof_after_encode)) != TMNN_OK) return rc;
+  const int IN = tr->IN, H = tr->d.hidden_dim, NHL = tr->d.num_hidden_layers;
+  const int M = tr->d.num_outputs;
+  const size_t N = static_cast<size_t>(n);
+  TMNN_HIP_TRY(tr->lw_act.ensure(N * H * NHL * sizeof(float)));
+  TMNN_HIP_TRY(tr->lw_y.ensure(N * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->lw_g.ensure(N * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->lw_d.ensure(2 * N * std::max(H, 1) * sizeof(float)));
+  const FieldLayout lay = make_layout(tr->INP, tr->HP, IN, H, NHL, M, 0, false, false, 1);
+  hipStream_t st = tr->ctx->stream;
+  float *act = tr->lw_act.as<float>();
+  auto act_k = [&](int k) { return act + static_cast<size_t>(k) * N * H; };
+  auto gemm = [&](LwGemmArgs g, int chunks) -> int {
+    if (g.R <= 0 || g.C <= 0) return TMNN_OK;
+    const dim3 grid((g.R + kLwTile - 1) / kLwTile, (g.C + kLwTile - 1) / kLwTile, chunks);
+    hipLaunchKernelGGL(lw_gemm_kernel, grid, dim3(256), 0, st, g);
+    TMNN_HIP_TRY(hipGetLastError());
+    return TMNN_OK;
+  };
+  LwGemmArgs base{};
+  base.KT0 = tr->INP / 16;
+  base.scale = 1.0f;
+  // ---- forward (kept when the caller re-runs the backward for another output)
+  if (!(reuse_x && a.mode == kModeInputGrad)) {
+    for (int k = 0; k <= NHL; ++k) {
+      LwGemmArgs g = base;
+      g.R = n;
+      g.K = k == 0 ? IN : H;
+      g.C = k == NHL ? M : H;
+      g.k_chunk = g.K;
+      g.a_mode = k == 0 ? kLwAXTiles : kLwARow;
+      g.A = k == 0 ? tr->xfeat.as<float>() : act_k(k - 1);
+      g.lda = H;
+      g.B = a.mlp + lay.w_off(k);
+      g.ldb = g.C;
+      g.bias = a.mlp + lay.b_off(k);
+      if (k < NHL) {
+        g.epi = kLwEpiHidden;
+        g.out = act_k(k);
+        g.ldo = H;
+      } else {
+        g.epi = kLwEpiOutput;
+        g.out = fwd_only ? a.out : nullptr;
+        g.out_index = a.out_index;
+        g.ldo = M;
+        g.out2 = tr->lw_y.as<float>();
+        g.ldo2 = M;
+      }
+      if ((rc = gemm(g, 1)) != TMNN_OK) return rc;
+    }
+  }
+  if (fwd_only) return 1;
+  // ---- output gradient (and the loss), per batch chunk
+  const int P = std::max(1, std::min(plan.max_blocks, (n + 255) / 256));
+  const int chunk = (n + P - 1) / P;
+  LwLossArgs la{};
+  la.n = n;
+  la.M = M;
+  la.mode = a.mode;
+  la.loss_kind = a.loss_kind;
+  la.grad_output = a.grad_output;
+  la.chunk = chunk;
+  la.huber_delta = a.huber_delta;
+  la.inv_n = a.inv_n;
+  la.loss_scale = 1.0f;
+  la.y = tr->lw_y.as<float>();
+  la.target = a.target;
+  la.tgt_index = a.tgt_index;
+  la.out = a.mode == kModeInputGrad ? a.out : nullptr;
+  la.g = tr->lw_g.as<float>();
+  la.loss_partials = a.loss_partials;
+  hipLaunchKernelGGL(lw_loss_kernel, dim3(P), dim3(256), 0, st, la);
+  TMNN_HIP_TRY(hipGetLastError());
+  // ---- backward: weight-gradient partial rows (training), deltas, dx
+  const bool wgrads = a.mode != kModeInputGrad;
+  const int64_t row = a.mlp_count;
+  float *dbuf[2] = {tr->lw_d.as<float>(), tr->lw_d.as<float>() + N * H};
+  auto partial_dw = [&](const float *A, int a_mode, int lda, int R, const float *D, int C,
+                        int w_off, int b_off) -> int {
+    LwGemmArgs g = base;
+    g.R = R;
+    g.C = C;
+    g.K = n;
+    g.k_chunk = chunk;
+    g.a_mode = a_mode;
+    g.A = A;
+    g.lda = lda;
+    g.B = D;
+    g.ldb = C;
+    g.epi = kLwEpiPartial;
+    g.dst = a.grad_partials;
+    g.dst_stride = row;
+    g.dst_off = w_off;
+    int r = gemm(g, P);
+    if (r != TMNN_OK) return r;
+    hipLaunchKernelGGL(lw_colsum_kernel, dim3((C + 255) / 256, P), dim3(256), 0, st, D, C, n, C,
+                       chunk, a.grad_partials, row, b_off);
+    TMNN_HIP_TRY(hipGetLastError());
+    return TMNN_OK;
+  };
+  const float *dcur = tr->lw_g.as<float>();  // gradient at the current layer's output
+  int dcols = M;
+  for (int k = NHL; k >= 0; --k) {
+    // layer k maps its input (X for k = 0, else h_{k-1}) to dcur
+    if (wgrads) {
+      if (k > 0)
+        rc = partial_dw(act_k(k - 1), kLwACol, H, H, dcur, dcols, lay.w_off(k), lay.b_off(k));
+      else
+        rc = partial_dw(tr->xfeat.as<float>(), kLwAXTilesT, 0, IN, dcur, dcols, lay.w_off(0),
+                        lay.b_off(0));
+      if (rc != TMNN_OK) return rc;
+    }
+    LwGemmArgs g = base;
+    g.R = n;
+    g.K = dcols;
+    g.k_chunk = dcols;
+    g.a_mode = kLwARow;
+    g.A = dcur;
+    g.lda = dcols;
+    g.B = a.mlp + lay.w_off(k);  // W_k [in][dcols], read transposed
+    g.b_trans = 1;
+    g.ldb = dcols;
+    if (k > 0) {
+      float *dnext = dbuf[k & 1];
+      g.C = H;
+      g.epi = kLwEpiMask;  // times [h_{k-1} > 0]
+      g.mask = act_k(k - 1);
+      g.ldm = H;
+      g.out = dnext;
+      g.ldo = H;
+      if ((rc = gemm(g, 1)) != TMNN_OK) return rc;
+      dcur = dnext;
+      dcols = H;
+    } else {
+      g.C = IN;
+      g.epi = kLwEpiScale;
+      g.out = a.dx_out;
+      g.ldo = IN;
+      if ((rc = gemm(g, 1)) != TMNN_OK) return rc;
+    }
+  }
+  return P;
 }
 
 // Power-of-two loss scale for the fp16 backward: d_out carries 1/N, which
@@ -774,7 +982,7 @@ int ensure_batch(tmnn_trainer *tr, int n) {
                              tr->IN * sizeof(float)));
   TMNN_HIP_TRY(tr->xfeat.ensure(static_cast<size_t>((n + kTilePts - 1) / kTilePts) * kTilePts *
                                 tr->INP * sizeof(float)));
-  if (tr->HP == kWideHP && tr->d.num_hidden_layers > 1) {
+  if (tr->train_plan.wide && tr->d.num_hidden_layers > 1) {
     const size_t tiles = static_cast<size_t>((n + kTilePts - 1) / kTilePts);
     const size_t layers = static_cast<size_t>(tr->d.num_hidden_layers - 1);
     TMNN_HIP_TRY(tr->wide_mask.ensure(layers * tiles * 64 * sizeof(uint64_t)));
@@ -1247,19 +1455,7 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
     return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_model_desc.struct_size mismatch");
   std::string why;
   if (!desc_ok(desc, why)) return fail(TMNN_ERR_INVALID_ARGUMENT, "KernelSpec: " + why);
-  if (desc->hidden_dim > 128)
-    return fail(TMNN_ERR_UNSUPPORTED, "hidden_dim > 128 is not built in this library");
-  if (desc->hidden_dim > 64 && desc->num_levels * desc->features_per_level > 32)
-    return fail(TMNN_ERR_UNSUPPORTED,
-                "hidden_dim > 64 needs num_levels * features_per_level <= 32 in this library");
-  if (desc->hidden_dim > 64 && desc->precision != TMNN_PRECISION_FP16)
-    return fail(TMNN_ERR_UNSUPPORTED,
-                "hidden_dim > 64 trains with precision fp16 only in this library");
-  if (desc->num_outputs > 16)
-    return fail(TMNN_ERR_UNSUPPORTED, "num_outputs > 16 is not built in this library");
   const int IN = desc->num_levels * desc->features_per_level;
-  if (IN > 64)
-    return fail(TMNN_ERR_UNSUPPORTED, "num_levels * features_per_level > 64 is not built");
   TMNN_HIP_TRY(hipSetDevice(ctx->device));
 
   // the planner decides the family the kernels come from
@@ -1283,8 +1479,11 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
     tr->d.morton_sort = 0;
   }
   tr->IN = IN;
-  tr->INP = IN <= 32 ? 32 : 64;
-  tr->HP = desc->hidden_dim <= 32 ? 32 : (desc->hidden_dim <= 64 ? 64 : kWideHP);
+  {
+    const ModelShape ms = shape_of(*desc);
+    tr->INP = ms.INP;
+    tr->HP = ms.HP;
+  }
   tr->lr_enc = desc->lr_encoding;
   tr->lr_net = desc->lr_network;
   tr->hash_count = static_cast<uint32_t>(desc->num_levels) *
@@ -1420,10 +1619,11 @@ int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
   if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
   if (!d_input || !d_target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
   if (!tr->ctx->scratch) return fail(TMNN_ERR_RUNTIME, "device scratch address unknown");
-  if (tr->train_plan.wide)
+  if (tr->train_plan.wide || tr->train_plan.layerwise)
     return fail(TMNN_ERR_UNSUPPORTED,
-                "the allocation-free step does not run hidden width 128 (its activation "
-                "buffers exceed the scratch): use tmnn_training_step_device");
+                "the allocation-free step runs neither hidden width 128 nor the layer-wise "
+                "path (their activation buffers exceed the scratch): use "
+                "tmnn_training_step_device");
   TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
   const int bn = std::min(n, tr->d.batch_size);
   // carve the scratch: [keys0 | keys1 | vals0 | vals1 | sort tmp | s_pos | s_tgt | xfeat | dx]
@@ -1933,8 +2133,9 @@ int tmnn_batch_plan(tmnn_trainer *tr, tmnn_batch_plan_t *out) {
   out->reduction_bytes_per_lane = static_cast<uint64_t>(tr->train_plan.max_blocks) * sizeof(float);
   const int tile = tr->train_plan.wide ? kWideWaves * kTilePts : kTilePts;
   out->threadgroup_size = static_cast<uint32_t>(64 * tr->train_plan.wpb);
-  out->points_per_threadgroup =
-      static_cast<uint32_t>(tr->train_plan.wide ? tile : kTilePts * tr->train_plan.wpb);
+  out->points_per_threadgroup = static_cast<uint32_t>(
+      tr->train_plan.layerwise ? kLwTile
+                               : (tr->train_plan.wide ? tile : kTilePts * tr->train_plan.wpb));
   return TMNN_OK;
 }
 
