@@ -457,6 +457,11 @@ def main() -> int:
     print(f"# timed {args.steps} steps in {elapsed * 1e3:.1f} ms; loss {first_loss:.5f} -> "
           f"{last_loss:.5f}; profile {prof}", file=sys.stderr, flush=True)
 
+    # reference rates at this shape over a batch in the step's Morton order:
+    # gather-only (the encode's loads), atomic-only and flag-store-only (the
+    # scatter's memory operations) -- the achievable denominators
+    rates = tr.debug_hash_rates(xs[0].data_ptr(), B_TRAIN, sorted=True, reps=20)
+
     # inference on the C1 shape (same field, fp32, 2^16 points per call)
     xi = torch.rand(B_INFER, 2, device=dev, generator=gen)
     yi = torch.empty(B_INFER, 3, device=dev)
@@ -480,6 +485,16 @@ def main() -> int:
 
     steps_prof = max(1, prof["steps"])
     per_kernel = kernel_rooflines(prof) if prof["steps"] else []
+    for r in per_kernel:
+        if r["kernel"].startswith("encode"):
+            r["achievable"] = {"reference": "gather-only kernel (the encode's corner loads)",
+                               "us": round(rates["gather_us"], 2),
+                               "frac_of_achievable": round(rates["gather_us"] / r["kernel_avg_us"], 4)}
+        elif r["kernel"].startswith("hash_scatter"):
+            r["achievable"] = {"reference": "flag-store-only and atomic-only kernels (the "
+                                            "scatter's memory operations, every corner)",
+                               "flag_us": round(rates["flag_us"], 2),
+                               "atomic_us": round(rates["atomic_us"], 2)}
     roofline = max(per_kernel, key=lambda r: r["kernel_avg_us"]) if per_kernel else None
     phases = {k: round(prof[k] / steps_prof, 2) for k in
               ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",

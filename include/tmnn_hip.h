@@ -478,6 +478,18 @@ int tmnn_debug_encode_tiles(tmnn_trainer *tr, const float *positions, int32_t n,
                             int32_t sorted, float *features, uint32_t *perm_out,
                             float *sorted_pos_out, uint64_t *padding_nonzero);
 
+/* Reference rates of the hash-grid memory operations at this trainer's
+ * shape, over n device-resident points (d_positions [n][spatial_dims]; with
+ * `sorted`, in the training step's Morton order): the average GPU time of one
+ * launch (over `reps`) of a kernel that only (gather) loads every corner's F
+ * floats of every level, (atomic) adds a constant with the scatter's atomic
+ * per corner and level into a scratch table, (flag) stores the visit byte per
+ * corner and level. Trainer state is not touched. The achievable-bandwidth
+ * denominators of the encode and scatter; no counterpart in the reference. */
+int tmnn_debug_hash_rates(tmnn_trainer *tr, const float *d_positions, int32_t n,
+                          int32_t sorted, int32_t reps, double *gather_us,
+                          double *atomic_us, double *flag_us);
+
 /* Accumulated gradients in reference layout: int32 fixed-point hash grads
  * [L][T][F] (scale 65536) and fp32 MLP grads. Either pointer may be null. */
 int tmnn_debug_get_gradients(tmnn_trainer *tr, int32_t *grad_hash,

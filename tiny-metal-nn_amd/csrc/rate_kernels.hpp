@@ -1,0 +1,92 @@
+// rate_kernels.hpp -- reference-rate kernels at a trainer's own hash-grid
+// shape (debug entry tmnn_debug_hash_rates): the throughput of the memory
+// operations the encode and scatter kernels are built from, with everything
+// else removed, over the same points in the same order. They give the
+// "achievable" denominators the encode and scatter are measured against.
+//   kRateGather -- every corner of every level, F floats each (the encode's
+//                  loads and addresses, no interpolation; one float per point
+//                  is written so the loads stay live);
+//   kRateAtomic -- one F-wide integer atomic add per corner and level
+//                  (64-bit for F = 2, as the scatter packs it) of a constant
+//                  nonzero value into a scratch table;
+//   kRateFlag   -- one byte store per corner and level (the visit flags).
+#pragma once
+
+#include "device_common.hpp"
+
+namespace tmnn_hip {
+
+enum : int32_t { kRateGather = 0, kRateAtomic = 1, kRateFlag = 2 };
+
+struct HashRateArgs {
+  int32_t n, L;
+  uint32_t log2T;
+  float res[kMaxLevels];
+  const float *pos;    // [n][D]
+  const float *table;  // [L][T][F]
+  float *out;          // [n] (gather)
+  int32_t *acc;        // [L][T][F] scratch (atomic)
+  uint8_t *flags;      // [L][T] scratch (flag)
+};
+
+template <int D, int F, int KIND>
+__global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
+  constexpr int C = 1 << D;
+  constexpr int G = C >= 16 ? 2 : (C >= 8 ? 4 : 8);  // levels whose loads are in flight together
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.n) return;
+  float p[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(i) * D + k];
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  float sum = 0.0f;
+  for (int l0 = 0; l0 < a.L; l0 += G) {
+    float v[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int l = l0 + g < a.L ? l0 + g : a.L - 1;
+      const Cell<D> c = cell_of<D>(p, a.res[l]);
+      const size_t lbase = static_cast<size_t>(l) << a.log2T;
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        int co[D];
+        float wc[D];
+        corner_of<D>(c, k, co, wc);
+        const size_t e = lbase + hash_corner<D>(co, tmask);
+        if constexpr (KIND == kRateGather) {
+          float t = 0.0f;
+          if constexpr (F == 1) {
+            t = a.table[e];
+          } else if constexpr (F == 2) {
+            const f32x2 q = *reinterpret_cast<const f32x2 *>(a.table + e * 2);
+            t = q[0] + q[1];
+          } else {
+            const f32x4 q = *reinterpret_cast<const f32x4 *>(a.table + e * 4);
+            t = (q[0] + q[1]) + (q[2] + q[3]);
+          }
+          v[g][k] = t;
+        } else if constexpr (KIND == kRateAtomic) {
+          if (l0 + g < a.L) {
+            if constexpr (F == 2) {
+              atomicAdd(reinterpret_cast<unsigned long long *>(a.acc + e * 2), 0x100000001ull);
+            } else {
+#pragma unroll
+              for (int f = 0; f < F; ++f) atomicAdd(a.acc + e * F + f, 1);
+            }
+          }
+        } else {
+          if (l0 + g < a.L) a.flags[e] = 1;
+        }
+      }
+    }
+    if constexpr (KIND == kRateGather) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < C; ++k) sum += l0 + g < a.L ? v[g][k] : 0.0f;
+    }
+  }
+  if constexpr (KIND == kRateGather) a.out[i] = sum;
+}
+
+}  // namespace tmnn_hip

@@ -27,6 +27,7 @@
 #include "field_kernel.hpp"
 #include "grad_kernel.hpp"
 #include "layer_kernels.hpp"
+#include "rate_kernels.hpp"
 #include "mlp_kernel.hpp"
 #include "scatter_kernel.hpp"
 #include "sort.hpp"
@@ -248,6 +249,18 @@ struct tmnn_trainer {
   DevBuf xfeat;  // input features of the batch as X tiles (encode_kernel.hpp)
   DevBuf wide_mask, wide_act;  // hidden-128 kernel: per-tile ReLU bits and fp16 activations
   DevBuf lw_act, lw_y, lw_g, lw_d;  // layer-wise path: activations, outputs, d_out, deltas
+  // The fused device step sorts its batch on a second stream into one of two
+  // buffer sets, so that a step's sort runs while the previous step's kernels
+  // still execute; the main stream waits for the sort (ev_sorted) and marks
+  // the set free again after the step (ev_consumed).
+  struct SortSet {
+    DevBuf keys0, keys1, vals0, vals1, tmp;
+  } step_sort[2];
+  hipStream_t side = nullptr;
+  hipEvent_t ev_sorted[2] = {nullptr, nullptr};
+  hipEvent_t ev_consumed[2] = {nullptr, nullptr};
+  bool consumed_recorded[2] = {false, false};
+  int sort_parity = 0;
   DevBuf dbg_a, dbg_b, dbg_c;
 
   KernelPlan train_plan, fwd_plan, infer_plan;
@@ -274,6 +287,12 @@ struct tmnn_trainer {
   size_t infer_used = 0;
 
   ~tmnn_trainer() {
+    if (side) {
+      (void)hipStreamSynchronize(side);
+      (void)hipStreamDestroy(side);
+    }
+    for (hipEvent_t e : {ev_sorted[0], ev_sorted[1], ev_consumed[0], ev_consumed[1]})
+      if (e) (void)hipEventDestroy(e);
     for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan, &grad_plan})
       if (p->image) (void)hipFree(p->image);
     for (auto &set : prof_events)
@@ -977,6 +996,14 @@ int ensure_batch(tmnn_trainer *tr, int n) {
   size_t tmp = 0;
   TMNN_HIP_TRY(morton_sort_temp_bytes(n, &tmp));
   TMNN_HIP_TRY(tr->sort_tmp.ensure(std::max<size_t>(tmp, 256)));
+  if (tr->d.morton_sort)
+    for (auto &ss : tr->step_sort) {
+      TMNN_HIP_TRY(ss.keys0.ensure(n * sizeof(uint32_t)));
+      TMNN_HIP_TRY(ss.keys1.ensure(n * sizeof(uint32_t)));
+      TMNN_HIP_TRY(ss.vals0.ensure(n * sizeof(uint32_t)));
+      TMNN_HIP_TRY(ss.vals1.ensure(n * sizeof(uint32_t)));
+      TMNN_HIP_TRY(ss.tmp.ensure(std::max<size_t>(tmp, 256)));
+    }
   // dx rows for the whole last tile: the MLP train kernel stores unconditionally
   TMNN_HIP_TRY(tr->dx.ensure(static_cast<size_t>((n + kTilePts - 1) / kTilePts) * kTilePts *
                              tr->IN * sizeof(float)));
@@ -1070,12 +1097,56 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
   return TMNN_OK;
 }
 
+// The fused step's Morton sort on the side stream into buffer set
+// tr->sort_parity (see tmnn_trainer::step_sort): the side stream first waits
+// until the step that last used the set has finished (and, when the batch
+// was staged on the main stream, for that copy); the main stream then waits
+// for the sort. The caller marks the set consumed after the step
+// (sort_set_consumed). Returns the permutation in *perm_out.
+int sort_batch_overlapped(tmnn_trainer *tr, const float *d_pos, int n, bool staged_on_main,
+                          const uint32_t **perm_out) {
+  hipStream_t st = tr->ctx->stream;
+  if (!tr->side) {
+    TMNN_HIP_TRY(hipStreamCreateWithFlags(&tr->side, hipStreamNonBlocking));
+    for (int k = 0; k < 2; ++k) {
+      TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_sorted[k], hipEventDisableTiming));
+      TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_consumed[k], hipEventDisableTiming));
+    }
+  }
+  const int k = tr->sort_parity;
+  auto &ss = tr->step_sort[k];
+  if (tr->consumed_recorded[k]) TMNN_HIP_TRY(hipStreamWaitEvent(tr->side, tr->ev_consumed[k], 0));
+  if (staged_on_main) {
+    // the batch was copied in on the main stream: the sort reads it after that
+    TMNN_HIP_TRY(hipEventRecord(tr->ev_sorted[k], st));
+    TMNN_HIP_TRY(hipStreamWaitEvent(tr->side, tr->ev_sorted[k], 0));
+  }
+  const uint32_t *sorted_keys = nullptr;
+  TMNN_HIP_TRY(morton_sort_batch(ss.tmp.ptr, ss.tmp.bytes, d_pos, tr->d.spatial_dims,
+                                 ss.keys0.as<uint32_t>(), ss.keys1.as<uint32_t>(),
+                                 ss.vals0.as<uint32_t>(), ss.vals1.as<uint32_t>(), n, tr->side,
+                                 &sorted_keys, perm_out));
+  TMNN_HIP_TRY(hipEventRecord(tr->ev_sorted[k], tr->side));
+  TMNN_HIP_TRY(hipStreamWaitEvent(st, tr->ev_sorted[k], 0));
+  return TMNN_OK;
+}
+
+// After the last reader of the current sort set on the main stream: the set
+// may be sorted into again (two steps later); the next step takes the other.
+int sort_set_consumed(tmnn_trainer *tr) {
+  const int k = tr->sort_parity;
+  TMNN_HIP_TRY(hipEventRecord(tr->ev_consumed[k], tr->ctx->stream));
+  tr->consumed_recorded[k] = true;
+  tr->sort_parity = k ^ 1;
+  return TMNN_OK;
+}
+
 // Fused forward/backward over n device-resident points, gradients
 // accumulated into grad_hash / grad_mlp / mask. Returns the block count used
 // (for the loss reduction) or a negative status.
 int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tgt,
                          int n, bool external_grad, float *d_loss = nullptr,
-                         bool reduce = true) {
+                         bool reduce = true, int overlap_sort = 0) {
   const bool f16 = tr->d.precision == TMNN_PRECISION_FP16;
   const float *pos = d_pos, *tgt = d_tgt;
   const uint32_t *perm = nullptr;
@@ -1083,8 +1154,13 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   if (rc != TMNN_OK) return rc;
   // the packed weight image (rebuilt after every Adam step) counts with the sort
   if ((rc = ensure_image(tr, tr->train_plan)) != TMNN_OK) return rc;
-  rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm,
-                  !tr->train_plan.xmem);
+  if (overlap_sort && tr->d.morton_sort && n > 1 && tr->train_plan.xmem) {
+    // feature-tile plans read the batch through the permutation (no gather)
+    rc = sort_batch_overlapped(tr, d_pos, n, overlap_sort > 1, &perm);
+  } else {
+    rc = sort_batch(tr, d_pos, d_tgt, tr->d.num_outputs, n, &pos, &tgt, &perm,
+                    !tr->train_plan.xmem);
+  }
   if (rc != TMNN_OK) return rc;
   if ((rc = prof_mark(tr, 1)) != TMNN_OK) return rc;
   FieldArgs a = base_args(tr);
@@ -1219,22 +1295,29 @@ void prof_abort(tmnn_trainer *tr) {
   tr->prof_cur = -1;
 }
 
+// overlap_sort: 0 sorts on the main stream (the step's buffers may be
+// borrowed scratch); 1 sorts on the side stream (the caller's batch is
+// ready); 2 as 1, the batch being staged on the main stream.
 int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, int n,
-                      float *d_loss) {
+                      float *d_loss, int overlap_sort = 1) {
   int rc = prof_begin_step(tr);
   if (rc != TMNN_OK) return rc;
   float *loss = d_loss ? d_loss : tr->loss_out.as<float>();
-  const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false, loss, false);
+  const bool overlapped = overlap_sort && tr->d.morton_sort && n > 1 && tr->train_plan.xmem;
+  const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false, loss, false, overlap_sort);
   if (blocks < 0) {
     prof_abort(tr);
+    if (overlapped) (void)sort_set_consumed(tr);
     return blocks;
   }
   // dW reduction, loss and Adam in one kernel (the reduce phase reads ~0)
   if ((rc = prof_mark(tr, 5)) != TMNN_OK || (rc = run_finish(tr, blocks, n, loss)) != TMNN_OK ||
       (rc = prof_mark(tr, 6)) != TMNN_OK) {
     prof_abort(tr);
+    if (overlapped) (void)sort_set_consumed(tr);
     return rc;
   }
+  if (overlapped && (rc = sort_set_consumed(tr)) != TMNN_OK) return rc;
   if (tr->prof_cur >= 0) tr->prof_acc.batch_size = static_cast<uint32_t>(n);
   tr->prof_cur = -1;
   ++tr->step;
@@ -1588,7 +1671,7 @@ int tmnn_training_step(tmnn_trainer *tr, const float *input, const float *target
                               static_cast<size_t>(bn) * tr->d.num_outputs * sizeof(float),
                               hipMemcpyHostToDevice, st));
   rc = train_step_device(tr, tr->in_pos.as<float>(), tr->in_tgt.as<float>(), bn,
-                         tr->loss_out.as<float>());
+                         tr->loss_out.as<float>(), 2);
   if (rc != TMNN_OK) return rc;
   float loss = 0.0f;
   TMNN_HIP_TRY(hipMemcpyAsync(&loss, tr->loss_out.ptr, sizeof(float), hipMemcpyDeviceToHost, st));
@@ -1662,7 +1745,7 @@ int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
     bufs[r]->borrowed = true;
   }
   tr->prof_suspended = true;
-  const int rc = train_step_device(tr, d_input, d_target, bn, d_loss_out);
+  const int rc = train_step_device(tr, d_input, d_target, bn, d_loss_out, 0);
   tr->prof_suspended = false;
   for (int r = 0; r < kRegions; ++r) {
     bufs[r]->ptr = saved[r].ptr;
@@ -2252,6 +2335,72 @@ int tmnn_debug_encode_tiles(tmnn_trainer *tr, const float *positions, int32_t n,
         ++pad;
     }
   if (padding_nonzero) *padding_nonzero = pad;
+  return TMNN_OK;
+}
+
+int tmnn_debug_hash_rates(tmnn_trainer *tr, const float *d_positions, int32_t n, int32_t sorted,
+                          int32_t reps, double *gather_us, double *atomic_us, double *flag_us) {
+  if (!tr || !d_positions) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (n <= 0 || reps < 1) return fail(TMNN_ERR_INVALID_ARGUMENT, "N and reps must be >= 1");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  hipStream_t st = tr->ctx->stream;
+  int rc = ensure_batch(tr, n);
+  if (rc != TMNN_OK) return rc;
+  const float *pos = d_positions, *unused = nullptr;
+  const uint32_t *perm = nullptr;
+  if (sorted && (rc = sort_batch(tr, d_positions, nullptr, 0, n, &pos, &unused, &perm)) != TMNN_OK)
+    return rc;
+  TMNN_HIP_TRY(tr->dbg_a.ensure(static_cast<size_t>(tr->hash_count) * sizeof(int32_t)));
+  TMNN_HIP_TRY(tr->dbg_b.ensure(tr->hash_entries));
+  TMNN_HIP_TRY(tr->dbg_c.ensure(static_cast<size_t>(n) * sizeof(float)));
+  if ((rc = zero_device(tr, tr->dbg_a.ptr, static_cast<size_t>(tr->hash_count) * 4)) != TMNN_OK ||
+      (rc = zero_device(tr, tr->dbg_b.ptr, tr->hash_entries)) != TMNN_OK)
+    return rc;
+  HashRateArgs ra{};
+  ra.n = n;
+  ra.L = tr->d.num_levels;
+  ra.log2T = static_cast<uint32_t>(tr->d.log2_hashmap_size);
+  for (int l = 0; l < kMaxLevels; ++l) ra.res[l] = tr->res[l];
+  ra.pos = pos;
+  ra.table = tr->params.as<float>();
+  ra.out = tr->dbg_c.as<float>();
+  ra.acc = tr->dbg_a.as<int32_t>();
+  ra.flags = tr->dbg_b.as<uint8_t>();
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  TMNN_HIP_TRY(hipEventCreate(&e0));
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return fail(TMNN_ERR_GPU, "hipEventCreate failed");
+  }
+  double *dst[3] = {gather_us, atomic_us, flag_us};
+  const dim3 grid((n + 255) / 256);
+  hipError_t err = hipSuccess;
+  for (int kind = 0; kind < 3 && err == hipSuccess; ++kind) {
+    err = hipEventRecord(e0, st);
+    for (int r = 0; r < reps && err == hipSuccess; ++r) {
+#define TMNN_RATE(DD, FF)                                                                        \
+  if (tr->d.spatial_dims == DD && tr->d.features_per_level == FF) {                              \
+    if (kind == kRateGather)                                                                     \
+      hipLaunchKernelGGL((hash_rate_kernel<DD, FF, kRateGather>), grid, dim3(256), 0, st, ra);   \
+    else if (kind == kRateAtomic)                                                                \
+      hipLaunchKernelGGL((hash_rate_kernel<DD, FF, kRateAtomic>), grid, dim3(256), 0, st, ra);   \
+    else                                                                                         \
+      hipLaunchKernelGGL((hash_rate_kernel<DD, FF, kRateFlag>), grid, dim3(256), 0, st, ra);     \
+  }
+      TMNN_RATE(2, 1) TMNN_RATE(2, 2) TMNN_RATE(2, 4) TMNN_RATE(3, 1) TMNN_RATE(3, 2)
+      TMNN_RATE(3, 4) TMNN_RATE(4, 1) TMNN_RATE(4, 2) TMNN_RATE(4, 4)
+#undef TMNN_RATE
+      err = hipGetLastError();
+    }
+    if (err == hipSuccess) err = hipEventRecord(e1, st);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+    if (err == hipSuccess && dst[kind]) *dst[kind] = 1e3 * static_cast<double>(ms) / reps;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (err != hipSuccess) return fail(TMNN_ERR_GPU, std::string("hash rates: ") + hipGetErrorString(err));
   return TMNN_OK;
 }
 

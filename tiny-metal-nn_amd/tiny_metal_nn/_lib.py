@@ -234,6 +234,10 @@ SIGNATURES = {
     "tmnn_debug_encode": (ctypes.c_int, [_V, _V, _I32, _V, _V, _V]),
     "tmnn_debug_encode_tiles": (ctypes.c_int, [_V, _V, _I32, _I32, _V, _V, _V,
                                                ctypes.POINTER(ctypes.c_uint64)]),
+    "tmnn_debug_hash_rates": (ctypes.c_int, [_V, _V, _I32, _I32, _I32,
+                                             ctypes.POINTER(ctypes.c_double),
+                                             ctypes.POINTER(ctypes.c_double),
+                                             ctypes.POINTER(ctypes.c_double)]),
     "tmnn_debug_get_gradients": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
     "tmnn_debug_get_active_mask": (ctypes.c_int, [_V, _V, _SZ]),
     "tmnn_debug_morton_sort": (ctypes.c_int, [_V, _V, _I32, _V, _V]),

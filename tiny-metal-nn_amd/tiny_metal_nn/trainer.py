@@ -413,6 +413,18 @@ class Trainer:
                                                          ctypes.byref(pad)))
         return feats, perm, spos, pad.value
 
+    def debug_hash_rates(self, positions_ptr: int, n: int, sorted: bool = True,
+                         reps: int = 20) -> dict:
+        """GPU microseconds per launch of the gather / atomic / flag-store
+        reference kernels over n device-resident positions at this trainer's
+        hash-grid shape (tmnn_debug_hash_rates)."""
+        g, a, f = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        with self._enter("debug_hash_rates"):
+            _lib.check(self._lib.tmnn_debug_hash_rates(
+                self._h, ctypes.c_void_p(positions_ptr), int(n), 1 if sorted else 0, int(reps),
+                ctypes.byref(g), ctypes.byref(a), ctypes.byref(f)))
+        return {"gather_us": g.value, "atomic_us": a.value, "flag_us": f.value}
+
     def debug_gradients(self) -> tuple[np.ndarray, np.ndarray]:
         self._check_open()
         gh = np.empty(self.hash_param_count, np.int32)
