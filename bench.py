@@ -492,7 +492,8 @@ def main() -> int:
                                "frac_of_achievable": round(rates["gather_us"] / r["kernel_avg_us"], 4)}
         elif r["kernel"].startswith("hash_scatter"):
             r["achievable"] = {"reference": "flag-store-only and atomic-only kernels (the "
-                                            "scatter's memory operations, every corner)",
+                                            "scatter's memory operations: one per run of "
+                                            "lanes on the same entry, every corner and level)",
                                "flag_us": round(rates["flag_us"], 2),
                                "atomic_us": round(rates["atomic_us"], 2)}
     roofline = max(per_kernel, key=lambda r: r["kernel_avg_us"]) if per_kernel else None

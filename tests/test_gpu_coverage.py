@@ -471,3 +471,27 @@ def _hip_to_host(host: np.ndarray, src: int, nbytes: int) -> None:
     assert host.nbytes == nbytes
     rc = hip.hipMemcpy(host.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(src), nbytes, 2)
     assert rc == 0, rc
+
+
+def test_hash_rate_reference_kernels_leave_the_trainer_alone():
+    """tmnn_debug_hash_rates (the gather / atomic / flag reference kernels)
+    returns positive per-launch times and touches no trainer state."""
+    torch = pytest.importorskip("torch")
+    _say("hash rates")
+    d, enc, net, m_out = GEOMS["2d_f2"]
+    with make_trainer(d, m_out, enc, net, precision="fp16", batch=1 << 16) as tr:
+        x = torch.rand(1 << 16, d, device="cuda:0")
+        y = torch.rand(1 << 16, m_out, device="cuda:0")
+        torch.cuda.synchronize()
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), 1 << 16)
+        tr.synchronize()
+        hw, mw = tr.get_weights()
+        gh, gm = tr.debug_gradients()
+        mask = tr.debug_active_mask()
+        r = tr.debug_hash_rates(x.data_ptr(), 1 << 16, sorted=True, reps=3)
+        assert all(v > 0.0 for v in r.values()), r
+        hw2, mw2 = tr.get_weights()
+        gh2, gm2 = tr.debug_gradients()
+        assert np.array_equal(hw, hw2) and np.array_equal(mw, mw2)
+        assert np.array_equal(gh, gh2) and np.array_equal(gm, gm2)
+        assert np.array_equal(mask, tr.debug_active_mask())

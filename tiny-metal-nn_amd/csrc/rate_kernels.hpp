@@ -6,10 +6,12 @@
 //   kRateGather -- every corner of every level, F floats each (the encode's
 //                  loads and addresses, no interpolation; one float per point
 //                  is written so the loads stay live);
-//   kRateAtomic -- one F-wide integer atomic add per corner and level
-//                  (64-bit for F = 2, as the scatter packs it) of a constant
-//                  nonzero value into a scratch table;
-//   kRateFlag   -- one byte store per corner and level (the visit flags).
+//   kRateAtomic -- one F-wide integer atomic add (64-bit for F = 2, as the
+//                  scatter packs it) of a constant nonzero value into a
+//                  scratch table per run of lanes on the same entry (corner
+//                  and level; the scatter merges such runs);
+//   kRateFlag   -- one byte store per run of lanes on the same entry (the
+//                  visit flags, as the scatter stores them).
 #pragma once
 
 #include "device_common.hpp"
@@ -34,10 +36,11 @@ __global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
   constexpr int C = 1 << D;
   constexpr int G = C >= 16 ? 2 : (C >= 8 ? 4 : 8);  // levels whose loads are in flight together
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.n) return;
+  const bool valid = i < a.n;  // lanes past the batch take part in the run test
+  const int lane = threadIdx.x & 63;
   float p[D];
 #pragma unroll
-  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(i) * D + k];
+  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(valid ? i : 0) * D + k];
   const uint32_t tmask = (1u << a.log2T) - 1u;
   float sum = 0.0f;
   for (int l0 = 0; l0 < a.L; l0 += G) {
@@ -52,7 +55,12 @@ __global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
         int co[D];
         float wc[D];
         corner_of<D>(c, k, co, wc);
-        const size_t e = lbase + hash_corner<D>(co, tmask);
+        const uint32_t local = valid ? hash_corner<D>(co, tmask) : 0xFFFFFFFFu;
+        const size_t e = lbase + (valid ? local : 0u);
+        // first lane of a run of equal entries (previous lane by DPP wave_shr:1)
+        const uint32_t prev = static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(-1, static_cast<int>(local), 0x138, 0xf, 0xf, false));
+        const bool head = valid && (lane == 0 || prev != local);
         if constexpr (KIND == kRateGather) {
           float t = 0.0f;
           if constexpr (F == 1) {
@@ -66,7 +74,7 @@ __global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
           }
           v[g][k] = t;
         } else if constexpr (KIND == kRateAtomic) {
-          if (l0 + g < a.L) {
+          if (head && l0 + g < a.L) {
             if constexpr (F == 2) {
               atomicAdd(reinterpret_cast<unsigned long long *>(a.acc + e * 2), 0x100000001ull);
             } else {
@@ -75,7 +83,7 @@ __global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
             }
           }
         } else {
-          if (l0 + g < a.L) a.flags[e] = 1;
+          if (head && l0 + g < a.L) a.flags[e] = 1;
         }
       }
     }
@@ -86,7 +94,8 @@ __global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
         for (int k = 0; k < C; ++k) sum += l0 + g < a.L ? v[g][k] : 0.0f;
     }
   }
-  if constexpr (KIND == kRateGather) a.out[i] = sum;
+  if constexpr (KIND == kRateGather)
+    if (valid) a.out[i] = sum;
 }
 
 }  // namespace tmnn_hip
