@@ -12,6 +12,10 @@
 // visited too, which Adam reads off the z = 0 partner's flag (the z = 1 entry
 // of a corner is its z = 0 entry XOR (805459861 mod T) within the level).
 //
+// A wave whose contributions at a level all truncate to 0 (every lane's
+// |d| < 2^-16; with d_out ~ 1/N this is 90-99% of a converging batch's
+// levels) only stores that level's visit flags (mark_level).
+//
 // Lanes of a wave hold consecutive Morton-sorted points of one level. When
 // more than kMergeMinLanes lanes of a corner have a nonzero contribution, runs
 // of lanes that hit the same entry are summed across lanes first (int32 sums
@@ -113,6 +117,38 @@ __device__ __forceinline__ bool grads_fit(const float *d) {
   return ok;
 }
 
+// |d| < 2^-16 for every feature: every corner's contribution truncates to 0.
+// The corner weight w is a product of per-axis factors in [0, 1], so each
+// rounded product fl(d * w...) is no larger in magnitude than d, and
+// fl(d * w) * 65536 (exact: a power of two) stays below 1. NaN is not small.
+template <int F>
+__device__ __forceinline__ bool grads_vanish(const float *d) {
+  bool ok = true;
+#pragma unroll
+  for (int f = 0; f < F; ++f) ok = ok && __builtin_fabsf(d[f]) < 1.0f / kGradScale;
+  return ok;
+}
+
+// A level whose contributions all truncate to 0 in every lane of the wave
+// (the common case once training converges: |d| ~ 1/N): only the visit flags
+// of its corners are stored, one per valid lane and corner, the same entries
+// the full path marks.
+template <int D>
+__device__ __forceinline__ void mark_level(const ScatterArgs &a, int l, const float *p,
+                                           bool valid) {
+  if (!valid) return;
+  const Cell<D> c = cell_of<D>(p, a.res[l]);
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+#pragma unroll
+  for (int k = 0; k < (1 << D); ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    mark_entry(a.mask, lbase + hash_corner<D>(co, tmask));
+  }
+}
+
 // One thread per point (or per point and share of its levels, blockIdx.y),
 // its levels in turn: the thread reads its dx row with
 // 16-byte loads (coalesced across the wave) and the lanes of a wave still
@@ -173,6 +209,19 @@ __device__ __forceinline__ void scatter_level(const ScatterArgs &a, int l, const
   }
 }
 
+// One level of one point: flags only when the whole wave's contributions
+// vanish, else the full scatter (plain or saturating conversion).
+template <int D, int F>
+__device__ __forceinline__ void scatter_point_level(const ScatterArgs &a, int l, const float *p,
+                                                    const float *d, bool valid, int lane) {
+  if (__all(!valid || grads_vanish<F>(d)))
+    mark_level<D>(a, l, p, valid);
+  else if (__all(grads_fit<F>(d)))
+    scatter_level<D, F, true>(a, l, p, d, valid, lane);
+  else
+    scatter_level<D, F, false>(a, l, p, d, valid, lane);
+}
+
 template <int D, int F>
 __global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterArgs a) {
   const int i = blockIdx.x * kScatterThreads + threadIdx.x;
@@ -207,10 +256,7 @@ __global__ void __launch_bounds__(kScatterThreads) hash_scatter_kernel(ScatterAr
       float d[F];
 #pragma unroll
       for (int f = 0; f < F; ++f) d[f] = v[lv * F + f];
-      if (__all(grads_fit<F>(d)))
-        scatter_level<D, F, true>(a, l, p, d, valid, lane);
-      else
-        scatter_level<D, F, false>(a, l, p, d, valid, lane);
+      scatter_point_level<D, F>(a, l, p, d, valid, lane);
     }
   }
 }
@@ -242,10 +288,7 @@ __global__ void __launch_bounds__(kScatterThreads) hash_scatter_level_kernel(Sca
   } else {
     d[0] = src[0];
   }
-  if (__all(grads_fit<F>(d)))
-    scatter_level<D, F, true>(a, l, p, d, valid, lane);
-  else
-    scatter_level<D, F, false>(a, l, p, d, valid, lane);
+  scatter_point_level<D, F>(a, l, p, d, valid, lane);
 }
 
 }  // namespace tmnn_hip
