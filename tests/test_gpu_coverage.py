@@ -328,19 +328,25 @@ def test_c4_backward_fp16_matches_oracle(oracle):
 
 @pytest.mark.parametrize("name", ["c2", "c3", "c4"])
 @pytest.mark.parametrize("mix", ["tiny", "mixed"])
-def test_scatter_vanishing_levels_match_oracle(oracle, name, mix):
+@pytest.mark.parametrize("precision", ["fp32", "fp16"])
+def test_scatter_vanishing_levels_match_oracle(oracle, name, mix, precision):
     """The hash-grid backward at the gradient sizes of a converging batch
     (|d_out| ~ 1/N): a wave whose contributions at a level all truncate to 0
     only marks that level's corners. "tiny": every point's gradient vanishes,
     so the int32 table stays all zero while the visited set is the oracle's;
-    "mixed": 2% of the points carry large gradients, so waves of both kinds
-    run in one launch (point-major at C2/C3, level-major at C4's T = 2^21)."""
-    _say(f"scatter vanishing levels {name} {mix}")
+    "mixed": 2% of the points carry large gradients, so lanes of both kinds
+    run in one launch. fp32 runs hash_scatter_kernel (point-major at C2/C3,
+    level-major at C4's T = 2^21); fp16 at C2/C3 runs the backward fused into
+    the MLP kernel's tiles (tile_scatter.hpp), at C4 the level-major kernel."""
+    _say(f"scatter vanishing levels {name} {mix} {precision}")
     d, enc, net, m_out, _ = BASELINE[name]
     rng = np.random.default_rng(41)
-    with make_trainer(d, m_out, enc, net, precision="fp32", hash_range=0.5, batch=1 << 16) as tr:
+    with make_trainer(d, m_out, enc, net, precision=precision, hash_range=0.5,
+                      batch=1 << 16) as tr:
         hw, mw = tr.get_weights()
         pos = rng.random((8192, d), dtype=np.float32)
+        if precision == "fp16":
+            pos = away_from_relu_kinks(oracle, tr, hw, mw, pos)
         g = rng.normal(0, 1.0, (len(pos), m_out)).astype(np.float32)
         scale = np.full((len(pos), 1), 1e-9, np.float32)
         if mix == "mixed":
@@ -352,13 +358,22 @@ def test_scatter_vanishing_levels_match_oracle(oracle, name, mix):
         mask = tr.debug_active_mask()
         ogh, ogm, omask, _, _ = oracle.forward_backward(omodel(oracle, tr), hw, mw, pos, d_out=g)
         assert np.array_equal(mask, omask)
-        assert rel_tensor(gm, ogm) <= 1e-5
+        # fp16 "tiny": d_out ~ 1e-9 times the loss scale (~N) is below fp16's
+        # normal range, so the fp16 MLP gradients are not compared there; the
+        # table and the visited set are what this case checks
+        if precision == "fp32":
+            assert rel_tensor(gm, ogm) <= 1e-5
+        elif mix == "mixed":
+            assert rel_tensor(gm, ogm) <= 2e-3
         if mix == "tiny":
             assert not ogh.any() and not gh.any()
-        else:
+        elif precision == "fp32":
             assert ogh.any()
             diff = np.abs(gh.astype(np.int64) - ogh.astype(np.int64))
             assert (diff == 0).mean() > 0.99 and diff.max() <= 16, int(diff.max())
+        else:
+            assert ogh.any()
+            assert rel_tensor(gh, ogh) <= 2e-3
 
 
 def _sdf_batch(rng, n, centers, radii):

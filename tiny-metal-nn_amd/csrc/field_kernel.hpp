@@ -76,6 +76,10 @@ struct FieldArgs {
   _Float16 *wide_act;       // wide kernel: hidden activations [NHL-1][n_tiles][128][32] (fp16 training)
   float *grad_partials;     // [gridDim.x][mlp_count]
   float *loss_partials;     // [gridDim.x]
+  // training kernels with the hash-grid backward fused (tile_scatter.hpp):
+  const float *spos;        // [n][D] positions in tile order
+  int32_t *grad_hash;       // [L][T][F] int32 fixed point
+  uint8_t *mask;            // [L][T] visit flags
 };
 
 // LDS plan of one launch, evaluated identically on host and device. All

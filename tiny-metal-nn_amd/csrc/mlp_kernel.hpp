@@ -36,9 +36,16 @@
 // delta tiles), each layer's bias is the accumulator's initial value (added
 // before the products, not after), and RelativeL2 takes its reciprocal from
 // v_rcp_f32.
+//
+// Instances with SD > 0 also run the hash-grid backward of each tile
+// (tile_scatter.hpp, a D = SD, F = SF grid) where the input-feature
+// gradients come off the matrix cores, instead of storing them for
+// hash_scatter_kernel; the tile's point positions are prefetched with its X
+// tiles.
 #pragma once
 
 #include "field_kernel.hpp"
+#include "tile_scatter.hpp"
 
 namespace tmnn_hip {
 
@@ -231,7 +238,7 @@ __device__ __forceinline__ void owner_schedule() {
   }
 }
 
-template <int HP, int INP, int NHL, int W = mlp_waves(INP, NHL)>
+template <int HP, int INP, int NHL, int W = mlp_waves(INP, NHL), int SD = 0, int SF = 0>
 __global__ void __launch_bounds__(W * 64)
     __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) mlp_train_kernel(FieldArgs a) {
   constexpr int HT = HP / 16;    // unit tiles of a hidden layer
@@ -306,6 +313,8 @@ __global__ void __launch_bounds__(W * 64)
   f32x4 Xn[KT0][kNT];
   uint32_t rown[kNT];
   float Tn[kNT][4];
+  constexpr int PD = SD > 0 ? SD : 1;
+  float Pn[kNT][PD];  // fused scatter: the next tile's point positions
   auto point_valid = [&](int tile, int nt) {
     return tile < a.n_tiles && tile * kTilePts + 16 * nt + p < a.n;
   };
@@ -317,6 +326,15 @@ __global__ void __launch_bounds__(W * 64)
         Xn[kt][nt] = tile < a.n_tiles
                          ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
                          : f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (SD > 0) {
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        const bool ok = point_valid(tile, nt);
+        const size_t pi = ok ? static_cast<size_t>(tile * kTilePts + 16 * nt + p) : 0u;
+#pragma unroll
+        for (int k = 0; k < SD; ++k) Pn[nt][k] = ok ? a.spos[pi * SD + k] : 0.0f;
+      }
+    }
   };
   auto fetch_rows = [&](int tile) {
 #pragma unroll
@@ -360,6 +378,11 @@ __global__ void __launch_bounds__(W * 64)
     for (int kt = 0; kt < KT0; ++kt)
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) X[kt][nt] = Xn[kt][nt];
+    float P[kNT][PD];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int k = 0; k < PD; ++k) P[nt][k] = Pn[nt][k];
     float Tv[kNT][4];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt)
@@ -483,7 +506,10 @@ __global__ void __launch_bounds__(W * 64)
       } else {
         f32x4 dx[KT0][kNT];
         mma_packed<HS, KT0>(smem + s.bwd_off(0), b, dx, lane);
-        if (have) {
+        if constexpr (SD > 0) {
+          tile_scatter<SD, SF, KT0>(a, dx, P, valid,
+                                    reinterpret_cast<const float *>(smem + s.res_off), q);
+        } else if (have) {
           // rows past the batch exist (the buffer is padded to whole tiles)
 #pragma unroll
           for (int nt = 0; nt < kNT; ++nt) {

@@ -1,0 +1,101 @@
+// tile_scatter.hpp -- the hash-grid backward of one 32-point MLP tile, run by
+// the MLP training kernel itself (mlp_kernel.hpp) right after the tile's
+// input-feature gradients dx come off the matrix cores, instead of storing
+// dx for hash_scatter_kernel.
+//
+// Same arithmetic as hash_scatter_kernel (scatter_kernel.hpp; reference
+// emitHashScatter, mlp_kernel_emitter.cpp:672-901, mask :48-71): per corner
+// and feature int32(trunc(d * w * 65536)) with w = ((wx * wy) * wz) (F = 2),
+// packed 64-bit atomics for the feature pair, every visited corner's flag
+// stored; a group of lanes whose contributions all truncate to 0 (the common
+// case once training converges) only stores the flags. Lanes that hit the
+// same entry each issue their own atomic (no run merging: a converging
+// batch's contributions are almost all zero).
+//
+// Why here: the separate scatter re-read 8 B of dx per feature and spent its
+// time on the per-lane memory requests of the flag stores; in the MLP kernel
+// the memory pipeline is nearly idle, so the index arithmetic and the stores
+// run beside the matrix work, and the dx round trip through HBM disappears.
+//
+// Lane layout (D layout of dx[kt][nt]): lane p + 16 q holds features
+// 16 kt + 4 q + r of point 16 nt + p; for F = 2 items r = 2h, 2h + 1 are the
+// two features of level 8 kt + 2 q + h. One wave instruction therefore
+// covers 16 points at each of four levels.
+#pragma once
+
+#include "field_kernel.hpp"
+#include "scatter_kernel.hpp"
+
+namespace tmnn_hip {
+
+// Compile-time shapes with a fused scatter: (D, F) of the hash grid. F = 2
+// only (the feature pair of a level lies in one lane).
+__host__ __device__ constexpr bool tile_scatter_shape(int D, int F) {
+  return F == 2 && (D == 2 || D == 3);
+}
+
+// dx: the tile's input-feature gradients (fp32, still carrying the loss
+// scale); pos: the lane's point positions per column tile (sorted order);
+// res: the per-level resolution table (the LDS image's copy).
+template <int D, int F, int KT0>
+__device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&dx)[KT0][kNT],
+                                             const float (&pos)[kNT][D], const bool (&valid)[kNT],
+                                             const float *res, int q) {
+  static_assert(tile_scatter_shape(D, F), "fused scatter shape");
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+#pragma unroll
+  for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int l = 8 * kt + 2 * q + h;
+      const bool lv = l < a.L;
+      const float rl = res[lv ? l : 0];
+      const size_t lbase = static_cast<size_t>(lv ? l : 0) << a.log2T;
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        const bool on = valid[nt] && lv;
+        float d[2];
+        d[0] = dx[kt][nt][2 * h] * a.inv_loss_scale;
+        d[1] = dx[kt][nt][2 * h + 1] * a.inv_loss_scale;
+        const Cell<D> c = cell_of<D>(pos[nt], rl);
+        if (__all(!on || grads_vanish<2>(d))) {
+          if (on) {
+#pragma unroll
+            for (int k = 0; k < (1 << D); ++k) {
+              int co[D];
+              float wc[D];
+              corner_of<D>(c, k, co, wc);
+              mark_entry(a.mask, lbase + hash_corner<D>(co, tmask));
+            }
+          }
+        } else {
+          const bool fits = __all(!on || grads_fit<2>(d));
+#pragma unroll
+          for (int k = 0; k < (1 << D); ++k) {
+            int co[D];
+            float wc[D];
+            corner_of<D>(c, k, co, wc);
+            const size_t entry = lbase + hash_corner<D>(co, tmask);
+            const float w = corner_weight<D>(wc);
+            int32_t ci[2];
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+              const float v = d[f] * w;
+              ci[f] = fits ? static_cast<int32_t>(v * kGradScale) : f2i_trunc(v * kGradScale);
+            }
+            if (on) {
+              const int64_t v64 = static_cast<int64_t>(
+                  (static_cast<uint64_t>(static_cast<uint32_t>(ci[1])) << 32) +
+                  static_cast<uint64_t>(static_cast<int64_t>(ci[0])));
+              if (v64 != 0)
+                atomicAdd(reinterpret_cast<unsigned long long *>(a.grad_hash + entry * 2),
+                          static_cast<unsigned long long>(v64));
+              mark_entry(a.mask, entry);
+            }
+          }
+        }
+      }
+    }
+}
+
+}  // namespace tmnn_hip

@@ -88,6 +88,7 @@ struct KernelChoice {
   bool xmem = false;    // input features from encode_features_kernel
   bool mlp = false;     // mlp_train_kernel (no activation staging in LDS)
   bool wide_train = false;  // wide_train_kernel (fp16 training at width 128)
+  bool tile_scatter = false;  // the training kernel runs the hash-grid backward per tile
 };
 
 // Hidden width 128: instantiated for the BASELINE 4D shape (16 levels x 2
@@ -114,7 +115,7 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
 // specialised on the BASELINE geometries (compile-time D, F) or on the
 // runtime geometry; the hidden-128 forward reads X tiles.
 KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL,
-                           int family) {
+                           int family, bool small_table = false) {
   const bool fused = family == TMNN_FAMILY_FULLY_FUSED;
   if (HP == kWideHP)
     return INP == 32 && fused ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
@@ -130,6 +131,18 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
 #undef TMNN_FWD_SPEC
   // fp16 training of the 64-wide BASELINE shapes: transposes on the matrix
   // cores instead of LDS staging (mlp_kernel.hpp)
+  // Tables whose level slices stay cache-sized (the scatter's point-major
+  // rule): the 64-wide fp16 kernels run the hash-grid backward of each tile
+  // themselves (tile_scatter.hpp)
+  if (fused && train && f16 && HP == 64 && INP == 32 && small_table &&
+      tile_scatter_shape(D, F)) {
+    if (NHL == 2)
+      return {D == 2 ? mlp_train_kernel<64, 32, 2, 8, 2, 2> : mlp_train_kernel<64, 32, 2, 8, 3, 2>,
+              true, false, true, true, false, true};
+    if (NHL == 1)
+      return {D == 2 ? mlp_train_kernel<64, 32, 1, 8, 2, 2> : mlp_train_kernel<64, 32, 1, 8, 3, 2>,
+              true, false, true, true, false, true};
+  }
   if (fused && train && f16 && HP == 64 && INP == 32 && NHL == 2)
     return {mlp_train_kernel<64, 32, 2>, true, false, true, true};
   if (fused && train && f16 && HP == 64 && INP == 32 && NHL == 1)
@@ -212,6 +225,7 @@ struct KernelPlan {
   bool xmem = false;       // features from encode_features_kernel (X tiles in xfeat)
   bool mlp = false;        // mlp_train_kernel
   bool wide_train = false; // wide_train_kernel
+  bool tile_scatter = false;  // hash-grid backward fused into the training kernel
   bool layerwise = false;  // layer-wise path (layer_kernels.hpp): one product per layer
   int max_blocks = 0;   // resident blocks on the whole device (layer-wise: batch chunks)
 };
@@ -410,7 +424,7 @@ int prof_collect(tmnn_trainer *tr) {
 
 // Padded widths and parameter count of a model (the kernels' view of it).
 struct ModelShape {
-  int D, F, L, IN, INP, H, HP, NHL, M, mlp_count;
+  int D, F, L, IN, INP, H, HP, NHL, M, mlp_count, log2T;
 };
 
 ModelShape shape_of(const tmnn_model_desc &d) {
@@ -418,6 +432,7 @@ ModelShape shape_of(const tmnn_model_desc &d) {
   m.D = d.spatial_dims;
   m.F = d.features_per_level;
   m.L = d.num_levels;
+  m.log2T = d.log2_hashmap_size;
   m.IN = d.num_levels * d.features_per_level;
   m.INP = m.IN <= 32 ? 32 : (m.IN <= 64 ? 64 : 128);
   m.H = d.hidden_dim;
@@ -474,13 +489,17 @@ bool size_plan_fused(const ModelShape &m, bool f16, bool train, int family, int 
     *why = m.HP > kWideHP ? TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED : TMNN_PLAN_NO_FUSED_INSTANCE;
     return false;
   }
-  const KernelChoice kc = select_kernel(m.HP, m.INP, f16, train, m.D, m.F, m.NHL, family);
+  // level slices up to 8 MB: the scatter runs point-major (level_major())
+  const bool small_table = (static_cast<size_t>(m.F) * 4u << m.log2T) <= (8u << 20);
+  const KernelChoice kc =
+      select_kernel(m.HP, m.INP, f16, train, m.D, m.F, m.NHL, family, small_table);
   out.fn = kc.fn;
   out.reg_dw = kc.reg_dw;
   out.wide = kc.wide;
   out.xmem = kc.xmem;
   out.mlp = kc.mlp;
   out.wide_train = kc.wide_train;
+  out.tile_scatter = kc.tile_scatter;
   out.f16 = f16;
   out.train = train;
   *why = 0;
@@ -1178,10 +1197,17 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   a.grad_partials = tr->partials.as<float>();
   a.loss_partials = tr->loss_partials.as<float>();
   a.dx_out = tr->dx.as<float>();
+  const bool fused_scatter = tr->train_plan.tile_scatter;
+  if (fused_scatter) {  // the training kernel runs the hash-grid backward per tile
+    a.spos = indexed ? sorted_pos : pos;
+    a.grad_hash = tr->grad_hash.as<int32_t>();
+    a.mask = tr->mask[tr->mask_cur].as<uint8_t>();
+  }
   const int blocks = launch_field(tr, tr->train_plan, a, n, 2, false, a.tgt_index, sorted_pos);
   if (blocks < 0) return blocks;
   if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
-  if ((rc = launch_scatter(tr, indexed ? sorted_pos : pos, n)) != TMNN_OK) return rc;
+  if (!fused_scatter && (rc = launch_scatter(tr, indexed ? sorted_pos : pos, n)) != TMNN_OK)
+    return rc;
   if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
   if (!reduce) return blocks;  // finish_step_kernel reduces the rows and the loss
   // dW rows, plus (training steps) the loss in one extra block
