@@ -59,14 +59,24 @@ __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&d
         d[1] = dx[kt][nt][2 * h + 1] * a.inv_loss_scale;
         const Cell<D> c = cell_of<D>(pos[nt], rl);
         if (__all(!on || grads_vanish<2>(d))) {
-          if (on) {
+          // flags only. Corners x and x + 1 of a cell differ only in the low
+          // bits the carry of x + 1 flips, so their flag bytes share a
+          // 128-byte line unless x ends in seven 1 bits: one
+          // v_permlane32_swap gives each store instruction both x-corners of
+          // 32 (point, level) pairs (lanes 0-31 corner x, lanes 32-63 corner
+          // x + 1 of the same pairs), half the line requests of one
+          // instruction per corner
 #pragma unroll
-            for (int k = 0; k < (1 << D); ++k) {
-              int co[D];
-              float wc[D];
-              corner_of<D>(c, k, co, wc);
-              mark_entry(a.mask, lbase + hash_corner<D>(co, tmask));
-            }
+          for (int m = 0; m < (1 << (D - 1)); ++m) {
+            int co[D];
+            float wc[D];
+            corner_of<D>(c, 2 * m, co, wc);
+            const uint32_t e0 = on ? static_cast<uint32_t>(lbase + hash_corner<D>(co, tmask)) : ~0u;
+            co[0] += 1;
+            const uint32_t e1 = on ? static_cast<uint32_t>(lbase + hash_corner<D>(co, tmask)) : ~0u;
+            const auto r = __builtin_amdgcn_permlane32_swap(e0, e1, false, false);
+            if (r[0] != ~0u) mark_entry(a.mask, r[0]);
+            if (r[1] != ~0u) mark_entry(a.mask, r[1]);
           }
         } else {
           const bool fits = __all(!on || grads_fit<2>(d));
