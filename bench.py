@@ -11,10 +11,12 @@ Workload ("C2"): the image-fit training step.
     bilinearly at 2^18 uniform random coordinates per step;
   * full backward through the MLP and the hash table (int32 fixed-point
     scatter), then the fused Adam pass (lr 1e-2, b1 0.9, b2 0.99, eps 1e-15).
-One step = Morton sort -> hash-grid encode kernel -> MLP train kernel
-(forward, loss, backward, dW) -> hash-grid scatter kernel -> finish kernel
-(dW / loss reductions, Adam, weight image for the next step), all on the
-library's HIP stream, inputs resident in HBM before the timed region starts.
+One step = Morton sort (a second stream, overlapping the previous step) ->
+hash-grid encode kernel -> MLP train kernel (forward, loss, backward, dW, and
+the hash-grid backward of each tile: int32 atomics and visit flags) ->
+finish kernel (dW / loss reductions, Adam, weight image for the next step),
+on the library's HIP streams, inputs resident in HBM before the timed region
+starts.
 
 Inside the timed region the library brackets the phases of one step in
 every K/5 (five sampled steps) with timing-only HIP events on its own stream
@@ -97,6 +99,10 @@ def kernel_models(d: int = 2, levels: int = 16, feats: int = 2, n_out: int = 3,
         "mlp": {"bound": "mfma", "per_point": 3 * flops},
         "scatter": {"bound": "hbm", "per_point": 4 * d + levels * feats * 4 + corners * levels * feats * 4},
         "adam": {"bound": "hbm", "per_step": 28 * (hash_params + mlp_params) + hash_params // feats},
+        # the hash-grid backward run inside the MLP kernel's tiles: position
+        # read and the int32 update of every corner and level (dx stays in
+        # registers)
+        "scatter_fused": {"bound": "hbm", "per_point": 4 * d + corners * levels * feats * 4},
     }
 
 
@@ -106,13 +112,26 @@ KERNELS = {  # model key -> (step-profile phase, kernel name in rocprof traces)
     "scatter": ("gpu_scatter_us", "hash_scatter_kernel<2, 2>"),
     "adam": ("gpu_adam_us", "finish_step_kernel<2>"),
 }
+# the C2 kernel when the hash-grid backward runs in its tiles (tile_scatter.hpp)
+MLP_FUSED_NAME = "mlp_train_kernel<64, 32, 2, 8, 2, 2>"
 
 
-def kernel_rooflines(prof: dict) -> list[dict]:
+def kernel_rooflines(prof: dict, fused_scatter: bool = False) -> list[dict]:
+    """Per-kernel roofline fractions from the sampled phase durations. With
+    the scatter fused into the MLP kernel, that kernel carries both the MLP's
+    FLOPs (bound "mfma", the headline figure) and the hash backward's bytes
+    ("fused_scatter": HBM rate of those bytes, and the fraction the kernel's
+    duration leaves of the roofline time max(FLOPs / MFMA peak, bytes / HBM
+    peak)); there is no separate scatter kernel then."""
     steps = max(1, prof["steps"])
+    models = kernel_models()
     out = []
-    for key, model in kernel_models().items():
+    for key, model in models.items():
+        if key == "scatter_fused" or (key == "scatter" and fused_scatter):
+            continue
         phase, name = KERNELS[key]
+        if key == "mlp" and fused_scatter:
+            name = MLP_FUSED_NAME
         us = prof[phase] / steps
         work = model.get("per_point", 0) * B_TRAIN + model.get("per_step", 0)
         if model["bound"] == "mfma":
@@ -125,6 +144,15 @@ def kernel_rooflines(prof: dict) -> list[dict]:
                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
         r.update({"traffic": traffic_from_profiles(key), "kernel": name,
                   "kernel_avg_us": round(us, 2), "work_per_launch": work})
+        if key == "mlp" and fused_scatter:
+            sb = models["scatter_fused"]["per_point"] * B_TRAIN
+            t_mfma = work / (MFMA_F16_PEAK_TFLOPS * 1e12) * 1e6
+            t_hbm = sb / (HBM_PEAK_GBS * 1e9) * 1e6
+            r["fused_scatter"] = {
+                "bytes_per_launch": sb, "achieved_GBps": round(sb / (us * 1e-6) / 1e9, 1),
+                "peak_GBps": HBM_PEAK_GBS, "t_mfma_us": round(t_mfma, 2),
+                "t_hbm_us": round(t_hbm, 2),
+                "frac_of_roofline_time": round(max(t_mfma, t_hbm) / us, 4)}
         out.append(r)
     return out
 
@@ -484,13 +512,14 @@ def main() -> int:
     infer_roof = infer_roofline(iprof)
 
     steps_prof = max(1, prof["steps"])
-    per_kernel = kernel_rooflines(prof) if prof["steps"] else []
+    fused = bool(ins.get("train_fused_scatter"))
+    per_kernel = kernel_rooflines(prof, fused) if prof["steps"] else []
     for r in per_kernel:
         if r["kernel"].startswith("encode"):
             r["achievable"] = {"reference": "gather-only kernel (the encode's corner loads)",
                                "us": round(rates["gather_us"], 2),
                                "frac_of_achievable": round(rates["gather_us"] / r["kernel_avg_us"], 4)}
-        elif r["kernel"].startswith("hash_scatter"):
+        elif r["kernel"].startswith("hash_scatter") or "fused_scatter" in r:
             r["achievable"] = {"reference": "flag-store-only and atomic-only kernels (the "
                                             "scatter's memory operations: one per run of "
                                             "lanes on the same entry, every corner and level)",

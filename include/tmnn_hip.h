@@ -171,6 +171,8 @@ typedef struct tmnn_inspection {
   uint32_t hash_param_count;
   uint32_t mlp_param_count;
   uint32_t batch_size;
+  int32_t train_fused_scatter; /* 1: the training kernel runs the hash-grid backward of
+                                  each tile itself (no separate scatter kernel) */
 } tmnn_inspection;
 
 typedef struct tmnn_context tmnn_context;

@@ -1677,6 +1677,7 @@ int tmnn_trainer_inspect(tmnn_trainer *tr, tmnn_inspection *o) {
   o->hash_param_count = tr->hash_count;
   o->mlp_param_count = tr->mlp_count;
   o->batch_size = static_cast<uint32_t>(tr->d.batch_size);
+  o->train_fused_scatter = tr->train_plan.tile_scatter ? 1 : 0;
   return TMNN_OK;
 }
 

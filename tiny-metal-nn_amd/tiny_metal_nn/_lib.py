@@ -116,6 +116,7 @@ class Inspection(ctypes.Structure):
         ("hash_param_count", ctypes.c_uint32),
         ("mlp_param_count", ctypes.c_uint32),
         ("batch_size", ctypes.c_uint32),
+        ("train_fused_scatter", ctypes.c_int32),
     ]
 
 
