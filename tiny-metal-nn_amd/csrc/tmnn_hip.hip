@@ -263,17 +263,21 @@ struct tmnn_trainer {
   DevBuf xfeat;  // input features of the batch as X tiles (encode_kernel.hpp)
   DevBuf wide_mask, wide_act;  // hidden-128 kernel: per-tile ReLU bits and fp16 activations
   DevBuf lw_act, lw_y, lw_g, lw_d;  // layer-wise path: activations, outputs, d_out, deltas
-  // The fused device step sorts its batch on a second stream into one of two
-  // buffer sets, so that a step's sort runs while the previous step's kernels
-  // still execute; the main stream waits for the sort (ev_sorted) and marks
-  // the set free again after the step (ev_consumed).
+  // The fused device step sorts its batch on a second stream into one of
+  // kSortSets buffer sets, so that a step's sort runs while the previous
+  // steps' kernels still execute; the main stream waits for the sort
+  // (ev_sorted) and marks the set free again after the step (ev_consumed).
+  // Three sets: step N's sort may start once step N - 3 is done, so it has
+  // the encode and finish windows of two steps (the MLP kernel leaves no CU
+  // room) instead of one.
+  static constexpr int kSortSets = 3;
   struct SortSet {
     DevBuf keys0, keys1, vals0, vals1, tmp;
-  } step_sort[2];
+  } step_sort[kSortSets];
   hipStream_t side = nullptr;
-  hipEvent_t ev_sorted[2] = {nullptr, nullptr};
-  hipEvent_t ev_consumed[2] = {nullptr, nullptr};
-  bool consumed_recorded[2] = {false, false};
+  hipEvent_t ev_sorted[kSortSets] = {};
+  hipEvent_t ev_consumed[kSortSets] = {};
+  bool consumed_recorded[kSortSets] = {};
   int sort_parity = 0;
   DevBuf dbg_a, dbg_b, dbg_c;
 
@@ -305,8 +309,9 @@ struct tmnn_trainer {
       (void)hipStreamSynchronize(side);
       (void)hipStreamDestroy(side);
     }
-    for (hipEvent_t e : {ev_sorted[0], ev_sorted[1], ev_consumed[0], ev_consumed[1]})
-      if (e) (void)hipEventDestroy(e);
+    for (int k = 0; k < kSortSets; ++k)
+      for (hipEvent_t e : {ev_sorted[k], ev_consumed[k]})
+        if (e) (void)hipEventDestroy(e);
     for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan, &grad_plan})
       if (p->image) (void)hipFree(p->image);
     for (auto &set : prof_events)
@@ -1127,7 +1132,7 @@ int sort_batch_overlapped(tmnn_trainer *tr, const float *d_pos, int n, bool stag
   hipStream_t st = tr->ctx->stream;
   if (!tr->side) {
     TMNN_HIP_TRY(hipStreamCreateWithFlags(&tr->side, hipStreamNonBlocking));
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < tmnn_trainer::kSortSets; ++k) {
       TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_sorted[k], hipEventDisableTiming));
       TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_consumed[k], hipEventDisableTiming));
     }
@@ -1151,12 +1156,13 @@ int sort_batch_overlapped(tmnn_trainer *tr, const float *d_pos, int n, bool stag
 }
 
 // After the last reader of the current sort set on the main stream: the set
-// may be sorted into again (two steps later); the next step takes the other.
+// may be sorted into again (kSortSets steps later); the next step takes the
+// next set.
 int sort_set_consumed(tmnn_trainer *tr) {
   const int k = tr->sort_parity;
   TMNN_HIP_TRY(hipEventRecord(tr->ev_consumed[k], tr->ctx->stream));
   tr->consumed_recorded[k] = true;
-  tr->sort_parity = k ^ 1;
+  tr->sort_parity = (k + 1) % tmnn_trainer::kSortSets;
   return TMNN_OK;
 }
 
@@ -1287,9 +1293,13 @@ int run_finish(tmnn_trainer *tr, int part_blocks, int n, float *d_loss) {
                     tr->d.num_outputs, static_cast<int>(tr->mlp_count), plan.f16, plan.train, 1);
   f.f16 = plan.f16 ? 1 : 0;
   f.image = image_current ? static_cast<unsigned char *>(plan.image) : nullptr;
+  // one round of resident blocks (two 1024-thread blocks per CU): the hash
+  // blocks take what the MLP and loss blocks leave, grid-striding the entries
+  const uint32_t resident = static_cast<uint32_t>(tr->ctx->cu_count) * 2u;
+  const uint32_t other = static_cast<uint32_t>(f.mlp_blocks) + 1u;
   const uint32_t hash_blocks = std::max<uint32_t>(
       1u, std::min<uint32_t>((tr->hash_entries + kFinishThreads - 1) / kFinishThreads,
-                             static_cast<uint32_t>(tr->ctx->cu_count) * 4u));
+                             resident > other + 1u ? resident - other : 1u));
   const dim3 grid(static_cast<uint32_t>(f.mlp_blocks) + 1u + hash_blocks);
   switch (tr->d.features_per_level) {
     case 1: hipLaunchKernelGGL(finish_step_kernel<1>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
