@@ -1293,13 +1293,17 @@ int run_finish(tmnn_trainer *tr, int part_blocks, int n, float *d_loss) {
                     tr->d.num_outputs, static_cast<int>(tr->mlp_count), plan.f16, plan.train, 1);
   f.f16 = plan.f16 ? 1 : 0;
   f.image = image_current ? static_cast<unsigned char *>(plan.image) : nullptr;
-  // one round of resident blocks (two 1024-thread blocks per CU): the hash
-  // blocks take what the MLP and loss blocks leave, grid-striding the entries
+  // Hash blocks: large tables grid-stride over at most four blocks per CU;
+  // a small table's blocks fill what the MLP and loss blocks leave of one
+  // round of resident blocks (two 1024-thread blocks per CU) when that keeps
+  // each thread at two entries or fewer (no second, partial round of blocks)
+  const uint32_t needed = (tr->hash_entries + kFinishThreads - 1) / kFinishThreads;
+  const uint32_t cap = static_cast<uint32_t>(tr->ctx->cu_count) * 4u;
   const uint32_t resident = static_cast<uint32_t>(tr->ctx->cu_count) * 2u;
   const uint32_t other = static_cast<uint32_t>(f.mlp_blocks) + 1u;
-  const uint32_t hash_blocks = std::max<uint32_t>(
-      1u, std::min<uint32_t>((tr->hash_entries + kFinishThreads - 1) / kFinishThreads,
-                             resident > other + 1u ? resident - other : 1u));
+  const uint32_t room = resident > other ? resident - other : 0u;
+  const uint32_t hash_blocks =
+      needed > cap ? cap : std::max<uint32_t>({1u, std::min(needed, room), (needed + 1u) / 2u});
   const dim3 grid(static_cast<uint32_t>(f.mlp_blocks) + 1u + hash_blocks);
   switch (tr->d.features_per_level) {
     case 1: hipLaunchKernelGGL(finish_step_kernel<1>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
