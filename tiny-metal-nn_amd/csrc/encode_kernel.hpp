@@ -50,7 +50,7 @@ struct EncodeArgs {
 constexpr int kEncodeThreads = 256;
 
 // float offset of feature quad fq (features 4 fq .. 4 fq + 3) of point i
-__host__ __device__ inline size_t xtile_offset(int i, int fq, int KT0) {
+__host__ __device__ __forceinline__ size_t xtile_offset(int i, int fq, int KT0) {
   const int t = i >> 5, nt = (i >> 4) & 1, p = i & 15;
   const int kt = fq >> 2, q = fq & 3;
   return ((((static_cast<size_t>(t) * KT0 + kt) * 2 + nt) * 64) + p + 16 * q) * 4;

@@ -99,35 +99,35 @@ struct FieldLayout {
   int32_t total;
 
   // LDS bytes of the forward A fragments (W_k^T) of layer k (k == NHL: output)
-  __host__ __device__ int32_t fwd_off(int k) const {
+  __host__ __device__ __forceinline__ int32_t fwd_off(int k) const {
     if (k == 0) return 0;
     return INP * HP * es + (k - 1) * HP * HP * es;
   }
   // LDS bytes of the forward low-part fragments fp16(W - fp16(W)) of layer k
-  __host__ __device__ int32_t fwd_lo_off(int k) const { return lo_base + fwd_off(k); }
+  __host__ __device__ __forceinline__ int32_t fwd_lo_off(int k) const { return lo_base + fwd_off(k); }
   // LDS bytes of the backward A fragments (W_k) of layer k
-  __host__ __device__ int32_t bwd_off(int k) const {
+  __host__ __device__ __forceinline__ int32_t bwd_off(int k) const {
     if (k == 0) return bwd_base;
     return bwd_base + INP * HP * es + (k - 1) * HP * HP * es;
   }
   // LDS bytes of the fp32 bias of layer k (padded to HP; output to 16)
-  __host__ __device__ int32_t bias_off(int k) const { return bias_base + k * HP * 4; }
+  __host__ __device__ __forceinline__ int32_t bias_off(int k) const { return bias_base + k * HP * 4; }
   // element offsets in the reference weight layout
   // [W0 (IN x H), b0, (W_k (H x H), b_k)..., WO (H x M), bO]
-  __host__ __device__ int32_t w_off(int k) const {
+  __host__ __device__ __forceinline__ int32_t w_off(int k) const {
     return k == 0 ? 0 : IN * H + H + (k - 1) * (H * H + H);
   }
-  __host__ __device__ int32_t b_off(int k) const {
+  __host__ __device__ __forceinline__ int32_t b_off(int k) const {
     return w_off(k) + (k == 0 ? IN * H : (k == NHL ? H * M : H * H));
   }
-  __host__ __device__ int32_t mlp_count() const { return b_off(NHL) + M; }
+  __host__ __device__ __forceinline__ int32_t mlp_count() const { return b_off(NHL) + M; }
 };
 
-__host__ __device__ inline int32_t round_up(int32_t v, int32_t m) {
+__host__ __device__ __forceinline__ int32_t round_up(int32_t v, int32_t m) {
   return (v + m - 1) / m * m;
 }
 
-__host__ __device__ inline FieldLayout make_layout(int INP, int HP, int IN,
+__host__ __device__ __forceinline__ FieldLayout make_layout(int INP, int HP, int IN,
                                                    int H, int NHL, int M,
                                                    int mlp_count, bool f16,
                                                    bool train, int wpb,
@@ -625,13 +625,13 @@ struct PackArgs {
 // K-slot order of one fp16 A fragment: slot (q, j) of K step ks covers unit
 // 32*ks + 4*q + j (j < 4) or 32*ks + 16 + 4*q + (j - 4) (j >= 4), matching
 // pack8() of two D-layout tiles.
-__host__ __device__ inline int kslot_f16(int ks, int q, int j) {
+__host__ __device__ __forceinline__ int kslot_f16(int ks, int q, int j) {
   return 32 * ks + (j < 4 ? 4 * q + j : 16 + 4 * q + (j - 4));
 }
 
 // Value of element e of layer k's forward (A = W_k^T) or backward (A = W_k)
 // fragments: the fragment slot -> (input unit i, output unit o) mapping.
-__host__ __device__ inline float frag_value(const PackArgs &a, int k, bool bwd, int e) {
+__host__ __device__ __forceinline__ float frag_value(const PackArgs &a, int k, bool bwd, int e) {
   const FieldLayout &s = a.s;
   const int kin = k == 0 ? s.INP : s.HP;
   const int kreal = k == 0 ? s.IN : s.H;

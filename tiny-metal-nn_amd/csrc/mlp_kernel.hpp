@@ -65,7 +65,7 @@ struct MlpLds {
   int32_t loss, ones, park, park_bytes, total;
 };
 
-__host__ __device__ inline MlpLds mlp_lds(const FieldLayout &s, int waves) {
+__host__ __device__ __forceinline__ MlpLds mlp_lds(const FieldLayout &s, int waves) {
   MlpLds m;
   m.loss = s.dw_off;
   m.ones = m.loss + 16 * 4;

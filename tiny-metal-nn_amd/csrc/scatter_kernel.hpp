@@ -58,7 +58,7 @@ constexpr int kMergeMinLanes = 8;
 __device__ __forceinline__ void mark_entry(uint8_t *mask, size_t entry) { mask[entry] = 1; }
 
 // feature 1 of a packed F == 2 gradient entry (see the file comment)
-__host__ __device__ inline int32_t unpack_hi(int32_t lo, int32_t hi) {
+__host__ __device__ __forceinline__ int32_t unpack_hi(int32_t lo, int32_t hi) {
   return static_cast<int32_t>(static_cast<uint32_t>(hi) + (lo < 0 ? 1u : 0u));
 }
 

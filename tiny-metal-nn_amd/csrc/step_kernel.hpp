@@ -45,7 +45,7 @@ __device__ __forceinline__ void kslot_f16_inverse(int u, int &ks, int &q, int &j
 // w: the forward (hi, and lo for fp16) and backward fragment slots of a
 // weight (the slots frag_value reads it into), or the bias slot. Padding
 // slots never change and keep the zeros pack_image_kernel wrote.
-__device__ inline void write_image_param(const FinishArgs &a, int idx, float w) {
+__device__ __forceinline__ void write_image_param(const FinishArgs &a, int idx, float w) {
   const FieldLayout &s = a.s;
   for (int k = 0; k <= s.NHL; ++k) {
     const int mreal = k == s.NHL ? s.M : s.H;

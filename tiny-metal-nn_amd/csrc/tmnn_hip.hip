@@ -150,11 +150,10 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
   if (fused && train && f16 && HP == 64 && INP == 64 && NHL == 3)
     return {mlp_train_kernel<64, 64, 3>, true, false, true, true};
   if (fused && train) {
+// fp32 training of the BASELINE shapes (fp16 took the kernels above)
 #define TMNN_TRAIN_SPEC(hp, inp, nhl)                                              \
-  if (HP == hp && INP == inp && NHL == nhl)                                        \
-    return {f16 ? field_train_kernel<hp, inp, true, nhl>                           \
-                : field_train_kernel<hp, inp, false, nhl>,                         \
-            true, false, true};
+  if (!f16 && HP == hp && INP == inp && NHL == nhl)                                \
+    return {field_train_kernel<hp, inp, false, nhl>, true, false, true};
     TMNN_TRAIN_SPEC(64, 32, 2)  // image fit: 16x2 features, 64x2 MLP
     TMNN_TRAIN_SPEC(64, 32, 1)  // NeRF density: 16x2, 64x1
     TMNN_TRAIN_SPEC(64, 64, 3)  // SDF: 16x4, 64x3

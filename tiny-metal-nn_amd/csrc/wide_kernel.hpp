@@ -45,7 +45,7 @@ struct WideLayout {
   int32_t total;
 };
 
-__host__ __device__ inline WideLayout make_wide_layout(const FieldLayout &fl, bool f16, bool train) {
+__host__ __device__ __forceinline__ WideLayout make_wide_layout(const FieldLayout &fl, bool f16, bool train) {
   WideLayout w;
   const int es = f16 ? 2 : 4;
   const int wbuf = (f16 ? 2 : 1) * kWideHP * kWideHP * es;  // largest layer's forward fragments

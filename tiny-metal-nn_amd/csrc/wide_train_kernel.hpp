@@ -42,7 +42,7 @@ struct WideTrainLds {
   int32_t bias, loss, park, park_bytes, total;
 };
 
-__host__ __device__ inline WideTrainLds wide_train_lds(const FieldLayout &s) {
+__host__ __device__ __forceinline__ WideTrainLds wide_train_lds(const FieldLayout &s) {
   WideTrainLds m;
   m.bias = 2 * kWideHP * kWideHP * 2;  // a hidden layer's forward hi + lo fragments
   m.loss = m.bias + round_up(s.res_off - s.bias_base, 16);
