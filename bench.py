@@ -116,24 +116,28 @@ KERNELS = {  # model key -> (step-profile phase, kernel name in rocprof traces)
 MLP_FUSED_NAME = "mlp_train_kernel<64, 32, 2, 8, 2, 2>"
 
 
-def kernel_rooflines(prof: dict, fused_scatter: bool = False) -> list[dict]:
+def kernel_rooflines(prof: dict, fused_scatter: bool = False, models: dict | None = None,
+                     names: dict | None = None, n: int = B_TRAIN) -> list[dict]:
     """Per-kernel roofline fractions from the sampled phase durations. With
     the scatter fused into the MLP kernel, that kernel carries both the MLP's
     FLOPs (bound "mfma", the headline figure) and the hash backward's bytes
     ("fused_scatter": HBM rate of those bytes, and the fraction the kernel's
     duration leaves of the roofline time max(FLOPs / MFMA peak, bytes / HBM
-    peak)); there is no separate scatter kernel then."""
+    peak)); there is no separate scatter kernel then. models / names / n
+    default to the C2 step (kernel_models(), KERNELS, B_TRAIN)."""
     steps = max(1, prof["steps"])
-    models = kernel_models()
+    models = models or kernel_models()
     out = []
     for key, model in models.items():
         if key == "scatter_fused" or (key == "scatter" and fused_scatter):
             continue
         phase, name = KERNELS[key]
-        if key == "mlp" and fused_scatter:
+        if names:
+            name = names[key]
+        elif key == "mlp" and fused_scatter:
             name = MLP_FUSED_NAME
         us = prof[phase] / steps
-        work = model.get("per_point", 0) * B_TRAIN + model.get("per_step", 0)
+        work = model.get("per_point", 0) * n + model.get("per_step", 0)
         if model["bound"] == "mfma":
             achieved = work / (us * 1e-6) / 1e12
             r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
@@ -142,10 +146,10 @@ def kernel_rooflines(prof: dict, fused_scatter: bool = False) -> list[dict]:
             achieved = work / (us * 1e-6) / 1e9
             r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
-        r.update({"traffic": traffic_from_profiles(key), "kernel": name,
+        r.update({"traffic": traffic_from_profiles(key) if not names else None, "kernel": name,
                   "kernel_avg_us": round(us, 2), "work_per_launch": work})
         if key == "mlp" and fused_scatter:
-            sb = models["scatter_fused"]["per_point"] * B_TRAIN
+            sb = models["scatter_fused"]["per_point"] * n
             t_mfma = work / (MFMA_F16_PEAK_TFLOPS * 1e12) * 1e6
             t_hbm = sb / (HBM_PEAK_GBS * 1e9) * 1e6
             r["fused_scatter"] = {
@@ -272,8 +276,21 @@ def run_other_workload(args, which: str) -> int:
     tr.synchronize()
     fwd = (time.perf_counter() - t1) / args.steps
     losses = loss_dev.cpu().numpy()
+    fused = bool(tr.inspect_runtime().get("train_fused_scatter"))
     tr.close()
     steps_prof = max(1, prof["steps"])
+    inp = 32 if levels * feats <= 32 else 64
+    mlp_params = (levels * feats * hidden + hidden + (nhl - 1) * (hidden * hidden + hidden)
+                  + hidden * m + m)
+    models = kernel_models(d, levels, feats, m, inp, hidden, nhl, levels * feats << log2t,
+                           mlp_params)
+    mlp_name = {"c3": "mlp_train_kernel<64, 32, 1, 8, 3, 2>" if fused else
+                      "mlp_train_kernel<64, 32, 1, 8, 0, 0>",
+                "c4": "mlp_train_kernel<64, 64, 3, 4, 0, 0>", "c5": "wide_train_kernel<4>"}[which]
+    names = {"encode": f"encode_level_kernel<{d}, {feats}>", "mlp": mlp_name,
+             "scatter": f"hash_scatter_level_kernel<{d}, {feats}>",
+             "adam": f"finish_step_kernel<{feats}>"}
+    per_kernel = kernel_rooflines(prof, fused, models, names, n) if prof["steps"] else []
     print(json.dumps({
         "metric": f"train samples/s ({which}); forward-only samples/s", "value": round(n * args.steps / el, 1),
         "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -284,6 +301,7 @@ def run_other_workload(args, which: str) -> int:
                    "mlp": f"{hidden}x{nhl}->{m}", "loss": loss},
         "forward_samples_per_s": round(n / fwd, 1), "forward_ms": round(fwd * 1e3, 4),
         "phase_us_per_step": {k: round(prof[k] / steps_prof, 2) for k in prof if k.startswith("gpu_")},
+        "kernel_rooflines": per_kernel,
         "loss_first_last": [round(float(losses[0]), 6),
                             round(float(losses[args.warmup + args.steps - 1]), 6)]}), flush=True)
     return 0

@@ -37,9 +37,13 @@ namespace tmnn_hip {
 // LDS plan of wide_train_kernel (bytes): one layer's staged weight fragments,
 // the biases of every layer (fp32, image order), the per-wave loss slots,
 // then per wave its parking slots (16 bytes per lane each): [0, 8) delta^T
-// tiles, [8, 16) layer-input^T tiles, 16 the output gradient^T.
+// tiles, [8, 16) layer-input^T tiles, 16 the output gradient^T; then per
+// wave its owned dW_0 and dW_out accumulators (kWideAccSlots f32x4 per lane),
+// which are live only during their layer's owner jobs.
+constexpr int kWideAccSlots = 6;  // dW_0: 2 * 8 / 4 tiles, dW_out: 8 / 4
+
 struct WideTrainLds {
-  int32_t bias, loss, park, park_bytes, total;
+  int32_t bias, loss, park, park_bytes, acc, total;
 };
 
 __host__ __device__ __forceinline__ WideTrainLds wide_train_lds(const FieldLayout &s) {
@@ -48,7 +52,8 @@ __host__ __device__ __forceinline__ WideTrainLds wide_train_lds(const FieldLayou
   m.loss = m.bias + round_up(s.res_off - s.bias_base, 16);
   m.park = m.loss + 16 * 4;
   m.park_bytes = (2 * kWideHT + 1) * 64 * 16;
-  m.total = m.park + kWideWaves * m.park_bytes;
+  m.acc = m.park + kWideWaves * m.park_bytes;
+  m.total = m.acc + kWideWaves * kWideAccSlots * 64 * 16;
   return m;
 }
 
@@ -70,6 +75,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   constexpr int kSlotsOut = (kJobsOut + W - 1) / W;
   constexpr int kSlotsHid = (kJobsHid + W - 1) / W;
   constexpr int kSlots0 = (kJobs0 + W - 1) / W;
+  static_assert(kSlots0 + kSlotsOut <= kWideAccSlots, "LDS accumulator slots");
   constexpr int kHSlot = HT;       // first layer-input^T slot
   constexpr int kGSlot = 2 * HT;   // output gradient^T slot
   extern __shared__ __align__(16) unsigned char smem[];
@@ -77,8 +83,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   const FieldLayout s = make_layout(INP, HP, a.IN, a.H, NHL, a.M, a.mlp_count, true, true, 1);
   const WideTrainLds ml = wide_train_lds(s);
   copy_to_lds(smem + ml.bias, a.image + s.bias_base, s.res_off - s.bias_base);
-  // parked operands of absent tiles must be finite (they meet zero deltas)
-  for (int e = threadIdx.x; e < W * ml.park_bytes / 16; e += blockDim.x)
+  // parked operands of absent tiles must be finite (they meet zero deltas);
+  // the LDS accumulators start at zero (they follow the parking slots)
+  for (int e = threadIdx.x; e < (ml.total - ml.park) / 16; e += blockDim.x)
     reinterpret_cast<uint4 *>(smem + ml.park)[e] = make_uint4(0u, 0u, 0u, 0u);
   __syncthreads();
 
@@ -93,6 +100,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
     return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
   };
   auto bias_of = [&](int k) { return reinterpret_cast<const float *>(smem + ml.bias + k * HP * 4); };
+  // this wave's LDS accumulator j: [0, kSlots0) dW_0, then dW_out (lane-private)
+  f32x4 *acc_lds = reinterpret_cast<f32x4 *>(smem + ml.acc) + wave * kWideAccSlots * 64 + lane;
+  auto acc_at = [&](int j) -> f32x4 & { return acc_lds[j * 64]; };
   // Weight stages, double-buffered: a round walks 3 NHL + 1 stages (below),
   // stage i in buffer (i + par) & 1 of two 32 KB buffers. At each stage
   // boundary the block waits for its loads and meets at one barrier, which
@@ -143,9 +153,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
 
-  f32x4 accO[kSlotsOut];
   f32x4 accH[NHL - 1][kSlotsHid];
-  f32x4 acc0[kSlots0];
   float bsO = 0.0f;                       // output bias (wave 0): lane partial sums
   float bsH[NHL - 1][kBiasTiles];         // hidden biases of the owned unit tiles
   float bs0[kBiasTiles];
@@ -164,13 +172,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
     return acc;
   };
 #pragma unroll
-  for (int j = 0; j < kSlotsOut; ++j) accO[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
   for (int k = 0; k < NHL - 1; ++k)
 #pragma unroll
     for (int j = 0; j < kSlotsHid; ++j) accH[k][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < kSlots0; ++j) acc0[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float lane_loss = 0.0f;
   const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
   half8 *act_store = reinterpret_cast<half8 *>(a.wide_act);
@@ -299,6 +303,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
         boundary();
         fetch_stage(2 * NHL + 1);
         if (wgrads) {
+          f32x4 accO[kSlotsOut];
+#pragma unroll
+          for (int j = 0; j < kSlotsOut; ++j) accO[j] = acc_at(kSlots0 + j);
 #pragma unroll 1
           for (int w = 0; w < W; ++w)  // waves outermost: one wave's operands live
 #pragma unroll
@@ -309,6 +316,8 @@ __global__ void __launch_bounds__(kWideWaves * 64)
                                                                  opnd(w, kGSlot), accO[j], 0, 0, 0);
               if (j == 0 && wave == 0) bsO = add8(bsO, opnd(w, kGSlot));
             }
+#pragma unroll
+          for (int j = 0; j < kSlotsOut; ++j) acc_at(kSlots0 + j) = accO[j];
         }
         // delta of the last hidden layer (backward fragments of the output layer)
         mma_packed<1, HT>(buf(2 * NHL), gb, act, lane);  // act now holds W_out g (pre-mask)
@@ -386,6 +395,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
               if (j < kBiasTiles) bsH[k - 1][j] = add8(bsH[k - 1][j], opnd(w, wave + W * j));
             }
         } else {
+          f32x4 acc0[kSlots0];
+#pragma unroll
+          for (int j = 0; j < kSlots0; ++j) acc0[j] = acc_at(j);
 #pragma unroll 1
           for (int w = 0; w < W; ++w)
 #pragma unroll
@@ -396,6 +408,8 @@ __global__ void __launch_bounds__(kWideWaves * 64)
                     opnd(w, kHSlot + job / HT), opnd(w, job % HT), acc0[j], 0, 0, 0);
               if (j < kBiasTiles) bs0[j] = add8(bs0[j], opnd(w, wave + W * j));
             }
+#pragma unroll
+          for (int j = 0; j < kSlots0; ++j) acc_at(j) = acc0[j];
         }
       }
       if (k > 0) {
@@ -446,6 +460,11 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   // ---- owners write their tiles of the block's partial row (reference layout)
   float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
   const float sc = a.inv_loss_scale;
+  f32x4 accO[kSlotsOut], acc0[kSlots0];
+#pragma unroll
+  for (int j = 0; j < kSlotsOut; ++j) accO[j] = acc_at(kSlots0 + j);
+#pragma unroll
+  for (int j = 0; j < kSlots0; ++j) acc0[j] = acc_at(j);
   const int H = a.H, IN = a.IN, M = a.M;
 #pragma unroll
   for (int j = 0; j < kSlotsOut; ++j) {
