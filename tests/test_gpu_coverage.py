@@ -115,8 +115,10 @@ def _identity_mlp(IN, H, NHL, M, first):
 @pytest.mark.parametrize("name", ["2d_f2", "3d_f2", "3d_f4"])
 @pytest.mark.parametrize("family", ["auto", "Tiled"])
 def test_inference_inline_encode_bit_exact(oracle, name, family):
-    """The inline encode of the fp32 inference kernel (field_forward_kernel,
-    specialised per geometry under FullyFused, generic under Tiled), read
+    """The encode of the fp32 inference path (inline in field_forward_kernel,
+    specialised per geometry under FullyFused, generic under Tiled; for F <= 2
+    tables with level slices over 2 MB, 3d_f2 here, encode_level_kernel's X
+    tiles read by field_forward_x_kernel), read
     through an MLP that copies features to outputs: with a positive table
     the features are >= 0, ReLU passes them, and each output is
     1.0 * feature + exact zeros, so every output equals the oracle's feature

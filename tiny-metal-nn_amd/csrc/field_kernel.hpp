@@ -1057,8 +1057,11 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   float P[kNT][4];
   Gathered<(DF ? DF / 8 : 2), (DF ? DF % 8 : 2), KT0> G;
   f32x4 Xn[KT0][kNT];  // XMEM: features of the next tile, in flight
+  // the X prefetch runs one tile ahead when its registers are cheap: 32
+  // features, or the forward-only kernels (no dW accumulators)
+  constexpr bool kPrefetchX = KT0 <= 2 || !TRAIN;
   if constexpr (XMEM) {
-    if constexpr (KT0 <= 2) load_x(tile, Xn);
+    if constexpr (kPrefetchX) load_x(tile, Xn);
   } else {
     load_pos(tile, P);
     if constexpr (kPipe) gather_issue<DF / 8, DF % 8, KT0>(a, res, q, P, G);
@@ -1078,13 +1081,12 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
     f32x4 X[KT0][kNT];
     float Pn[kNT][4];
     if constexpr (XMEM) {
-      if constexpr (KT0 > 2) load_x(tile, Xn);
+      if constexpr (!kPrefetchX) load_x(tile, Xn);
 #pragma unroll
       for (int kt = 0; kt < KT0; ++kt)
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt) X[kt][nt] = Xn[kt][nt];
-      // one tile ahead when the prefetch registers are cheap (32 features)
-      if constexpr (KT0 <= 2) load_x(next, Xn);
+      if constexpr (kPrefetchX) load_x(next, Xn);
     } else {
       if constexpr (kPipe)
         gather_finish<DF / 8, DF % 8, KT0>(a, res, q, P, G, X);
@@ -1393,6 +1395,16 @@ __global__ void __launch_bounds__(kBlockThreads)
 template <int HP, int INP, bool F16, int DF>
 __global__ void __launch_bounds__(kBlockThreads) field_forward_kernel(FieldArgs a) {
   field_body<HP, INP, F16, false, DF, 0>(a);
+}
+
+// Forward only over X tiles written by the level-major encode
+// (encode_level_kernel), for tables whose level slices exceed 2 MB: there the
+// inline gathers of field_forward_kernel miss to HBM at one or two waves per
+// SIMD and stall its MFMA work, while the level-major encode keeps one
+// level's slice in the caches at full occupancy.
+template <int HP, int INP, bool F16>
+__global__ void __launch_bounds__(kBlockThreads) field_forward_x_kernel(FieldArgs a) {
+  field_body<HP, INP, F16, false, 0, 0, true>(a);
 }
 
 }  // namespace tmnn_hip

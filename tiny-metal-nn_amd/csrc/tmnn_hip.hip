@@ -115,10 +115,21 @@ KernelChoice select_wide_kernel(bool f16, bool train, int D, int F, int NHL) {
 // specialised on the BASELINE geometries (compile-time D, F) or on the
 // runtime geometry; the hidden-128 forward reads X tiles.
 KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, int NHL,
-                           int family, bool small_table = false) {
+                           int family, bool small_table = false, bool split_encode = false) {
   const bool fused = family == TMNN_FAMILY_FULLY_FUSED;
   if (HP == kWideHP)
     return INP == 32 && fused ? select_wide_kernel(f16, train, D, F, NHL) : KernelChoice{};
+  // forward passes over tables with level slices above 2 MB: the level-major
+  // encode, then the MLP over its X tiles (every family)
+#define TMNN_FWD_X(hp, inp)                                                          \
+  if (!train && split_encode && HP == hp && INP == inp)                              \
+    return {f16 ? field_forward_x_kernel<hp, inp, true> : field_forward_x_kernel<hp, inp, false>, \
+            false, false, true};
+  TMNN_FWD_X(64, 32)
+  TMNN_FWD_X(64, 64)
+  TMNN_FWD_X(32, 32)
+  TMNN_FWD_X(32, 64)
+#undef TMNN_FWD_X
   const int DF = D * 8 + F;
 #define TMNN_FWD_SPEC(hp, inp, df)                                                   \
   if (fused && !train && HP == hp && INP == inp && DF == df)                         \
@@ -493,10 +504,15 @@ bool size_plan_fused(const ModelShape &m, bool f16, bool train, int family, int 
     *why = m.HP > kWideHP ? TMNN_PLAN_HIDDEN_DIM_UNSUPPORTED : TMNN_PLAN_NO_FUSED_INSTANCE;
     return false;
   }
-  // level slices up to 8 MB: the scatter runs point-major (level_major())
-  const bool small_table = (static_cast<size_t>(m.F) * 4u << m.log2T) <= (8u << 20);
-  const KernelChoice kc =
-      select_kernel(m.HP, m.INP, f16, train, m.D, m.F, m.NHL, family, small_table);
+  // level slices up to 8 MB: the scatter runs point-major (level_major());
+  // above 2 MB the encode runs level-major (encode_level_major()), and so do
+  // the forward passes of F <= 2 tables (C3: 789 -> 510 us at 2^20 points;
+  // C4's F = 4 slices measured 571 inline against 578 split, kept inline)
+  const size_t slice = static_cast<size_t>(m.F) * 4u << m.log2T;
+  const bool small_table = slice <= (8u << 20);
+  const bool split_encode = slice > (2u << 20) && m.F <= 2;
+  const KernelChoice kc = select_kernel(m.HP, m.INP, f16, train, m.D, m.F, m.NHL, family,
+                                        small_table, split_encode);
   out.fn = kc.fn;
   out.reg_dw = kc.reg_dw;
   out.wide = kc.wide;
@@ -647,7 +663,7 @@ void plan_network_impl(const tmnn_device_caps &caps, const tmnn_model_desc &d,
     int why = 0;
     p.fused_eval = sel == TMNN_FAMILY_FULLY_FUSED &&
                    size_plan(m, false, false, sel, caps.lds_bytes_per_cu, ep, &why) &&
-                   (ep.wide || ep.fn != select_kernel(m.HP, m.INP, false, false, m.D, m.F, m.NHL,
+                   (ep.wide || ep.xmem || ep.fn != select_kernel(m.HP, m.INP, false, false, m.D, m.F, m.NHL,
                                                       TMNN_FAMILY_TILED).fn);
   }
   p.train_lds_bytes = fam[sel].tp.lds;
