@@ -34,6 +34,24 @@ __host__ __device__ constexpr bool tile_scatter_shape(int D, int F) {
   return F == 2 && (D == 2 || D == 3);
 }
 
+// Visit flags are stored through a raw buffer resource over the flag array
+// (num_records = L * T bytes): the entry index is the store's 32-bit offset
+// (no 64-bit address arithmetic), and a lane with nothing to mark passes
+// kNoEntry, an offset past num_records, whose store the buffer range check
+// drops (no branch around the store). Flag arrays of the fused shapes are at
+// most 32 levels of 2^20 entries (8 MB slices at F = 2), far below 2^31.
+constexpr uint32_t kNoEntry = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t flag_rsrc(uint8_t *mask, int L, uint32_t log2T) {
+  // dword 3: 32-bit data format, the raw-buffer setting of gfx9 parts
+  return __builtin_amdgcn_make_buffer_rsrc(mask, 0, static_cast<int>(static_cast<uint32_t>(L) << log2T),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ void mark_flag(__amdgpu_buffer_rsrc_t r, uint32_t entry) {
+  __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(1), r, static_cast<int>(entry), 0, 0);
+}
+
 // dx: the tile's input-feature gradients (fp32, still carrying the loss
 // scale); pos: the lane's point positions per column tile (sorted order);
 // res: the per-level resolution table (the LDS image's copy).
@@ -43,6 +61,7 @@ __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&d
                                              const float *res, int q) {
   static_assert(tile_scatter_shape(D, F), "fused scatter shape");
   const uint32_t tmask = (1u << a.log2T) - 1u;
+  const __amdgpu_buffer_rsrc_t flags = flag_rsrc(a.mask, a.L, a.log2T);
 #pragma unroll
   for (int kt = 0; kt < KT0; ++kt)
 #pragma unroll
@@ -50,7 +69,7 @@ __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&d
       const int l = 8 * kt + 2 * q + h;
       const bool lv = l < a.L;
       const float rl = res[lv ? l : 0];
-      const size_t lbase = static_cast<size_t>(lv ? l : 0) << a.log2T;
+      const uint32_t lbase = static_cast<uint32_t>(lv ? l : 0) << a.log2T;
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) {
         const bool on = valid[nt] && lv;
@@ -71,12 +90,12 @@ __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&d
             int co[D];
             float wc[D];
             corner_of<D>(c, 2 * m, co, wc);
-            const uint32_t e0 = on ? static_cast<uint32_t>(lbase + hash_corner<D>(co, tmask)) : ~0u;
+            const uint32_t e0 = on ? lbase + hash_corner<D>(co, tmask) : kNoEntry;
             co[0] += 1;
-            const uint32_t e1 = on ? static_cast<uint32_t>(lbase + hash_corner<D>(co, tmask)) : ~0u;
+            const uint32_t e1 = on ? lbase + hash_corner<D>(co, tmask) : kNoEntry;
             const auto r = __builtin_amdgcn_permlane32_swap(e0, e1, false, false);
-            if (r[0] != ~0u) mark_entry(a.mask, r[0]);
-            if (r[1] != ~0u) mark_entry(a.mask, r[1]);
+            mark_flag(flags, r[0]);
+            mark_flag(flags, r[1]);
           }
         } else {
           const bool fits = __all(!on || grads_fit<2>(d));
@@ -85,7 +104,7 @@ __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&d
             int co[D];
             float wc[D];
             corner_of<D>(c, k, co, wc);
-            const size_t entry = lbase + hash_corner<D>(co, tmask);
+            const uint32_t entry = lbase + hash_corner<D>(co, tmask);
             const float w = corner_weight<D>(wc);
             int32_t ci[2];
 #pragma unroll
@@ -93,15 +112,13 @@ __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&d
               const float v = d[f] * w;
               ci[f] = fits ? static_cast<int32_t>(v * kGradScale) : f2i_trunc(v * kGradScale);
             }
-            if (on) {
-              const int64_t v64 = static_cast<int64_t>(
-                  (static_cast<uint64_t>(static_cast<uint32_t>(ci[1])) << 32) +
-                  static_cast<uint64_t>(static_cast<int64_t>(ci[0])));
-              if (v64 != 0)
-                atomicAdd(reinterpret_cast<unsigned long long *>(a.grad_hash + entry * 2),
-                          static_cast<unsigned long long>(v64));
-              mark_entry(a.mask, entry);
-            }
+            const int64_t v64 = static_cast<int64_t>(
+                (static_cast<uint64_t>(static_cast<uint32_t>(ci[1])) << 32) +
+                static_cast<uint64_t>(static_cast<int64_t>(ci[0])));
+            if (on && v64 != 0)
+              atomicAdd(reinterpret_cast<unsigned long long *>(a.grad_hash + static_cast<size_t>(entry) * 2),
+                        static_cast<unsigned long long>(v64));
+            mark_flag(flags, on ? entry : kNoEntry);
           }
         }
       }
