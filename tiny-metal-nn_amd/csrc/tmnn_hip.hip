@@ -287,6 +287,7 @@ struct tmnn_trainer {
   hipStream_t side = nullptr;
   hipEvent_t ev_sorted[kSortSets] = {};
   hipEvent_t ev_consumed[kSortSets] = {};
+  hipEvent_t ev_staged = nullptr;  // host-staged batch copied in on the main stream
   bool consumed_recorded[kSortSets] = {};
   int sort_parity = 0;
   DevBuf dbg_a, dbg_b, dbg_c;
@@ -322,6 +323,7 @@ struct tmnn_trainer {
     for (int k = 0; k < kSortSets; ++k)
       for (hipEvent_t e : {ev_sorted[k], ev_consumed[k]})
         if (e) (void)hipEventDestroy(e);
+    if (ev_staged) (void)hipEventDestroy(ev_staged);
     for (KernelPlan *p : {&train_plan, &fwd_plan, &infer_plan, &grad_plan})
       if (p->image) (void)hipFree(p->image);
     for (auto &set : prof_events)
@@ -1136,6 +1138,14 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
   return TMNN_OK;
 }
 
+// Flags of the events that order the side stream's sort and the main stream's
+// step. Both streams run on this device, so the producer's release and the
+// consumer's acquire only need device scope: without
+// hipEventDisableSystemFence every record and wait adds a system-scope fence
+// (cache write-back and invalidation), measured at C2 as 98.7 -> 94.6 us per
+// step.
+constexpr unsigned kSyncEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
+
 // The fused step's Morton sort on the side stream into buffer set
 // tr->sort_parity (see tmnn_trainer::step_sort): the side stream first waits
 // until the step that last used the set has finished (and, when the batch
@@ -1148,24 +1158,28 @@ int sort_batch_overlapped(tmnn_trainer *tr, const float *d_pos, int n, bool stag
   if (!tr->side) {
     TMNN_HIP_TRY(hipStreamCreateWithFlags(&tr->side, hipStreamNonBlocking));
     for (int k = 0; k < tmnn_trainer::kSortSets; ++k) {
-      TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_sorted[k], hipEventDisableTiming));
-      TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_consumed[k], hipEventDisableTiming));
+      TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_sorted[k], kSyncEventFlags));
+      TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_consumed[k], kSyncEventFlags));
     }
   }
   const int k = tr->sort_parity;
   auto &ss = tr->step_sort[k];
-  if (tr->consumed_recorded[k]) TMNN_HIP_TRY(hipStreamWaitEvent(tr->side, tr->ev_consumed[k], 0));
+  hipStream_t sd = tr->side;
+  if (tr->consumed_recorded[k]) TMNN_HIP_TRY(hipStreamWaitEvent(sd, tr->ev_consumed[k], 0));
   if (staged_on_main) {
-    // the batch was copied in on the main stream: the sort reads it after that
-    TMNN_HIP_TRY(hipEventRecord(tr->ev_sorted[k], st));
-    TMNN_HIP_TRY(hipStreamWaitEvent(tr->side, tr->ev_sorted[k], 0));
+    // the batch was copied in on the main stream: the sort reads it after
+    // that (an event with the system-scope fence, as the copy came from host
+    // memory)
+    if (!tr->ev_staged) TMNN_HIP_TRY(hipEventCreateWithFlags(&tr->ev_staged, hipEventDisableTiming));
+    TMNN_HIP_TRY(hipEventRecord(tr->ev_staged, st));
+    TMNN_HIP_TRY(hipStreamWaitEvent(sd, tr->ev_staged, 0));
   }
   const uint32_t *sorted_keys = nullptr;
   TMNN_HIP_TRY(morton_sort_batch(ss.tmp.ptr, ss.tmp.bytes, d_pos, tr->d.spatial_dims,
                                  ss.keys0.as<uint32_t>(), ss.keys1.as<uint32_t>(),
-                                 ss.vals0.as<uint32_t>(), ss.vals1.as<uint32_t>(), n, tr->side,
+                                 ss.vals0.as<uint32_t>(), ss.vals1.as<uint32_t>(), n, sd,
                                  &sorted_keys, perm_out));
-  TMNN_HIP_TRY(hipEventRecord(tr->ev_sorted[k], tr->side));
+  TMNN_HIP_TRY(hipEventRecord(tr->ev_sorted[k], sd));
   TMNN_HIP_TRY(hipStreamWaitEvent(st, tr->ev_sorted[k], 0));
   return TMNN_OK;
 }
