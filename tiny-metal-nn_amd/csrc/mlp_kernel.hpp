@@ -210,16 +210,26 @@ __device__ __forceinline__ void pack_tiles(const f32x4 (&t)[KT][kNT], half8 (&b)
     for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = pack8(t[2 * ks][nt], t[2 * ks + 1][nt]);
 }
 
-// ReLU' of a packed fp16 activation tile pair as fp16 factors: 1 where the
-// activation is > 0, else 0 (or -0 for a -0 activation): min(h * 65504 *
-// 65504, 1) lifts the smallest positive fp16 (2^-24) above 1. Three packed
-// fp16 ops per pair of elements here, one packed multiply (exact) to apply;
-// integer masks instead are rewritten by the compiler into per-element
-// compares and selects.
-__device__ __forceinline__ half8 relu_factors(half8 h) {
-  const half8 big = static_cast<_Float16>(65504.0f);
-  const half8 one = static_cast<_Float16>(1.0f);
-  return __builtin_elementwise_min((h * big) * big, one);
+// ReLU' of a packed fp16 activation tile pair (ReLU outputs: +0, positive or
+// NaN) as 16-bit masks: 0 - min(bits, 1) is 0x0000 exactly for +0, else
+// 0xFFFF; applied to a packed fp16 delta by a 32-bit AND. Two packed integer
+// ops per pair to make (the fp16 factors take three), one to apply. `ones`
+// holds 0x00010001 in an opaque scalar register (set up once per kernel):
+// with a literal the compiler proves the 0/1 range and rewrites the ops into
+// per-element compares and selects.
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint4 relu_keep(half8 h, uint32_t ones) {
+  const u16x8 o = __builtin_bit_cast(u16x8, make_uint4(ones, ones, ones, ones));
+  const u16x8 m = static_cast<u16x8>(0) - __builtin_elementwise_min(__builtin_bit_cast(u16x8, h), o);
+  return __builtin_bit_cast(uint4, m);
+}
+__device__ __forceinline__ half8 apply_keep(half8 d, uint4 keep) {
+  uint4 v = __builtin_bit_cast(uint4, d);
+  v.x &= keep.x;
+  v.y &= keep.y;
+  v.z &= keep.z;
+  v.w &= keep.w;
+  return __builtin_bit_cast(half8, v);
 }
 
 // max(x, 0) as one v_maximum3_f32 (fmaxf on an MFMA result adds a NaN-quieting
@@ -288,6 +298,8 @@ __global__ void __launch_bounds__(W * 64)
   };
   half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
+  uint32_t ones16 = 0x00010001u;  // relu_keep's operand, opaque to the compiler
+  asm volatile("" : "+s"(ones16));
 
   f32x4 accO[kSlotsOut];
   f32x4 accH[NHL > 1 ? NHL - 1 : 1][kSlotsHid];
@@ -399,7 +411,7 @@ __global__ void __launch_bounds__(W * 64)
 
     // ---- forward; transposed fp16 layer inputs parked, ReLU masks kept
     f32x4 act[HT][kNT];
-    half8 mask[NHL][HS][kNT];  // ReLU' factors of the hidden layers
+    uint4 mask[NHL][HS][kNT];  // ReLU' masks of the hidden layers (relu_keep)
     {
       half8 bh[XS][kNT], bl[XS][kNT];
       pack_split_tiles<KT0>(X, bh, bl);
@@ -425,7 +437,7 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
       for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) mask[k][ks][nt] = relu_factors(bh[ks][nt]);
+        for (int nt = 0; nt < kNT; ++nt) mask[k][ks][nt] = relu_keep(bh[ks][nt], ones16);
       half8 hT[HT];
       transpose_tiles<HS>(bh, sel_lo, sel_hi, hT);
 #pragma unroll
@@ -494,7 +506,7 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
       for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = b[ks][nt] * mask[k][ks][nt];
+        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = apply_keep(b[ks][nt], mask[k][ks][nt]);
       {
         half8 dT[HT];
         transpose_tiles<HS>(b, sel_lo, sel_hi, dT);

@@ -152,6 +152,8 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   };
   half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
+  uint32_t ones16 = 0x00010001u;  // relu_keep's operand, opaque to the compiler
+  asm volatile("" : "+s"(ones16));
 
   f32x4 accH[NHL - 1][kSlotsHid];
   float bsO = 0.0f;                       // output bias (wave 0): lane partial sums
@@ -237,7 +239,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
       mma_split_packed<XS, HT>(buf(0), buf(0) + INP * HP * 2, bh, bl, bias_of(0), act, lane);
       relu();
     }
-    half8 fac[HS][kNT];  // ReLU' factors of the layer whose delta is formed next
+    uint4 fac[HS][kNT];  // ReLU' masks of the layer whose delta is formed next (relu_keep)
 #pragma unroll
     for (int k = 1; k <= NHL; ++k) {
       half8 bh[HS][kNT], bl[HS][kNT];
@@ -276,7 +278,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
         for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-          for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_factors(bh[ks][nt]);
+          for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_keep(bh[ks][nt], ones16);
         boundary();  // stage 2 NHL - 1: F_out
         fetch_stage(2 * NHL);
         f32x4 y[1][kNT];
@@ -335,7 +337,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
       for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = b[ks][nt] * fac[ks][nt];
+        for (int nt = 0; nt < kNT; ++nt) b[ks][nt] = apply_keep(b[ks][nt], fac[ks][nt]);
       {
         half8 dT[HT];
         transpose_tiles<HS>(b, sel_lo, sel_hi, dT);
@@ -356,7 +358,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
         for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-          for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_factors(hb[ks][nt]);
+          for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_keep(hb[ks][nt], ones16);
       } else {
         // the input features again (L2-resident): not kept live across the round
         f32x4 X0[KT0][kNT];
