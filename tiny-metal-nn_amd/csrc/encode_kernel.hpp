@@ -71,19 +71,25 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeA
   const size_t src = valid ? (a.perm ? a.perm[i] : static_cast<uint32_t>(i)) : 0u;
 #pragma unroll
   for (int k = 0; k < D; ++k) p[k] = valid ? a.pos[src * D + k] : 0.0f;
-  if (a.pos_out && valid)
+  if (a.pos_out && valid && blockIdx.y == 0)
 #pragma unroll
     for (int k = 0; k < D; ++k) a.pos_out[static_cast<size_t>(i) * D + k] = p[k];
   const uint32_t tmask = (1u << a.log2T) - 1u;
+  // gridDim.y > 1 (batches too small to fill the chip): thread (i, y) takes
+  // feature quads [y * qps, (y + 1) * qps) of point i, so a small batch's
+  // gathers spread over more threads instead of queueing in a few
   const int nquads = 4 * a.KT0;
-  for (int q0 = 0; q0 < nquads; q0 += QG) {
+  const int qps = (nquads + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
+  const int qbeg = static_cast<int>(blockIdx.y) * qps;
+  const int qend = qbeg + qps < nquads ? qbeg + qps : nquads;
+  for (int q0 = qbeg; q0 < qend; q0 += QG) {
     float v[QG][LPQ][C][F];
 #pragma unroll
     for (int g = 0; g < QG; ++g)
 #pragma unroll
       for (int lv = 0; lv < LPQ; ++lv) {
         const int l = (q0 + g) * LPQ + lv;
-        const bool on = valid && q0 + g < nquads && l < a.L;
+        const bool on = valid && q0 + g < qend && l < a.L;
         const Cell<D> c = cell_of<D>(p, a.res[on ? l : 0]);
         const size_t lbase = static_cast<size_t>(on ? l : 0) << a.log2T;
 #pragma unroll
@@ -107,7 +113,7 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_features_kernel(EncodeA
       }
 #pragma unroll
     for (int g = 0; g < QG; ++g) {
-      if (q0 + g >= nquads) break;
+      if (q0 + g >= qend) break;
       f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int lv = 0; lv < LPQ; ++lv) {

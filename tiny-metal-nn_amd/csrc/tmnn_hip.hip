@@ -802,7 +802,15 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *per
       e.pos_out = nullptr;
     }
   }
-  const dim3 grid((e.n_pad + kEncodeThreads - 1) / kEncodeThreads, by_level ? e.L : 1);
+  // point-major: a batch of fewer blocks than one full round (four per CU)
+  // splits each point's feature quads over up to 4 * KT0 threads
+  const uint32_t bx = static_cast<uint32_t>((e.n_pad + kEncodeThreads - 1) / kEncodeThreads);
+  uint32_t split = 1;
+  if (!by_level)
+    while (split < static_cast<uint32_t>(4 * e.KT0) &&
+           bx * split < static_cast<uint32_t>(tr->ctx->cu_count) * 4u)
+      split *= 2;
+  const dim3 grid(bx, by_level ? static_cast<uint32_t>(e.L) : split);
 #define TMNN_ENCODE(d, f)                                                                     \
   if (by_level)                                                                               \
     hipLaunchKernelGGL((encode_level_kernel<d, f>), grid, dim3(kEncodeThreads), 0, st, e);    \
