@@ -120,11 +120,12 @@ def kernel_rooflines(prof: dict, fused_scatter: bool = False, models: dict | Non
                      names: dict | None = None, n: int = B_TRAIN) -> list[dict]:
     """Per-kernel roofline fractions from the sampled phase durations. With
     the scatter fused into the MLP kernel, that kernel carries both the MLP's
-    FLOPs (bound "mfma", the headline figure) and the hash backward's bytes
-    ("fused_scatter": HBM rate of those bytes, and the fraction the kernel's
-    duration leaves of the roofline time max(FLOPs / MFMA peak, bytes / HBM
-    peak)); there is no separate scatter kernel then. models / names / n
-    default to the C2 step (kernel_models(), KERNELS, B_TRAIN)."""
+    FLOPs and the hash backward's bytes; its roofline time is max(FLOPs / MFMA
+    peak, bytes / HBM peak), and the entry's bound, achieved, peak and frac
+    are those of the larger term (the HBM bytes at every BASELINE shape), with
+    the other in "mfma" (FLOP rate) and both times in "fused_scatter"; there
+    is no separate scatter kernel then. models / names / n default to the C2
+    step (kernel_models(), KERNELS, B_TRAIN)."""
     steps = max(1, prof["steps"])
     models = models or kernel_models()
     out = []
@@ -157,6 +158,12 @@ def kernel_rooflines(prof: dict, fused_scatter: bool = False, models: dict | Non
                 "peak_GBps": HBM_PEAK_GBS, "t_mfma_us": round(t_mfma, 2),
                 "t_hbm_us": round(t_hbm, 2),
                 "frac_of_roofline_time": round(max(t_mfma, t_hbm) / us, 4)}
+            if t_hbm > t_mfma:  # the bytes bound the kernel: report them up front
+                r["mfma"] = {k: r[k] for k in ("achieved", "peak", "unit", "frac")}
+                gbs = sb / (us * 1e-6) / 1e9
+                r.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                          "work_per_launch": sb, "flops_per_launch": work})
         out.append(r)
     return out
 
