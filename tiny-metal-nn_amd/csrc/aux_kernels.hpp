@@ -192,6 +192,12 @@ __device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j) {
   load_vec<F>(a.params + static_cast<size_t>(j) * F, w);
   load_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
   load_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
+  // an accumulator that is already zero needs no clearing store (once
+  // training converges most contributions truncate to 0: the stores were a
+  // seventh of the pass's traffic)
+  bool any = false;
+#pragma unroll
+  for (int f = 0; f < F; ++f) any = any || gi[f] != 0;
   // F == 2 entries accumulate as one packed 64-bit sum (scatter_kernel.hpp)
   if constexpr (F == 2) gi[1] = unpack_hi(gi[0], gi[1]);
 #pragma unroll
@@ -202,7 +208,7 @@ __device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j) {
   store_vec<F>(a.params + static_cast<size_t>(j) * F, w);
   store_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
   store_vec<F>(a.v + static_cast<size_t>(j) * F, ve);
-  if (a.clear_grads) {
+  if (a.clear_grads && any) {
     int32_t z[F];
 #pragma unroll
     for (int f = 0; f < F; ++f) z[f] = 0;
