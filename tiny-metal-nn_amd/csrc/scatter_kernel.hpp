@@ -57,6 +57,24 @@ constexpr int kMergeMinLanes = 8;
 // atomic_fetch_or marks the same set: all F floats of a visited corner).
 __device__ __forceinline__ void mark_entry(uint8_t *mask, size_t entry) { mask[entry] = 1; }
 
+// Visit flags are stored through a raw buffer resource over the flag array
+// (num_records = L * T bytes): the entry index is the store's 32-bit offset
+// (no 64-bit address arithmetic), and a lane with nothing to mark passes
+// kNoEntry, an offset past num_records, whose store the buffer range check
+// drops (no branch around the store). Flag arrays hold at most 32 levels of
+// 2^24 entries (the planner's limits), below 2^31.
+constexpr uint32_t kNoEntry = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t flag_rsrc(uint8_t *mask, int L, uint32_t log2T) {
+  // dword 3: 32-bit data format, the raw-buffer setting of gfx9 parts
+  return __builtin_amdgcn_make_buffer_rsrc(mask, 0, static_cast<int>(static_cast<uint32_t>(L) << log2T),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ void mark_flag(__amdgpu_buffer_rsrc_t r, uint32_t entry) {
+  __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(1), r, static_cast<int>(entry), 0, 0);
+}
+
 // feature 1 of a packed F == 2 gradient entry (see the file comment)
 __host__ __device__ __forceinline__ int32_t unpack_hi(int32_t lo, int32_t hi) {
   return static_cast<int32_t>(static_cast<uint32_t>(hi) + (lo < 0 ? 1u : 0u));
@@ -131,21 +149,31 @@ __device__ __forceinline__ bool grads_vanish(const float *d) {
 
 // A level whose contributions all truncate to 0 in every lane of the wave
 // (the common case once training converges: |d| ~ 1/N): only the visit flags
-// of its corners are stored, one per valid lane and corner, the same entries
-// the full path marks.
-template <int D>
+// of its corners are stored, the same entries the full path marks. Corners x
+// and x + 1 differ only in the low bits the carry of x + 1 flips (x has
+// multiplier 1 in the hash), so their flag bytes share a line unless x ends
+// in seven 1 bits: a v_permlane32_swap gives each store instruction both
+// x-corners of 32 points (lanes 0-31 corner x, lanes 32-63 corner x + 1 of
+// the same points, then the other way round), half the line requests of one
+// instruction per corner.
+template <int D, int F>
 __device__ __forceinline__ void mark_level(const ScatterArgs &a, int l, const float *p,
                                            bool valid) {
-  if (!valid) return;
   const Cell<D> c = cell_of<D>(p, a.res[l]);
   const uint32_t tmask = (1u << a.log2T) - 1u;
-  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+  const uint32_t lbase = static_cast<uint32_t>(l) << a.log2T;
+  const __amdgpu_buffer_rsrc_t flags = flag_rsrc(a.mask, a.IN / F, a.log2T);
 #pragma unroll
-  for (int k = 0; k < (1 << D); ++k) {
+  for (int m = 0; m < (1 << (D - 1)); ++m) {
     int co[D];
     float wc[D];
-    corner_of<D>(c, k, co, wc);
-    mark_entry(a.mask, lbase + hash_corner<D>(co, tmask));
+    corner_of<D>(c, 2 * m, co, wc);
+    const uint32_t e0 = valid ? lbase + hash_corner<D>(co, tmask) : kNoEntry;
+    co[0] += 1;
+    const uint32_t e1 = valid ? lbase + hash_corner<D>(co, tmask) : kNoEntry;
+    const auto r = __builtin_amdgcn_permlane32_swap(e0, e1, false, false);
+    mark_flag(flags, r[0]);
+    mark_flag(flags, r[1]);
   }
 }
 
@@ -215,7 +243,7 @@ template <int D, int F>
 __device__ __forceinline__ void scatter_point_level(const ScatterArgs &a, int l, const float *p,
                                                     const float *d, bool valid, int lane) {
   if (__all(!valid || grads_vanish<F>(d)))
-    mark_level<D>(a, l, p, valid);
+    mark_level<D, F>(a, l, p, valid);
   else if (__all(grads_fit<F>(d)))
     scatter_level<D, F, true>(a, l, p, d, valid, lane);
   else

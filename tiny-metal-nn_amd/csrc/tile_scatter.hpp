@@ -34,24 +34,6 @@ __host__ __device__ constexpr bool tile_scatter_shape(int D, int F) {
   return F == 2 && (D == 2 || D == 3);
 }
 
-// Visit flags are stored through a raw buffer resource over the flag array
-// (num_records = L * T bytes): the entry index is the store's 32-bit offset
-// (no 64-bit address arithmetic), and a lane with nothing to mark passes
-// kNoEntry, an offset past num_records, whose store the buffer range check
-// drops (no branch around the store). Flag arrays of the fused shapes are at
-// most 32 levels of 2^20 entries (8 MB slices at F = 2), far below 2^31.
-constexpr uint32_t kNoEntry = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t flag_rsrc(uint8_t *mask, int L, uint32_t log2T) {
-  // dword 3: 32-bit data format, the raw-buffer setting of gfx9 parts
-  return __builtin_amdgcn_make_buffer_rsrc(mask, 0, static_cast<int>(static_cast<uint32_t>(L) << log2T),
-                                           0x00020000);
-}
-
-__device__ __forceinline__ void mark_flag(__amdgpu_buffer_rsrc_t r, uint32_t entry) {
-  __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(1), r, static_cast<int>(entry), 0, 0);
-}
-
 // dx: the tile's input-feature gradients (fp32, still carrying the loss
 // scale); pos: the lane's point positions per column tile (sorted order);
 // res: the per-level resolution table (the LDS image's copy).
