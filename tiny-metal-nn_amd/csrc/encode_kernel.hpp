@@ -33,6 +33,8 @@
 
 namespace tmnn_hip {
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 struct EncodeArgs {
   int32_t n;       // points
   int32_t n_pad;   // n rounded up to whole 32-point tiles
@@ -152,7 +154,9 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_level_kernel(EncodeArgs
   constexpr int C = 1 << D;  // corners per level
   const int l = blockIdx.y;
   const int i = blockIdx.x * kEncodeThreads + threadIdx.x;
-  if (i >= a.n_pad) return;
+  // every lane of a wave takes part in the lane swaps below: threads past the
+  // padded batch gather for position 0 and store nothing
+  const bool live = i < a.n_pad;
   const bool valid = i < a.n;
   float p[D];
   const size_t src = valid ? (a.perm ? a.perm[i] : static_cast<uint32_t>(i)) : 0u;
@@ -163,24 +167,50 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_level_kernel(EncodeArgs
     for (int k = 0; k < D; ++k) a.pos_out[static_cast<size_t>(i) * D + k] = p[k];
   const uint32_t tmask = (1u << a.log2T) - 1u;
   const Cell<D> c = cell_of<D>(p, a.res[l]);
-  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+  const float *lt = a.table + (static_cast<size_t>(l) << a.log2T) * F;
+  // Corners x and x + 1 (k = 2m, 2m + 1) are neighbouring entries unless x
+  // ends in seven 1 bits, so mostly one line. A v_permlane32_swap of their
+  // entry indices lets one load instruction fetch both x-corners of 32 points
+  // (lanes 0-31 corner x, lanes 32-63 corner x + 1 of the same points, then
+  // the other 32 points): half the distinct lines per instruction. A second
+  // swap of the loaded values returns each lane its own corners. The values
+  // are swapped as the integers they were loaded as: with float operands
+  // bit-cast to integers the compiler (ROCm 7.2) used the swap's first result
+  // for both.
   float v[C][F];
 #pragma unroll
-  for (int k = 0; k < C; ++k) {
+  for (int m = 0; m < C / 2; ++m) {
     int co[D];
     float wc[D];
-    corner_of<D>(c, k, co, wc);
-    const float *e = a.table + (lbase + hash_corner<D>(co, tmask)) * F;
-    if constexpr (F == 1) {
-      v[k][0] = e[0];
-    } else if constexpr (F == 2) {
-      const f32x2 t = *reinterpret_cast<const f32x2 *>(e);
-      v[k][0] = t[0];
-      v[k][1] = t[1];
-    } else {
-      const f32x4 t = *reinterpret_cast<const f32x4 *>(e);
+    corner_of<D>(c, 2 * m, co, wc);
+    const uint32_t e0 = hash_corner<D>(co, tmask);
+    co[0] += 1;
+    const uint32_t e1 = hash_corner<D>(co, tmask);
+    const auto r = __builtin_amdgcn_permlane32_swap(e0, e1, false, false);
+    uint32_t t[2][F];
 #pragma unroll
-      for (int f = 0; f < 4; ++f) v[k][f] = t[f];
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t *e = reinterpret_cast<const uint32_t *>(lt) + static_cast<size_t>(r[h]) * F;
+      if constexpr (F == 1) {
+        t[h][0] = e[0];
+      } else if constexpr (F == 2) {
+        const u32x2 x = *reinterpret_cast<const u32x2 *>(e);
+        t[h][0] = x[0];
+        t[h][1] = x[1];
+      } else {
+        const uint4 x = *reinterpret_cast<const uint4 *>(e);
+        t[h][0] = x.x;
+        t[h][1] = x.y;
+        t[h][2] = x.z;
+        t[h][3] = x.w;
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      const auto b = __builtin_amdgcn_permlane32_swap(t[0][f], t[1][f], false, false);
+      const uint32_t lo = b[0], hi = b[1];
+      v[2 * m][f] = __builtin_bit_cast(float, lo);
+      v[2 * m + 1][f] = __builtin_bit_cast(float, hi);
     }
   }
   float feat[F];
@@ -195,6 +225,7 @@ __global__ void __launch_bounds__(kEncodeThreads) encode_level_kernel(EncodeArgs
 #pragma unroll
     for (int f = 0; f < F; ++f) feat[f] = feat[f] + w * v[k][f];
   }
+  if (!live) return;
   const int f0 = l * F;  // the level's first feature
   float *dst = a.xfeat + xtile_offset(i, f0 / 4, a.KT0) + f0 % 4;
   if constexpr (F == 4) {
