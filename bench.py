@@ -79,7 +79,7 @@ def kernel_models(d: int = 2, levels: int = 16, feats: int = 2, n_out: int = 3,
                   inp: int = 32, hidden: int = 64, n_hidden: int = 2,
                   hash_params: int = 16 << 16, mlp_params: int = 6467) -> dict:
     """Algorithmic work of one step's kernels (per point, or per step for
-    Adam), as stated in DESIGN.md:
+    Adam):
       encode   -- position read, 2^D corner gathers of every level (fp32
                   features), the X tile write (fp32, padded input width);
       mlp      -- 3 x the forward FLOPs 2 * sum(in * out) (forward, delta chain,
@@ -450,8 +450,9 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one "
-              "MI355X (the hot path runs on a single GPU; see the sharding design in "
-              "DESIGN.md)", file=sys.stderr)
+              "MI355X (the hot path runs on a single GPU: samples are data parallel, a "
+              "multi-GPU step would shard the batch and all-reduce the gradients)",
+              file=sys.stderr)
         return 2
 
     import torch
