@@ -328,7 +328,27 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 
     // ---- hidden layers NHL-1 .. 1: delta_k parked over slots [0, 8), the
     // layer input h_{k-1} (reloaded, transposed) over [8, 16); owners add
-    // dW_k / b_k; then delta_{k-1} on the staged backward fragments
+    // dW_k / b_k; then delta_{k-1} on the staged backward fragments. The
+    // reloads of h_{k-1} (and of the input features for dW_0) are issued one
+    // layer ahead, before layer k + 1's owner jobs (h_{NHL-2} here), so their
+    // latency runs under the owner products.
+    half8 hpf[HS][kNT];
+    auto load_h = [&](int k) {
+#pragma unroll
+      for (int ks = 0; ks < HS; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) hpf[ks][nt] = have ? *act_slot(k, ks, nt) : half8{};
+    };
+    f32x4 xpf[KT0][kNT];
+    auto load_x = [&]() {  // L2-resident: not kept live across the round
+#pragma unroll
+      for (int kt = 0; kt < KT0; ++kt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          xpf[kt][nt] = have ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    load_h(NHL - 2);
 #pragma unroll
     for (int k = NHL - 1; k >= 0; --k) {
       half8 b[HS][kNT];
@@ -349,8 +369,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
         for (int ks = 0; ks < HS; ++ks)
 #pragma unroll
-          for (int nt = 0; nt < kNT; ++nt)
-            hb[ks][nt] = have ? *act_slot(k - 1, ks, nt) : half8{};
+          for (int nt = 0; nt < kNT; ++nt) hb[ks][nt] = hpf[ks][nt];
         half8 hT[HT];
         transpose_tiles<HS>(hb, sel_lo, sel_hi, hT);
 #pragma unroll
@@ -360,16 +379,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
           for (int nt = 0; nt < kNT; ++nt) fac[ks][nt] = relu_keep(hb[ks][nt], ones16);
       } else {
-        // the input features again (L2-resident): not kept live across the round
-        f32x4 X0[KT0][kNT];
-#pragma unroll
-        for (int kt = 0; kt < KT0; ++kt)
-#pragma unroll
-          for (int nt = 0; nt < kNT; ++nt)
-            X0[kt][nt] = have ? xt[((static_cast<size_t>(tile) * KT0 + kt) * kNT + nt) * 64 + lane]
-                              : f32x4{0.f, 0.f, 0.f, 0.f};
+        // the input features again (prefetched by load_x)
         half8 bh[XS][kNT], bl[XS][kNT];
-        pack_split_tiles<KT0>(X0, bh, bl);
+        pack_split_tiles<KT0>(xpf, bh, bl);
         half8 xT[KT0];
         transpose_tiles<XS>(bh, sel_lo, sel_hi, xT);
 #pragma unroll
@@ -382,6 +394,10 @@ __global__ void __launch_bounds__(kWideWaves * 64)
         fetch_stage(3 * NHL - k + 1);
       else if (round + static_cast<int>(gridDim.x) < n_rounds)
         fetch_stage(kStages);
+      if (k >= 2)
+        load_h(k - 2);
+      else if (k == 1)
+        load_x();
       if (wgrads) {
         // waves outermost (not unrolled): one wave's operands live at a
         // time; every accumulator still adds the waves in order
