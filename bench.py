@@ -18,14 +18,14 @@ finish kernel (dW / loss reductions, Adam, weight image for the next step),
 on the library's HIP streams, inputs resident in HBM before the timed region
 starts.
 
-Inside the timed region the library brackets the phases of one step in
-every K/5 (five sampled steps) with timing-only HIP events on its own stream
-(`profile_every`); those sampled steps give the per-kernel durations behind
-the roofline fractions (`kernel_rooflines`, the slowest kernel is
-`roofline`) and `phase_us_per_step`. The seven events of a sampled step cost
-~12 us of stream time (measured: 0.1409 ms/step with events on every step,
-0.1286 ms without), so five samples add ~60 us to the timed region: 3 us per
-step at K = 20, 0.3 us at K = 200 (`profile_overhead_us_per_step`).
+Inside the timed region the library brackets the phases of a few sampled
+steps with timing-only HIP events on its own stream (`profile_every`: two
+sampled steps for K < 100, five from K = 100); those sampled steps give the
+per-kernel durations behind the roofline fractions (`kernel_rooflines`, the
+slowest kernel is `roofline`) and `phase_us_per_step`. The events of a
+sampled step cost ~13.4 us of stream time (measured: 107.3 us/step with
+events on every step, 93.9 us without), so the samples add 1.3 us per step
+at K = 20 and 0.3 us at K = 200 (`profile_overhead_us_per_step`).
 
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
 fp32, 2^16 points per call) and the CPU restatement of the reference math
@@ -58,7 +58,13 @@ B_TRAIN = 1 << 18
 B_INFER = 1 << 16
 IMG = 1024
 HBM_PEAK_GBS = 8000.0
-EVENT_COST_US = 12.3  # stream time of one sampled step's seven phase events (measured)
+EVENT_COST_US = 13.4  # stream time of one sampled step's phase events (measured)
+
+
+def profile_every(steps: int) -> int:
+    """Phase events on one timed step in this many: two sampled steps below
+    100 timed steps, five from 100."""
+    return max(1, steps // (2 if steps < 100 else 5))
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 C2_CONFIG = {
@@ -261,7 +267,7 @@ def run_other_workload(args, which: str) -> int:
         tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[i].data_ptr())
     tr.synchronize()
     # timed steps, phase events on one in `every` (as the C2 line)
-    every = max(1, args.steps // 5)
+    every = profile_every(args.steps)
     tr.set_training_step_profiling(True, every)
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -488,7 +494,7 @@ def main() -> int:
 
     # timed region: phase events on one step in `every` (the kernel durations),
     # the rest run exactly as a caller runs them
-    every = max(1, args.steps // 5) if args.profile_every is None else args.profile_every
+    every = profile_every(args.steps) if args.profile_every is None else args.profile_every
     tr.set_training_step_profiling(every > 0, max(every, 1))
     torch.cuda.synchronize()
     t0 = time.perf_counter()

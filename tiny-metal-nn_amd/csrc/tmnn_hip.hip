@@ -305,6 +305,10 @@ struct tmnn_trainer {
   int32_t prof_every = 0;
   uint64_t prof_seen = 0;
   std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
+  // per event set: bit k set when boundary k was recorded; a boundary with
+  // no work before it (the fused step's scatter and reduce phases) is not
+  // recorded and reads as the previous one (a zero-length phase)
+  std::vector<uint32_t> prof_recorded;
   size_t prof_used = 0;
   int prof_cur = -1;  // event set of the step being enqueued, or -1
   bool prof_suspended = false;  // allocation-free steps record no events
@@ -382,7 +386,9 @@ int prof_begin_step(tmnn_trainer *tr) {
     for (hipEvent_t &e : set)
       TMNN_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     tr->prof_events.push_back(set);
+    tr->prof_recorded.push_back(0u);
   }
+  tr->prof_recorded[tr->prof_used] = 0u;
   tr->prof_cur = static_cast<int>(tr->prof_used++);
   return TMNN_OK;
 }
@@ -391,6 +397,7 @@ int prof_begin_step(tmnn_trainer *tr) {
 int prof_mark(tmnn_trainer *tr, int k) {
   if (tr->prof_cur < 0) return TMNN_OK;
   TMNN_HIP_TRY(hipEventRecord(tr->prof_events[tr->prof_cur][k], tr->ctx->stream));
+  tr->prof_recorded[tr->prof_cur] |= 1u << k;
   return TMNN_OK;
 }
 
@@ -423,9 +430,18 @@ int prof_collect(tmnn_trainer *tr) {
   tr->infer_used = 0;
   for (size_t i = 0; i < tr->prof_used; ++i) {
     const auto &e = tr->prof_events[i];
+    // boundary k reads the last recorded boundary at or before k (boundary 0,
+    // the step's start, is always recorded)
+    int at[tmnn_trainer::kProfEvents];
+    for (int k = 0, last = 0; k < tmnn_trainer::kProfEvents; ++k) {
+      if (tr->prof_recorded[i] & (1u << k)) last = k;
+      at[k] = last;
+    }
     float ms[tmnn_trainer::kProfEvents - 1];
-    for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k)
-      TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[k], e[k + 1]));
+    for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k) {
+      ms[k] = 0.0f;
+      if (at[k] != at[k + 1]) TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[at[k]], e[at[k + 1]]));
+    }
     tr->prof_acc.gpu_sort_us += 1e3 * ms[0];
     tr->prof_acc.gpu_encode_us += 1e3 * ms[1];
     tr->prof_acc.gpu_fwd_bwd_us += 1e3 * ms[2];
@@ -1249,9 +1265,10 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   const int blocks = launch_field(tr, tr->train_plan, a, n, 2, false, a.tgt_index, sorted_pos);
   if (blocks < 0) return blocks;
   if ((rc = prof_mark(tr, 3)) != TMNN_OK) return rc;
-  if (!fused_scatter && (rc = launch_scatter(tr, indexed ? sorted_pos : pos, n)) != TMNN_OK)
-    return rc;
-  if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
+  if (!fused_scatter) {  // else the scatter phase is empty (no boundary event)
+    if ((rc = launch_scatter(tr, indexed ? sorted_pos : pos, n)) != TMNN_OK) return rc;
+    if ((rc = prof_mark(tr, 4)) != TMNN_OK) return rc;
+  }
   if (!reduce) return blocks;  // finish_step_kernel reduces the rows and the loss
   // dW rows, plus (training steps) the loss in one extra block
   const uint32_t rblocks = (tr->mlp_count + kReduceCols - 1) / kReduceCols + (d_loss ? 1 : 0);
@@ -1387,9 +1404,9 @@ int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, 
     if (overlapped) (void)sort_set_consumed(tr);
     return blocks;
   }
-  // dW reduction, loss and Adam in one kernel (the reduce phase reads ~0)
-  if ((rc = prof_mark(tr, 5)) != TMNN_OK || (rc = run_finish(tr, blocks, n, loss)) != TMNN_OK ||
-      (rc = prof_mark(tr, 6)) != TMNN_OK) {
+  // dW reduction, loss and Adam in one kernel (the reduce phase is empty: no
+  // boundary event)
+  if ((rc = run_finish(tr, blocks, n, loss)) != TMNN_OK || (rc = prof_mark(tr, 6)) != TMNN_OK) {
     prof_abort(tr);
     if (overlapped) (void)sort_set_consumed(tr);
     return rc;
