@@ -547,3 +547,35 @@ def test_hash_rate_reference_kernels_leave_the_trainer_alone():
         assert np.array_equal(hw, hw2) and np.array_equal(mw, mw2)
         assert np.array_equal(gh, gh2) and np.array_equal(gm, gm2)
         assert np.array_equal(mask, tr.debug_active_mask())
+
+
+def test_fused_step_profile_phases():
+    """Phase events of the fused device step at the C2 shape (hash-grid
+    backward inside the MLP kernel, reduction inside the finish kernel): the
+    scatter and reduce phases have no work and no boundary events, so they
+    read exactly 0; every other phase is positive and the phases add up to
+    the step total."""
+    torch = pytest.importorskip("torch")
+    _say("fused step profile phases")
+    d, enc, net, m_out, loss = BASELINE["c2"]
+    n = 1 << 14
+    with make_trainer(d, m_out, enc, net, loss=loss, precision="fp16", batch=n) as tr:
+        assert tr.inspect_runtime()["train_fused_scatter"] == 1
+        x = torch.rand(n, d, device="cuda:0")
+        y = torch.rand(n, m_out, device="cuda:0")
+        torch.cuda.synchronize()
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), n)
+        tr.synchronize()
+        tr.set_training_step_profiling(True, 1)
+        for _ in range(3):
+            tr.training_step_device(x.data_ptr(), y.data_ptr(), n)
+        tr.synchronize()
+        prof = tr.training_step_profile()
+        tr.set_training_step_profiling(False)
+        assert prof["steps"] == 3, prof
+        assert prof["gpu_scatter_us"] == 0.0 and prof["gpu_reduce_us"] == 0.0, prof
+        for k in ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_adam_us"):
+            assert prof[k] > 0.0, (k, prof)
+        parts = sum(prof[k] for k in ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us",
+                                      "gpu_scatter_us", "gpu_reduce_us", "gpu_adam_us"))
+        assert abs(parts - prof["gpu_total_us"]) <= 1e-3 * prof["gpu_total_us"], prof
