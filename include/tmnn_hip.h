@@ -486,7 +486,11 @@ int tmnn_debug_encode_tiles(tmnn_trainer *tr, const float *positions, int32_t n,
  * launch (over `reps`) of a kernel that only (gather) loads every corner's F
  * floats of every level, (atomic) adds a constant with the scatter's atomic
  * per corner and level into a scratch table, (flag) stores the visit byte per
- * corner and level. Trainer state is not touched. The achievable-bandwidth
+ * corner and level. Each kernel walks the levels as the kernel it stands
+ * for does: level-major (one level's table slice at a time) for the gather
+ * when the trainer's encode is level-major (level slices over 2 MB), and for
+ * the atomic and flag kernels when its scatter is (over 8 MB); else
+ * point-major. Trainer state is not touched. The achievable-bandwidth
  * denominators of the encode and scatter; no counterpart in the reference. */
 int tmnn_debug_hash_rates(tmnn_trainer *tr, const float *d_positions, int32_t n,
                           int32_t sorted, int32_t reps, double *gather_us,

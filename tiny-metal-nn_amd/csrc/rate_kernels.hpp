@@ -98,4 +98,66 @@ __global__ void __launch_bounds__(256) hash_rate_kernel(HashRateArgs a) {
     if (valid) a.out[i] = sum;
 }
 
+// Level-major variant, for the shapes whose encode or scatter walks the
+// levels one at a time (tables over 2 MB or 8 MB per level): blockIdx.y =
+// level, one thread per point, so the resident blocks work on one level's
+// slice at a time, as encode_level_kernel and hash_scatter_level_kernel do.
+// Every lane issues its own corner operations (no lane pairing). The gather
+// sums its corners and stores only on an impossible bit pattern, so the
+// loads stay live without an output stream.
+template <int D, int F, int KIND>
+__global__ void __launch_bounds__(256) hash_rate_level_kernel(HashRateArgs a) {
+  constexpr int C = 1 << D;
+  const int l = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool valid = i < a.n;
+  const int lane = threadIdx.x & 63;
+  float p[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) p[k] = a.pos[static_cast<size_t>(valid ? i : 0) * D + k];
+  const uint32_t tmask = (1u << a.log2T) - 1u;
+  const Cell<D> c = cell_of<D>(p, a.res[l]);
+  const size_t lbase = static_cast<size_t>(l) << a.log2T;
+  float v[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    int co[D];
+    float wc[D];
+    corner_of<D>(c, k, co, wc);
+    const uint32_t local = valid ? hash_corner<D>(co, tmask) : 0xFFFFFFFFu;
+    const size_t e = lbase + (valid ? local : 0u);
+    const uint32_t prev = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(-1, static_cast<int>(local), 0x138, 0xf, 0xf, false));
+    const bool head = valid && (lane == 0 || prev != local);
+    if constexpr (KIND == kRateGather) {
+      if constexpr (F == 1) {
+        v[k] = a.table[e];
+      } else if constexpr (F == 2) {
+        const f32x2 q = *reinterpret_cast<const f32x2 *>(a.table + e * 2);
+        v[k] = q[0] + q[1];
+      } else {
+        const f32x4 q = *reinterpret_cast<const f32x4 *>(a.table + e * 4);
+        v[k] = (q[0] + q[1]) + (q[2] + q[3]);
+      }
+    } else if constexpr (KIND == kRateAtomic) {
+      if (head) {
+        if constexpr (F == 2) {
+          atomicAdd(reinterpret_cast<unsigned long long *>(a.acc + e * 2), 0x100000001ull);
+        } else {
+#pragma unroll
+          for (int f = 0; f < F; ++f) atomicAdd(a.acc + e * F + f, 1);
+        }
+      }
+    } else {
+      if (head) a.flags[e] = 1;
+    }
+  }
+  if constexpr (KIND == kRateGather) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < C; ++k) sum += v[k];
+    if (valid && __builtin_bit_cast(uint32_t, sum) == 0x7fc0beefu) a.out[i] = sum;
+  }
+}
+
 }  // namespace tmnn_hip

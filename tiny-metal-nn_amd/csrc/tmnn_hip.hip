@@ -2469,22 +2469,34 @@ int tmnn_debug_hash_rates(tmnn_trainer *tr, const float *d_positions, int32_t n,
   }
   double *dst[3] = {gather_us, atomic_us, flag_us};
   const dim3 grid((n + 255) / 256);
+  // the level-major kernels where the trainer's encode (gather) or scatter
+  // (atomic, flag) walks the levels one at a time
+  const dim3 grid_l((n + 255) / 256, static_cast<uint32_t>(tr->d.num_levels));
+  const bool lm_gather = encode_level_major(tr), lm_scatter = level_major(tr);
   hipError_t err = hipSuccess;
   for (int kind = 0; kind < 3 && err == hipSuccess; ++kind) {
+    const bool lm = kind == kRateGather ? lm_gather : lm_scatter;
     err = hipEventRecord(e0, st);
     for (int r = 0; r < reps && err == hipSuccess; ++r) {
+#define TMNN_RATE_KIND(DD, FF, KK)                                                               \
+  if (lm)                                                                                        \
+    hipLaunchKernelGGL((hash_rate_level_kernel<DD, FF, KK>), grid_l, dim3(256), 0, st, ra);      \
+  else                                                                                           \
+    hipLaunchKernelGGL((hash_rate_kernel<DD, FF, KK>), grid, dim3(256), 0, st, ra);
 #define TMNN_RATE(DD, FF)                                                                        \
   if (tr->d.spatial_dims == DD && tr->d.features_per_level == FF) {                              \
-    if (kind == kRateGather)                                                                     \
-      hipLaunchKernelGGL((hash_rate_kernel<DD, FF, kRateGather>), grid, dim3(256), 0, st, ra);   \
-    else if (kind == kRateAtomic)                                                                \
-      hipLaunchKernelGGL((hash_rate_kernel<DD, FF, kRateAtomic>), grid, dim3(256), 0, st, ra);   \
-    else                                                                                         \
-      hipLaunchKernelGGL((hash_rate_kernel<DD, FF, kRateFlag>), grid, dim3(256), 0, st, ra);     \
+    if (kind == kRateGather) {                                                                   \
+      TMNN_RATE_KIND(DD, FF, kRateGather)                                                        \
+    } else if (kind == kRateAtomic) {                                                            \
+      TMNN_RATE_KIND(DD, FF, kRateAtomic)                                                        \
+    } else {                                                                                     \
+      TMNN_RATE_KIND(DD, FF, kRateFlag)                                                          \
+    }                                                                                            \
   }
       TMNN_RATE(2, 1) TMNN_RATE(2, 2) TMNN_RATE(2, 4) TMNN_RATE(3, 1) TMNN_RATE(3, 2)
       TMNN_RATE(3, 4) TMNN_RATE(4, 1) TMNN_RATE(4, 2) TMNN_RATE(4, 4)
 #undef TMNN_RATE
+#undef TMNN_RATE_KIND
       err = hipGetLastError();
     }
     if (err == hipSuccess) err = hipEventRecord(e1, st);
