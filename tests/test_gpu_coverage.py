@@ -525,12 +525,15 @@ def _hip_to_host(host: np.ndarray, src: int, nbytes: int) -> None:
     assert rc == 0, rc
 
 
-def test_hash_rate_reference_kernels_leave_the_trainer_alone():
+@pytest.mark.parametrize("name", ["2d_f2", "3d_bigT", "4d_bigT"])
+def test_hash_rate_reference_kernels_leave_the_trainer_alone(name):
     """tmnn_debug_hash_rates (the gather / atomic / flag reference kernels)
-    returns positive per-launch times and touches no trainer state."""
+    returns positive per-launch times and touches no trainer state, with the
+    point-major kernels (2d_f2) and the level-major ones (16 MB level slices
+    of the bigT tables)."""
     torch = pytest.importorskip("torch")
-    _say("hash rates")
-    d, enc, net, m_out = GEOMS["2d_f2"]
+    _say(f"hash rates {name}")
+    d, enc, net, m_out = GEOMS[name]
     with make_trainer(d, m_out, enc, net, precision="fp16", batch=1 << 16) as tr:
         x = torch.rand(1 << 16, d, device="cuda:0")
         y = torch.rand(1 << 16, m_out, device="cuda:0")
