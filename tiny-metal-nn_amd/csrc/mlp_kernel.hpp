@@ -513,14 +513,14 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
         for (int ut = 0; ut < HT; ++ut) park(pk, hslot(k, ut), lane, dT[ut]);
       }
+      f32x4 dx[KT0][kNT];  // k == 0: the input-feature gradients
       if (k > 0) {
         mma_packed<HS, HT>(smem + s.bwd_off(k), b, dl, lane);
       } else {
-        f32x4 dx[KT0][kNT];
         mma_packed<HS, KT0>(smem + s.bwd_off(0), b, dx, lane);
         if constexpr (SD > 0) {
-          tile_scatter<SD, SF, KT0>(a, dx, P, valid,
-                                    reinterpret_cast<const float *>(smem + s.res_off), q);
+          // the hash-grid backward runs after this wave's dW_0 owner jobs
+          // (below), in the same barrier interval
         } else if (have) {
           // rows past the batch exist (the buffer is padded to whole tiles)
 #pragma unroll
@@ -586,6 +586,10 @@ __global__ void __launch_bounds__(W * 64)
           }
         }
       }
+      if constexpr (SD > 0)
+        if (k == 0)
+          tile_scatter<SD, SF, KT0>(a, dx, P, valid,
+                                    reinterpret_cast<const float *>(smem + s.res_off), q);
       __syncthreads();
     }
   }
