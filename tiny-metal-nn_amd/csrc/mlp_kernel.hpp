@@ -32,8 +32,8 @@
 // encode_features_kernel. Details that differ are of fp16 size: the ReLU
 // derivative is taken from the fp16 activation (a positive activation below
 // 2^-25 rounds to 0 and masks its delta), the bias gradients sum the fp16
-// deltas on the matrix cores (an all-ones A operand against the transposed
-// delta tiles), each layer's bias is the accumulator's initial value (added
+// deltas on the matrix cores (each wave its own tiles' column sums, the
+// waves' partials added in wave order at the end), each layer's bias is the accumulator's initial value (added
 // before the products, not after), and RelativeL2 takes its reciprocal from
 // v_rcp_f32.
 //
@@ -57,19 +57,17 @@ __host__ __device__ constexpr int mlp_waves(int INP, int NHL) {
 }
 
 // LDS plan of mlp_train_kernel (bytes): the packed weight image, the per-wave
-// loss slots, one slot of fp16 ones (the bias jobs' operand), then per wave
-// its parking slots (16 bytes per lane each): [0, KT0) input features,
+// loss slots, then per wave its parking slots (16 bytes per lane each): [0, KT0) input features,
 // KT0 + k * HT + t hidden layer k (then delta_k), KT0 + NHL * HT the output
 // gradient.
 struct MlpLds {
-  int32_t loss, ones, park, park_bytes, total;
+  int32_t loss, park, park_bytes, total;
 };
 
 __host__ __device__ __forceinline__ MlpLds mlp_lds(const FieldLayout &s, int waves) {
   MlpLds m;
   m.loss = s.dw_off;
-  m.ones = m.loss + 16 * 4;
-  m.park = m.ones + 64 * 16;
+  m.park = m.loss + 16 * 4;
   m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + 1) * 64 * 16;
   m.total = m.park + waves * m.park_bytes;
   return m;
@@ -256,10 +254,12 @@ __global__ void __launch_bounds__(W * 64)
   constexpr int KT0 = INP / 16;  // input feature tiles
   constexpr int XS = KT0 / 2;    // K steps over the input
   static_assert(HT % 2 == 0 && KT0 % 2 == 0 && NHL >= 1 && W % 4 == 0, "shape");
+  static_assert(HT <= 4, "bias_mma maps unit tile u to lanes 16 u .. 16 u + 15");
   // owned jobs (dW tiles + bias tiles) per phase, wave w owns jobs w + W j
-  constexpr int kJobsOut = HT + 1;        // dW_out tiles (units x outputs) + b_out
-  constexpr int kJobsHid = HT * HT + HT;  // dW_k tiles + b_k tiles
-  constexpr int kJobs0 = KT0 * HT + HT;   // dW_0 tiles + b_0 tiles
+  // (bias gradients: each wave's own partials, bias_mma below)
+  constexpr int kJobsOut = HT;        // dW_out tiles (units x outputs)
+  constexpr int kJobsHid = HT * HT;   // dW_k tiles
+  constexpr int kJobs0 = KT0 * HT;    // dW_0 tiles
   constexpr int kSlotsOut = (kJobsOut + W - 1) / W;
   constexpr int kSlotsHid = (kJobsHid + W - 1) / W;
   constexpr int kSlots0 = (kJobs0 + W - 1) / W;
@@ -272,9 +272,6 @@ __global__ void __launch_bounds__(W * 64)
   // parked operands of absent tiles must be finite (they meet zero deltas)
   for (int e = threadIdx.x; e < W * ml.park_bytes / 16; e += blockDim.x)
     reinterpret_cast<uint4 *>(smem + ml.park)[e] = make_uint4(0u, 0u, 0u, 0u);
-  if (threadIdx.x < 64)
-    reinterpret_cast<uint4 *>(smem + ml.ones)[threadIdx.x] =
-        make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);  // fp16 1.0 pairs
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -290,12 +287,6 @@ __global__ void __launch_bounds__(W * 64)
   auto opnd = [&](int w, int slot) {
     return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
   };
-  // wave w's slot, or the ones slot for a bias job: a select of the address,
-  // so an owner's loads and MFMAs form one branch-free run
-  auto opnd_or_ones = [&](bool ones, int w, int slot) {
-    const int off = ones ? ml.ones : ml.park + w * ml.park_bytes + slot * 64 * 16;
-    return *reinterpret_cast<const half8 *>(smem + off + lane * 16);
-  };
   half8 sel_lo, sel_hi;
   selection_fragments(p, q, sel_lo, sel_hi);
   uint32_t ones16 = 0x00010001u;  // relu_keep's operand, opaque to the compiler
@@ -304,6 +295,20 @@ __global__ void __launch_bounds__(W * 64)
   f32x4 accO[kSlotsOut];
   f32x4 accH[NHL > 1 ? NHL - 1 : 1][kSlotsHid];
   f32x4 acc0[kSlots0];
+  // bias gradient partials of this wave's tiles: lane l holds unit l of
+  // hidden layer k (biasH[k]) or output l (biasO, lanes < 16)
+  f32x4 biasH[NHL], biasO = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < NHL; ++k) biasH[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Column sums of a transposed delta tile (units along N, the tile's 32
+  // points along K) on the matrix cores: the A operand is 1 in rows
+  // 4 u .. 4 u + 3 and 0 elsewhere, so unit tile u's sums land in rows
+  // 4 u .. 4 u + 3 of the D tile, i.e. lane p + 16 u holds the sum for unit
+  // 16 u + p; one accumulator takes all four unit tiles of a layer.
+  auto bias_mma = [&](int u, half8 t, f32x4 acc) {
+    const half8 one8 = {1, 1, 1, 1, 1, 1, 1, 1}, zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16((p >> 2) == u ? one8 : zero8, t, acc, 0, 0, 0);
+  };
 #pragma unroll
   for (int j = 0; j < kSlotsOut; ++j) accO[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -470,6 +475,7 @@ __global__ void __launch_bounds__(W * 64)
       half8 gT[2];
       transpose_tiles<1>(gb, sel_lo, sel_hi, gT);
       park(pk, kGSlot, lane, gT[0]);
+      biasO = bias_mma(0, gT[0], biasO);
     }
     f32x4 dl[HT][kNT];
     mma_packed<1, HT>(smem + s.bwd_off(NHL), gb, dl, lane);
@@ -484,7 +490,7 @@ __global__ void __launch_bounds__(W * 64)
           half8 oa[W], ob[W];  // every operand requested before the first product
 #pragma unroll
           for (int w = 0; w < W; ++w) {
-            oa[w] = opnd_or_ones(job >= HT, w, hslot(NHL - 1, job));
+            oa[w] = opnd(w, hslot(NHL - 1, job));
             ob[w] = opnd(w, kGSlot);
           }
           f32x4 acc = accO[j];
@@ -512,6 +518,8 @@ __global__ void __launch_bounds__(W * 64)
         transpose_tiles<HS>(b, sel_lo, sel_hi, dT);
 #pragma unroll
         for (int ut = 0; ut < HT; ++ut) park(pk, hslot(k, ut), lane, dT[ut]);
+#pragma unroll
+        for (int ut = 0; ut < HT; ++ut) biasH[k] = bias_mma(ut, dT[ut], biasH[k]);
       }
       f32x4 dx[KT0][kNT];  // k == 0: the input-feature gradients
       if (k > 0) {
@@ -550,12 +558,11 @@ __global__ void __launch_bounds__(W * 64)
           for (int j = 0; j < kSlotsHid; ++j) {
             const int job = wave + W * j;
             if (job < kJobsHid) {
-              // job < HT*HT: dW tile (it, ut) = (job / HT, job % HT); else bias tile
-              const int it = job / HT, ut = job < HT * HT ? job % HT : job - HT * HT;
+              const int it = job / HT, ut = job % HT;  // dW tile (it, ut)
               half8 oa[W], ob[W];
 #pragma unroll
               for (int w = 0; w < W; ++w) {
-                oa[w] = opnd_or_ones(job >= HT * HT, w, hslot(k - 1, it));
+                oa[w] = opnd(w, hslot(k - 1, it));
                 ob[w] = opnd(w, hslot(k, ut));
               }
               f32x4 acc = accH[k - 1][j];
@@ -570,11 +577,11 @@ __global__ void __launch_bounds__(W * 64)
           for (int j = 0; j < kSlots0; ++j) {
             const int job = wave + W * j;
             if (job < kJobs0) {
-              const int ft = job / HT, ut = job < KT0 * HT ? job % HT : job - KT0 * HT;
+              const int ft = job / HT, ut = job % HT;
               half8 oa[W], ob[W];
 #pragma unroll
               for (int w = 0; w < W; ++w) {
-                oa[w] = opnd_or_ones(job >= KT0 * HT, w, ft);
+                oa[w] = opnd(w, ft);
                 ob[w] = opnd(w, hslot(0, ut));
               }
               f32x4 acc = acc0[j];
@@ -620,8 +627,6 @@ __global__ void __launch_bounds__(W * 64)
         const int u = 16 * job + 4 * q + r;
         if (u < H && p < M) dst[s.w_off(NHL) + u * M + p] = accO[j][r] * sc;
       }
-    } else if (job == HT && q == 0 && p < M) {
-      dst[s.b_off(NHL) + p] = accO[j][0] * sc;
     }
   }
 #pragma unroll
@@ -636,9 +641,6 @@ __global__ void __launch_bounds__(W * 64)
           const int i = 16 * it + 4 * q + r, u = 16 * ut + p;
           if (i < H && u < H) dst[s.w_off(k) + i * H + u] = accH[k - 1][j][r] * sc;
         }
-      } else if (job < kJobsHid && q == 0) {
-        const int u = 16 * (job - HT * HT) + p;
-        if (u < H) dst[s.b_off(k) + u] = accH[k - 1][j][0] * sc;
       }
     }
 #pragma unroll
@@ -651,10 +653,20 @@ __global__ void __launch_bounds__(W * 64)
         const int f = 16 * ft + 4 * q + r, u = 16 * ut + p;
         if (f < IN && u < H) dst[s.w_off(0) + f * H + u] = acc0[j][r] * sc;
       }
-    } else if (job < kJobs0 && q == 0) {
-      const int u = 16 * (job - KT0 * HT) + p;
-      if (u < H) dst[s.b_off(0) + u] = acc0[j][0] * sc;
     }
+  }
+  // ---- bias gradients: the waves' partials (lane l: unit l) summed in wave
+  // order through LDS (the parking slots are free after the last round)
+  float *bred = reinterpret_cast<float *>(smem + ml.park);
+#pragma unroll
+  for (int k = 0; k < NHL; ++k) bred[(wave * (NHL + 1) + k) * 64 + lane] = biasH[k][0];
+  bred[(wave * (NHL + 1) + NHL) * 64 + lane] = biasO[0];
+  __syncthreads();
+  for (int e = threadIdx.x; e < (NHL + 1) * 64; e += blockDim.x) {
+    const int k = e / 64, u = e % 64;
+    float t = 0.0f;
+    for (int w = 0; w < W; ++w) t += bred[(w * (NHL + 1) + k) * 64 + u];
+    if (u < (k == NHL ? M : H)) dst[s.b_off(k) + u] = t * sc;
   }
 }
 
