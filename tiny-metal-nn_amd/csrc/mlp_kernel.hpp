@@ -23,8 +23,12 @@
 // all eight waves' points, in wave order, in registers that live across all
 // rounds. Each dW element has exactly one owner (deterministic sums, no
 // cross-wave reduction); the owners write the block's partial row at the end.
-// Parking slots are reused as layers die: the output gradient, then delta_k
-// in the slots of h_k once dW_{k+1} (the last reader of h_k) is done.
+// Parking slots are reused as layers die: delta_k goes into the slots of h_k
+// once dW_{k+1} (the last reader of h_k) is done. In 8-wave blocks dW_out
+// needs no exchange: each wave accumulates it from its own parked last
+// hidden layer and its output gradient in registers (no barrier), and the
+// waves' partials are added in wave order at the end, as are the bias
+// gradients; 4-wave blocks (one job per wave) keep dW_out as owner jobs.
 //
 // Everything else follows field_body in the fp16 training configuration:
 // split-fp16 forward (hi/lo operands, three MFMAs per product), fp16 backward
@@ -58,8 +62,8 @@ __host__ __device__ constexpr int mlp_waves(int INP, int NHL) {
 
 // LDS plan of mlp_train_kernel (bytes): the packed weight image, the per-wave
 // loss slots, then per wave its parking slots (16 bytes per lane each): [0, KT0) input features,
-// KT0 + k * HT + t hidden layer k (then delta_k), KT0 + NHL * HT the output
-// gradient.
+// KT0 + k * HT + t hidden layer k (then delta_k), and in 4-wave blocks
+// KT0 + NHL * HT the output gradient.
 struct MlpLds {
   int32_t loss, park, park_bytes, total;
 };
@@ -68,7 +72,7 @@ __host__ __device__ __forceinline__ MlpLds mlp_lds(const FieldLayout &s, int wav
   MlpLds m;
   m.loss = s.dw_off;
   m.park = m.loss + 16 * 4;
-  m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + 1) * 64 * 16;
+  m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + (waves == 8 ? 0 : 1)) * 64 * 16;
   m.total = m.park + waves * m.park_bytes;
   return m;
 }
@@ -257,10 +261,8 @@ __global__ void __launch_bounds__(W * 64)
   static_assert(HT <= 4, "bias_mma maps unit tile u to lanes 16 u .. 16 u + 15");
   // owned jobs (dW tiles + bias tiles) per phase, wave w owns jobs w + W j
   // (bias gradients: each wave's own partials, bias_mma below)
-  constexpr int kJobsOut = HT;        // dW_out tiles (units x outputs)
   constexpr int kJobsHid = HT * HT;   // dW_k tiles
   constexpr int kJobs0 = KT0 * HT;    // dW_0 tiles
-  constexpr int kSlotsOut = (kJobsOut + W - 1) / W;
   constexpr int kSlotsHid = (kJobsHid + W - 1) / W;
   constexpr int kSlots0 = (kJobs0 + W - 1) / W;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -282,7 +284,6 @@ __global__ void __launch_bounds__(W * 64)
   unsigned char *park0 = smem + ml.park;
   unsigned char *pk = park0 + wave * ml.park_bytes;
   auto hslot = [](int k, int it) { return KT0 + k * HT + it; };
-  constexpr int kGSlot = KT0 + NHL * HT;
   // operand of wave w's slot
   auto opnd = [&](int w, int slot) {
     return *reinterpret_cast<const half8 *>(park0 + w * ml.park_bytes + (slot * 64 + lane) * 16);
@@ -292,6 +293,13 @@ __global__ void __launch_bounds__(W * 64)
   uint32_t ones16 = 0x00010001u;  // relu_keep's operand, opaque to the compiler
   asm volatile("" : "+s"(ones16));
 
+  // dW_out (units x outputs): 8-wave blocks, this wave's tiles, unit tile u
+  // in accO[u] (lane n + 16 q: units 16 u + 4 q + r, output n), the waves'
+  // partials added in wave order at the end; 4-wave blocks, owner job
+  // wave + W j in accO[j]
+  constexpr bool kOwnOut = W == 8;
+  constexpr int kSlotsOut = kOwnOut ? HT : (HT + W - 1) / W;
+  constexpr int kGSlot = KT0 + NHL * HT;  // 4-wave blocks: the output gradient
   f32x4 accO[kSlotsOut];
   f32x4 accH[NHL > 1 ? NHL - 1 : 1][kSlotsHid];
   f32x4 acc0[kSlots0];
@@ -310,7 +318,7 @@ __global__ void __launch_bounds__(W * 64)
     return __builtin_amdgcn_mfma_f32_16x16x32_f16((p >> 2) == u ? one8 : zero8, t, acc, 0, 0, 0);
   };
 #pragma unroll
-  for (int j = 0; j < kSlotsOut; ++j) accO[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < kSlotsOut; ++u) accO[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int k = 0; k < (NHL > 1 ? NHL - 1 : 1); ++k)
 #pragma unroll
@@ -474,34 +482,47 @@ __global__ void __launch_bounds__(W * 64)
     {
       half8 gT[2];
       transpose_tiles<1>(gb, sel_lo, sel_hi, gT);
-      park(pk, kGSlot, lane, gT[0]);
       biasO = bias_mma(0, gT[0], biasO);
+      // dW_out of this wave's tile, from its own parked h_{NHL-1} tiles (no
+      // other wave reads them: no barrier, and delta_{NHL-1} is parked over
+      // them below in this wave's program order)
+      if (!kOwnOut) park(pk, kGSlot, lane, gT[0]);
+      if (kOwnOut && wgrads) {
+        wave_lds_sync();
+        half8 hT[HT];
+#pragma unroll
+        for (int u = 0; u < HT; ++u) hT[u] = unpark(pk, hslot(NHL - 1, u), lane);
+#pragma unroll
+        for (int u = 0; u < HT; ++u) accO[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hT[u], gT[0], accO[u], 0, 0, 0);
+        wave_lds_sync();
+      }
     }
     f32x4 dl[HT][kNT];
     mma_packed<1, HT>(smem + s.bwd_off(NHL), gb, dl, lane);
 
-    // ---- owners: dW_out (units x outputs) and b_out over the round's points
-    __syncthreads();
-    if (wgrads) {
+    if constexpr (!kOwnOut) {  // owners: dW_out (units x outputs) over the round's points
+      __syncthreads();
+      if (wgrads) {
 #pragma unroll
-      for (int j = 0; j < kSlotsOut; ++j) {
-        const int job = wave + W * j;
-        if (job < kJobsOut) {
-          half8 oa[W], ob[W];  // every operand requested before the first product
+        for (int j = 0; j < kSlotsOut; ++j) {
+          const int job = wave + W * j;
+          if (job < HT) {
+            half8 oa[W], ob[W];  // every operand requested before the first product
 #pragma unroll
-          for (int w = 0; w < W; ++w) {
-            oa[w] = opnd(w, hslot(NHL - 1, job));
-            ob[w] = opnd(w, kGSlot);
+            for (int w = 0; w < W; ++w) {
+              oa[w] = opnd(w, hslot(NHL - 1, job));
+              ob[w] = opnd(w, kGSlot);
+            }
+            f32x4 acc = accO[j];
+#pragma unroll
+            for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
+            accO[j] = acc;
+            owner_schedule<W>();
           }
-          f32x4 acc = accO[j];
-#pragma unroll
-          for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
-          accO[j] = acc;
-          owner_schedule<W>();
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
 
     // ---- hidden layers NHL-1 .. 0: delta_k (masked, fp16) parked over h_k,
     // owners add dW_k / b_k, then delta_{k-1} (or the input-feature gradient)
@@ -619,17 +640,6 @@ __global__ void __launch_bounds__(W * 64)
   const float sc = a.inv_loss_scale;
   const int H = a.H, IN = a.IN, M = a.M;
 #pragma unroll
-  for (int j = 0; j < kSlotsOut; ++j) {
-    const int job = wave + W * j;
-    if (job < HT) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int u = 16 * job + 4 * q + r;
-        if (u < H && p < M) dst[s.w_off(NHL) + u * M + p] = accO[j][r] * sc;
-      }
-    }
-  }
-#pragma unroll
   for (int k = 1; k < NHL; ++k)
 #pragma unroll
     for (int j = 0; j < kSlotsHid; ++j) {
@@ -661,7 +671,38 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
   for (int k = 0; k < NHL; ++k) bred[(wave * (NHL + 1) + k) * 64 + lane] = biasH[k][0];
   bred[(wave * (NHL + 1) + NHL) * 64 + lane] = biasO[0];
+  // 8-wave blocks: dW_out partials after them (wave w, unit tile u, lane,
+  // item r); 4-wave blocks: the owners' tiles
+  float *ored = bred + W * (NHL + 1) * 64;
+  if constexpr (kOwnOut) {
+#pragma unroll
+    for (int u = 0; u < HT; ++u)
+      *reinterpret_cast<f32x4 *>(ored + ((wave * HT + u) * 64 + lane) * 4) = accO[u];
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSlotsOut; ++j) {
+      const int job = wave + W * j;
+      if (job < HT) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int u = 16 * job + 4 * q + r;
+          if (u < H && p < M) dst[s.w_off(NHL) + u * M + p] = accO[j][r] * sc;
+        }
+      }
+    }
+  }
   __syncthreads();
+  if constexpr (kOwnOut) {
+    for (int e = threadIdx.x; e < HP * 16; e += blockDim.x) {
+      const int i = e / 16, n = e % 16;  // unit i, output n
+      if (i < H && n < M) {
+        const int u = i / 16, qq = (i % 16) / 4, r = i % 4;
+        float t = 0.0f;
+        for (int w = 0; w < W; ++w) t += ored[((w * HT + u) * 64 + n + 16 * qq) * 4 + r];
+        dst[s.w_off(NHL) + i * M + n] = t * sc;
+      }
+    }
+  }
   for (int e = threadIdx.x; e < (NHL + 1) * 64; e += blockDim.x) {
     const int k = e / 64, u = e % 64;
     float t = 0.0f;
