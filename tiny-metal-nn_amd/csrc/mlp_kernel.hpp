@@ -63,7 +63,8 @@ __host__ __device__ constexpr int mlp_waves(int INP, int NHL) {
 // LDS plan of mlp_train_kernel (bytes): the packed weight image, the per-wave
 // loss slots, then per wave its parking slots (16 bytes per lane each): [0, KT0) input features,
 // KT0 + k * HT + t hidden layer k (then delta_k), and in 4-wave blocks
-// KT0 + NHL * HT the output gradient.
+// KT0 + NHL * HT the output gradient, in 8-wave blocks KT0 + (NHL + k) * HT + t
+// delta_k for k < NHL - 1.
 struct MlpLds {
   int32_t loss, park, park_bytes, total;
 };
@@ -72,7 +73,8 @@ __host__ __device__ __forceinline__ MlpLds mlp_lds(const FieldLayout &s, int wav
   MlpLds m;
   m.loss = s.dw_off;
   m.park = m.loss + 16 * 4;
-  m.park_bytes = (s.INP / 16 + s.NHL * (s.HP / 16) + (waves == 8 ? 0 : 1)) * 64 * 16;
+  m.park_bytes =
+      (s.INP / 16 + s.NHL * (s.HP / 16) + (waves == 8 ? (s.NHL - 1) * (s.HP / 16) : 1)) * 64 * 16;
   m.total = m.park + waves * m.park_bytes;
   return m;
 }
@@ -300,6 +302,11 @@ __global__ void __launch_bounds__(W * 64)
   constexpr bool kOwnOut = W == 8;
   constexpr int kSlotsOut = kOwnOut ? HT : (HT + W - 1) / W;
   constexpr int kGSlot = KT0 + NHL * HT;  // 4-wave blocks: the output gradient
+  // slot of unit tile ut of delta_k: over h_k in 4-wave blocks and for
+  // delta_{NHL-1}; in 8-wave blocks the other deltas follow the hidden layers
+  auto dslot = [](int k, int ut) {
+    return (!kOwnOut || k == NHL - 1) ? KT0 + k * HT + ut : KT0 + NHL * HT + k * HT + ut;
+  };
   f32x4 accO[kSlotsOut];
   f32x4 accH[NHL > 1 ? NHL - 1 : 1][kSlotsHid];
   f32x4 acc0[kSlots0];
@@ -524,8 +531,56 @@ __global__ void __launch_bounds__(W * 64)
       __syncthreads();
     }
 
-    // ---- hidden layers NHL-1 .. 0: delta_k (masked, fp16) parked over h_k,
-    // owners add dW_k / b_k, then delta_{k-1} (or the input-feature gradient)
+    // ---- hidden layers NHL-1 .. 0: delta_k (masked, fp16) parked, owners add
+    // dW_k, then delta_{k-1} (or the input-feature gradient). 4-wave blocks
+    // park delta_k over h_k once the owners of dW_{k+1} are done (a barrier
+    // per layer either side of its owner phase). 8-wave blocks park every
+    // delta without a barrier (delta_{NHL-1} over this wave's own
+    // h_{NHL-1}, which only its dW_out read; the others in slots of their
+    // own), then meet once and run all layers' owner jobs in one phase.
+    f32x4 dx[KT0][kNT];  // the input-feature gradients (k == 0)
+    auto owners = [&](int k) __attribute__((always_inline)) {
+      if (!wgrads) return;
+      if (k > 0) {
+#pragma unroll
+        for (int j = 0; j < kSlotsHid; ++j) {
+          const int job = wave + W * j;
+          if (job < kJobsHid) {
+            const int it = job / HT, ut = job % HT;  // dW tile (it, ut)
+            half8 oa[W], ob[W];
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+              oa[w] = opnd(w, hslot(k - 1, it));
+              ob[w] = opnd(w, dslot(k, ut));
+            }
+            f32x4 acc = accH[k - 1][j];
+#pragma unroll
+            for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
+            accH[k - 1][j] = acc;
+            owner_schedule<W>();
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kSlots0; ++j) {
+          const int job = wave + W * j;
+          if (job < kJobs0) {
+            const int ft = job / HT, ut = job % HT;
+            half8 oa[W], ob[W];
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+              oa[w] = opnd(w, ft);
+              ob[w] = opnd(w, dslot(0, ut));
+            }
+            f32x4 acc = acc0[j];
+#pragma unroll
+            for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
+            acc0[j] = acc;
+            owner_schedule<W>();
+          }
+        }
+      }
+    };
 #pragma unroll
     for (int k = NHL - 1; k >= 0; --k) {
       half8 b[HS][kNT];
@@ -538,11 +593,10 @@ __global__ void __launch_bounds__(W * 64)
         half8 dT[HT];
         transpose_tiles<HS>(b, sel_lo, sel_hi, dT);
 #pragma unroll
-        for (int ut = 0; ut < HT; ++ut) park(pk, hslot(k, ut), lane, dT[ut]);
+        for (int ut = 0; ut < HT; ++ut) park(pk, dslot(k, ut), lane, dT[ut]);
 #pragma unroll
         for (int ut = 0; ut < HT; ++ut) biasH[k] = bias_mma(ut, dT[ut], biasH[k]);
       }
-      f32x4 dx[KT0][kNT];  // k == 0: the input-feature gradients
       if (k > 0) {
         mma_packed<HS, HT>(smem + s.bwd_off(k), b, dl, lane);
       } else {
@@ -572,53 +626,24 @@ __global__ void __launch_bounds__(W * 64)
           }
         }
       }
-      __syncthreads();
-      if (wgrads) {
-        if (k > 0) {
-#pragma unroll
-          for (int j = 0; j < kSlotsHid; ++j) {
-            const int job = wave + W * j;
-            if (job < kJobsHid) {
-              const int it = job / HT, ut = job % HT;  // dW tile (it, ut)
-              half8 oa[W], ob[W];
-#pragma unroll
-              for (int w = 0; w < W; ++w) {
-                oa[w] = opnd(w, hslot(k - 1, it));
-                ob[w] = opnd(w, hslot(k, ut));
-              }
-              f32x4 acc = accH[k - 1][j];
-#pragma unroll
-              for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
-              accH[k - 1][j] = acc;
-              owner_schedule<W>();
-            }
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < kSlots0; ++j) {
-            const int job = wave + W * j;
-            if (job < kJobs0) {
-              const int ft = job / HT, ut = job % HT;
-              half8 oa[W], ob[W];
-#pragma unroll
-              for (int w = 0; w < W; ++w) {
-                oa[w] = opnd(w, ft);
-                ob[w] = opnd(w, hslot(0, ut));
-              }
-              f32x4 acc = acc0[j];
-#pragma unroll
-              for (int w = 0; w < W; ++w) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa[w], ob[w], acc, 0, 0, 0);
-              acc0[j] = acc;
-              owner_schedule<W>();
-            }
-          }
-        }
+      if constexpr (!kOwnOut) {
+        __syncthreads();
+        owners(k);
+        if constexpr (SD > 0)
+          if (k == 0)
+            tile_scatter<SD, SF, KT0>(a, dx, P, valid,
+                                      reinterpret_cast<const float *>(smem + s.res_off), q);
+        __syncthreads();
       }
+    }
+    if constexpr (kOwnOut) {
+      __syncthreads();  // every wave's deltas are parked
+#pragma unroll
+      for (int k = NHL - 1; k >= 0; --k) owners(k);
       if constexpr (SD > 0)
-        if (k == 0)
-          tile_scatter<SD, SF, KT0>(a, dx, P, valid,
-                                    reinterpret_cast<const float *>(smem + s.res_off), q);
-      __syncthreads();
+        tile_scatter<SD, SF, KT0>(a, dx, P, valid,
+                                  reinterpret_cast<const float *>(smem + s.res_off), q);
+      __syncthreads();  // the next round parks its operands over these slots
     }
   }
 
