@@ -18,25 +18,30 @@ finish kernel (dW / loss reductions, Adam, weight image for the next step),
 on the library's HIP streams, inputs resident in HBM before the timed region
 starts.
 
-Inside the timed region the library brackets the phases of a few sampled
-steps with timing-only HIP events on its own stream (`profile_every`: two
-sampled steps for K < 100, five from K = 100); those sampled steps give the
-per-kernel durations behind the roofline fractions (`kernel_rooflines`, the
-slowest kernel is `roofline`) and `phase_us_per_step`. The events of a
-sampled step cost ~13.4 us of stream time (measured: 107.3 us/step with
-events on every step, 93.9 us without), so the samples add 1.3 us per step
-at K = 20 and 0.3 us at K = 200 (`profile_overhead_us_per_step`).
+The timed region runs the K steps exactly as a caller runs them (no
+profiling events). After it, PROFILED_STEPS more steps run with timing-only
+HIP events around every phase of every step (tmnn_get_step_profile_samples);
+the MEDIAN of those per-step phase times is each kernel's duration behind
+`phase_us_per_step`, the roofline fractions (`kernel_rooflines`) and
+`roofline` (the MLP training kernel: max(FLOPs / fp16 MFMA peak, LDS bytes /
+LDS peak) over its duration, the LDS peak measured in the same run by
+tmnn_debug_lds_rate). The same statistic over the same kernel's dispatches
+in a rocprofv3 kernel trace of this command is what `--trace-summary`
+prints.
 
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
-fp32, 2^16 points per call) and the CPU restatement of the reference math
-timed on this host.
+fp32, 2^16 points per call), the C2 step in fp32 (the reference's own
+training precision), the other BASELINE training configs C3-C5 (training
+step and forward-only pass over the same batch, timed separately) under
+`workloads`, and the CPU restatement of the reference math timed on this
+host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5]
+       python bench.py --trace-summary KERNEL_TRACE_CSV
 
---workload c3/c4/c5 time the other BASELINE training configs (synthetic
-inputs as described in BASELINE.json; the training step and a forward-only
-pass over the same batch, timed separately) and print one JSON line for them;
-the default, c2, is the headline line above.
+--workload c3/c4/c5 print the one JSON line of that config alone; the
+default, c2, is the headline line above with every config under
+`workloads`.
 """
 from __future__ import annotations
 
@@ -58,14 +63,8 @@ B_TRAIN = 1 << 18
 B_INFER = 1 << 16
 IMG = 1024
 HBM_PEAK_GBS = 8000.0
-EVENT_COST_US = 13.4  # stream time of one sampled step's phase events (measured)
-
-
-def profile_every(steps: int) -> int:
-    """Phase events on one timed step in this many: two sampled steps below
-    100 timed steps, five from 100."""
-    return max(1, steps // (2 if steps < 100 else 5))
 MFMA_F16_PEAK_TFLOPS = 2500.0
+PROFILED_STEPS = 40  # steps after the timed region with every phase timed (medians)
 
 C2_CONFIG = {
     "encoding": {"otype": "HashGrid", "n_levels": 16, "n_features_per_level": 2,
@@ -111,65 +110,154 @@ def kernel_models(d: int = 2, levels: int = 16, feats: int = 2, n_out: int = 3,
         "scatter_fused": {"bound": "hbm", "per_point": 4 * d + corners * levels * feats * 4},
     }
 
+# ---------------------------------------------------------------- LDS model --
+# LDS bytes of the MLP training kernels, counted from their code: every LDS
+# instruction of these kernels moves 16 bytes per lane (ds_read_b128 /
+# ds_write_b128 of weight fragments, bias rows and parked operands; 1 KiB
+# per wave-wide instruction), and the width-128 kernel's direct
+# global-to-LDS weight stages write 16 bytes per lane as well. The counts are
+# per 32-point wave tile (64-wide kernel) or per 128-point block round
+# (width-128 kernel); the end-of-launch reductions (a few KB per block) and
+# the fused hash-grid backward's resolution-table reads (4 bytes per point
+# and level) are left out.
 
-KERNELS = {  # model key -> (step-profile phase, kernel name in rocprof traces)
-    "encode": ("gpu_encode_us", "encode_features_kernel<2, 2>"),
-    "mlp": ("gpu_fwd_bwd_us", "mlp_train_kernel<64, 32, 2, 8>"),
-    "scatter": ("gpu_scatter_us", "hash_scatter_kernel<2, 2>"),
-    "adam": ("gpu_adam_us", "finish_step_kernel<2>"),
-}
-# the C2 kernel when the hash-grid backward runs in its tiles (tile_scatter.hpp)
-MLP_FUSED_NAME = "mlp_train_kernel<64, 32, 2, 8, 2, 2>"
+def mlp_lds_bytes_per_tile(inp: int, nhl: int, waves: int) -> int:
+    """mlp_train_kernel<64, INP, NHL, W>: HT = 4 unit tiles, HS = 2 K steps per
+    hidden layer, KT0 = INP / 16 input tiles, XS = KT0 / 2.
+      forward A fragments, hi + lo: 2 XS HT (layer 0) + 2 HS HT per further
+        hidden layer + 2 HS (output);
+      bias rows: HT per hidden layer + 1;
+      backward A fragments: HT (output) + HS HT per further hidden layer +
+        HS KT0 (the input-feature gradient);
+      parked transposed operands: KT0 inputs + HT per hidden layer's
+        activations + HT per delta (+1 output gradient in 4-wave blocks);
+      dW_out: 8-wave blocks read their own HT parked tiles; 4-wave blocks run
+        HT owner jobs per round of W tiles, 2 W operands each: 2 HT per tile;
+      owner jobs: HT^2 dW tiles per further hidden layer and KT0 HT for dW_0,
+        each reading 2 W parked operands per round of W tiles: 2 per tile."""
+    HT, HS, KT0, XS = 4, 2, inp // 16, inp // 32
+    fwd = 2 * XS * HT + (nhl - 1) * 2 * HS * HT + 2 * HS
+    bias = nhl * HT + 1
+    bwd = HT + (nhl - 1) * HS * HT + HS * KT0
+    park = KT0 + 2 * nhl * HT + (0 if waves == 8 else 1)
+    dwout = HT if waves == 8 else 2 * HT
+    owners = (nhl - 1) * 2 * HT * HT + 2 * KT0 * HT
+    return 1024 * (fwd + bias + bwd + park + dwout + owners)
 
 
-def kernel_rooflines(prof: dict, fused_scatter: bool = False, models: dict | None = None,
-                     names: dict | None = None, n: int = B_TRAIN) -> list[dict]:
-    """Per-kernel roofline fractions from the sampled phase durations. With
-    the scatter fused into the MLP kernel, that kernel carries both the MLP's
-    FLOPs and the hash backward's bytes; its roofline time is max(FLOPs / MFMA
-    peak, bytes / HBM peak), and the entry's bound, achieved, peak and frac
-    are those of the larger term (the HBM bytes at every BASELINE shape), with
-    the other in "mfma" (FLOP rate) and both times in "fused_scatter"; there
-    is no separate scatter kernel then. models / names / n default to the C2
-    step (kernel_models(), KERNELS, B_TRAIN)."""
-    steps = max(1, prof["steps"])
-    models = models or kernel_models()
+def wide_lds_bytes_per_round(nhl: int) -> int:
+    """wide_train_kernel<NHL> (hidden width 128, 32 inputs, four waves, one
+    32-point tile each per round): HT = 8, HS = 4, KT0 = 2, XS = 1.
+    Per wave: forward hi + lo fragments 2 XS HT + 2 HS HT per further hidden
+    layer + 2 HS; bias rows HT per hidden layer + 1; backward fragments HT +
+    HS HT per further hidden layer + HS KT0; parks 1 (output gradient) + HT
+    (last hidden layer) + 2 HT per further hidden layer (delta, layer input) +
+    HT + KT0 (delta_0, inputs); owner jobs 2 W operands each: HT^2 / W per
+    further hidden layer, HT KT0 / W for dW_0, HT / W for dW_out, with the
+    bias sums' parked-tile reads (2 W per layer) and the dW_0 / dW_out
+    accumulator slots (load + store). Per block: the weight stages written
+    into LDS, the image's forward hi + lo and backward fragments."""
+    HT, HS, KT0, XS, W = 8, 4, 2, 1, 4
+    fwd = 2 * XS * HT + (nhl - 1) * 2 * HS * HT + 2 * HS
+    bias = nhl * HT + 1
+    bwd = HT + (nhl - 1) * HS * HT + HS * KT0
+    park = 1 + HT + 2 * HT * (nhl - 1) + HT + KT0
+    owners = (2 * W * (HT * HT // W) * (nhl - 1) + 2 * W * (HT * KT0 // W) + 2 * W * (HT // W)
+              + 2 * W * nhl + 2 * (HT * KT0 // W + HT // W))
+    per_wave = fwd + bias + bwd + park + owners
+    stages = 2 * 32 * 128 * 2 + (nhl - 1) * 2 * 128 * 128 * 2 + 2 * 128 * 16 * 2 \
+        + 128 * 32 * 2 + (nhl - 1) * 128 * 128 * 2 + 32 * 128 * 2
+    return 1024 * W * per_wave + stages
+
+
+def lds_bytes_per_launch(kernel: str, n: int, inp: int, nhl: int, waves: int) -> int:
+    if kernel.startswith("wide_train_kernel"):
+        return wide_lds_bytes_per_round(nhl) * ((n + 127) // 128)
+    return mlp_lds_bytes_per_tile(inp, nhl, waves) * ((n + 31) // 32)
+
+
+def median_phases(samples) -> dict:
+    """Per-phase medians of the per-step samples (rows = steps)."""
+    from tiny_metal_nn._lib import PROFILE_PHASES
+    if len(samples) == 0:
+        return {k: 0.0 for k in PROFILE_PHASES}
+    med = np.median(np.asarray(samples, np.float64), axis=0)
+    return {k: float(v) for k, v in zip(PROFILE_PHASES, med)}
+
+
+def kernel_rooflines(phase_us: dict, models: dict, names: dict, n: int, fused_scatter: bool,
+                     mlp_shape: tuple, lds_peak_gbs: float, rates: dict | None,
+                     traffic: dict | None = None, fp32: bool = False) -> list[dict]:
+    """Roofline entries of one training step's kernels from the kernels'
+    median durations (phase_us): encode and finish (Adam) against the HBM
+    peak (the encode also against its gather-only reference kernel); the MLP
+    training kernel against max(FLOPs / MFMA peak, LDS bytes / LDS peak)
+    (bound "mfma" or "lds", whichever term is larger), with the hash-grid
+    backward it runs in its tiles (fused_scatter) rated against the
+    flag-store-only reference kernel at the same shape; a separate scatter
+    kernel against its flag and atomic references. mlp_shape = (kernel's
+    input width, hidden layers, waves per block)."""
     out = []
-    for key, model in models.items():
-        if key == "scatter_fused" or (key == "scatter" and fused_scatter):
+    mfma_peak = FP32_MFMA_PEAK_TFLOPS if fp32 else MFMA_F16_PEAK_TFLOPS
+    for key, phase in (("encode", "gpu_encode_us"), ("mlp", "gpu_fwd_bwd_us"),
+                       ("scatter", "gpu_scatter_us"), ("adam", "gpu_adam_us")):
+        if key == "scatter" and fused_scatter:
             continue
-        phase, name = KERNELS[key]
-        if names:
-            name = names[key]
-        elif key == "mlp" and fused_scatter:
-            name = MLP_FUSED_NAME
-        us = prof[phase] / steps
+        us = phase_us[phase]
+        if us <= 0:
+            continue
+        model = models[key]
         work = model.get("per_point", 0) * n + model.get("per_step", 0)
-        if model["bound"] == "mfma":
-            achieved = work / (us * 1e-6) / 1e12
-            r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4)}
+        r = {"kernel": names[key], "kernel_us": round(us, 2),
+             "traffic": (traffic or {}).get(key)}
+        if key == "mlp":
+            tf = work / (us * 1e-6) / 1e12
+            t_mfma = work / (mfma_peak * 1e12) * 1e6
+            mfma = {"achieved": round(tf, 1), "peak": mfma_peak, "unit": "TFLOP/s",
+                    "frac": round(tf / mfma_peak, 4), "flops_per_launch": work,
+                    "t_us": round(t_mfma, 2)}
+            r["mfma"] = mfma
+            if fp32:  # the fp32 training kernels: no LDS model, fp32 MFMA peak
+                r.update({"bound": "mfma", "achieved": mfma["achieved"], "peak": mfma_peak,
+                          "unit": "TFLOP/s", "frac": mfma["frac"]})
+            else:
+                lb = lds_bytes_per_launch(names[key], n, *mlp_shape)
+                t_lds = lb / (lds_peak_gbs * 1e9) * 1e6
+                lgbs = lb / (us * 1e-6) / 1e9
+                r["lds"] = {"bytes_per_launch": lb, "achieved": round(lgbs, 1),
+                            "peak": round(lds_peak_gbs, 1), "unit": "GB/s",
+                            "frac": round(lgbs / lds_peak_gbs, 4), "t_us": round(t_lds, 2)}
+                if t_lds >= t_mfma:
+                    r.update({"bound": "lds", "achieved": round(lgbs, 1),
+                              "peak": round(lds_peak_gbs, 1), "unit": "GB/s",
+                              "frac": round(t_lds / us, 4)})
+                else:
+                    r.update({"bound": "mfma", "achieved": mfma["achieved"], "peak": mfma_peak,
+                              "unit": "TFLOP/s", "frac": round(t_mfma / us, 4)})
+                r["roofline_us"] = round(max(t_mfma, t_lds), 2)
+            if fused_scatter and rates:
+                sb = models["scatter_fused"]["per_point"] * n
+                t_ref = rates["flag_us"]
+                r["fused_scatter"] = {
+                    "bytes_per_launch": sb,
+                    "reference": "flag-store-only kernel at this shape (one flag store per run of "
+                                 "lanes on an entry, every corner and level; a converging batch's "
+                                 "hash-grid backward stores flags only for 90-99% of its groups)",
+                    "flag_ref_us": round(t_ref, 2), "atomic_ref_us": round(rates["atomic_us"], 2),
+                    "frac_with_scatter": round(max(r.get("roofline_us", 0.0), t_ref) / us, 4)}
         else:
-            achieved = work / (us * 1e-6) / 1e9
-            r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
-        r.update({"traffic": traffic_from_profiles(key) if not names else None, "kernel": name,
-                  "kernel_avg_us": round(us, 2), "work_per_launch": work})
-        if key == "mlp" and fused_scatter:
-            sb = models["scatter_fused"]["per_point"] * n
-            t_mfma = work / (MFMA_F16_PEAK_TFLOPS * 1e12) * 1e6
-            t_hbm = sb / (HBM_PEAK_GBS * 1e9) * 1e6
-            r["fused_scatter"] = {
-                "bytes_per_launch": sb, "achieved_GBps": round(sb / (us * 1e-6) / 1e9, 1),
-                "peak_GBps": HBM_PEAK_GBS, "t_mfma_us": round(t_mfma, 2),
-                "t_hbm_us": round(t_hbm, 2),
-                "frac_of_roofline_time": round(max(t_mfma, t_hbm) / us, 4)}
-            if t_hbm > t_mfma:  # the bytes bound the kernel: report them up front
-                r["mfma"] = {k: r[k] for k in ("achieved", "peak", "unit", "frac")}
-                gbs = sb / (us * 1e-6) / 1e9
-                r.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                          "work_per_launch": sb, "flops_per_launch": work})
+            gbs = work / (us * 1e-6) / 1e9
+            r.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "bytes_per_launch": work})
+            if rates and key == "encode":
+                r["achievable"] = {"reference": "gather-only kernel (the encode's corner loads)",
+                                   "us": round(rates["gather_us"], 2),
+                                   "frac_of_achievable": round(rates["gather_us"] / us, 4)}
+            if rates and key == "scatter":
+                r["achievable"] = {"reference": "flag-store-only and atomic-only kernels",
+                                   "flag_us": round(rates["flag_us"], 2),
+                                   "atomic_us": round(rates["atomic_us"], 2)}
         out.append(r)
     return out
 
@@ -243,101 +331,134 @@ def workload_batch(torch, which: str, n: int, gen, dev):
         tgt = torch.sin(2 * math.pi * torch.einsum("nd,ckd->nck", pos, freq) + phase[None]).sum(-1) / 4.0
     return pos.contiguous().float(), tgt.contiguous().float()
 
+def _config(d, levels, feats, log2t, base, scale, hidden, nhl, loss, n, precision):
+    return {"encoding": {"otype": "HashGrid", "n_levels": levels, "n_features_per_level": feats,
+                         "log2_hashmap_size": log2t, "base_resolution": base,
+                         "per_level_scale": scale},
+            "network": {"otype": "FullyFusedMLP", "n_neurons": hidden, "n_hidden_layers": nhl},
+            "loss": {"otype": loss},
+            "optimizer": {"otype": "Adam", "learning_rate": 1e-2, "beta1": 0.9, "beta2": 0.99,
+                          "epsilon": 1e-15},
+            "weight_init": {"seed": 42, "hash_grid_range": 1e-4}, "batch_size": n,
+            "mi355x": {"precision": precision, "hash_adam": "lazy", "morton_sort": True}}
 
-def run_other_workload(args, which: str) -> int:
-    import torch
+
+def mlp_kernel_name(which: str, fused: bool, precision: str) -> str:
+    if precision == "fp32":
+        return {"c2": "field_train_kernel<64, 32, false, 2>"}.get(which, "field_train_kernel")
+    return {"c2": "mlp_train_kernel<64, 32, 2, 8, 2, 2>" if fused else
+                  "mlp_train_kernel<64, 32, 2, 8, 0, 0>",
+            "c3": "mlp_train_kernel<64, 32, 1, 8, 3, 2>" if fused else
+                  "mlp_train_kernel<64, 32, 1, 8, 0, 0>",
+            "c4": "mlp_train_kernel<64, 64, 3, 4, 0, 0>", "c5": "wide_train_kernel<4>"}[which]
+
+
+def run_workload(torch, which: str, steps: int, warmup: int, lds_peak_gbs: float,
+                 precision: str = "fp16", batches=None, profiled: int = 10) -> dict:
+    """One BASELINE training config on device-resident synthetic batches:
+    `steps` timed training steps (no profiling events), then `profiled` steps
+    with every phase timed (medians per kernel), then forward-only passes over
+    the same batch, timed separately, and the reference-rate kernels."""
     from tiny_metal_nn import Trainer
-    d, levels, feats, log2t, base, scale, hidden, nhl, m, loss, n = OTHER_WORKLOADS[which]
+    if which == "c2":
+        d, levels, feats, log2t, base, scale, hidden, nhl, m, loss, n = (
+            2, 16, 2, 15, 16.0, 1.5, 64, 2, 3, "RelativeL2", B_TRAIN)
+    else:
+        d, levels, feats, log2t, base, scale, hidden, nhl, m, loss, n = OTHER_WORKLOADS[which]
     dev = torch.device("cuda:0")
-    cfg = {"encoding": {"otype": "HashGrid", "n_levels": levels, "n_features_per_level": feats,
-                        "log2_hashmap_size": log2t, "base_resolution": base,
-                        "per_level_scale": scale},
-           "network": {"otype": "FullyFusedMLP", "n_neurons": hidden, "n_hidden_layers": nhl},
-           "loss": {"otype": loss},
-           "optimizer": {"otype": "Adam", "learning_rate": 1e-2, "beta1": 0.9, "beta2": 0.99,
-                         "epsilon": 1e-15},
-           "weight_init": {"seed": 42}, "batch_size": n,
-           "mi355x": {"precision": "fp16", "hash_adam": "lazy", "morton_sort": True}}
-    gen = torch.Generator(device=dev).manual_seed(7)
-    batches = [workload_batch(torch, which, n, gen, dev) for _ in range(2)]
-    loss_dev = torch.zeros(args.steps + args.warmup + 1, device=dev)
+    cfg = _config(d, levels, feats, log2t, base, scale, hidden, nhl, loss, n, precision)
+    if batches is None:
+        gen = torch.Generator(device=dev).manual_seed(7)
+        batches = [workload_batch(torch, which, n, gen, dev) for _ in range(2)]
+    loss_dev = torch.zeros(steps + warmup + profiled + 1, device=dev)
     tr = Trainer.from_config(cfg, n_input=d, n_output=m)
-    for i in range(args.warmup):
-        x, y = batches[i % 2]
+    ins = tr.inspect_runtime()
+
+    def step(i):
+        x, y = batches[i % len(batches)]
         tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[i].data_ptr())
+
+    for i in range(warmup):
+        step(i)
     tr.synchronize()
-    # timed steps, phase events on one in `every` (as the C2 line)
-    every = profile_every(args.steps)
-    tr.set_training_step_profiling(True, every)
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        x, y = batches[i % 2]
-        tr.training_step_device(x.data_ptr(), y.data_ptr(), n,
-                                loss_dev[args.warmup + i].data_ptr())
+    for i in range(steps):
+        step(warmup + i)
     tr.synchronize()
     el = time.perf_counter() - t0
-    prof = tr.training_step_profile()
+    tr.set_training_step_profiling(True, 1)
+    for i in range(profiled):
+        step(warmup + steps + i)
+    samples = tr.training_step_profile_samples()
     tr.set_training_step_profiling(False)
     out = torch.empty(n, m, device=dev)
     x = batches[0][0]
     for _ in range(3):
         tr.inference_device(x.data_ptr(), out.data_ptr(), n)
     tr.synchronize()
+    fwd_iters = max(5, steps)
     t1 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(fwd_iters):
         tr.inference_device(x.data_ptr(), out.data_ptr(), n)
     tr.synchronize()
-    fwd = (time.perf_counter() - t1) / args.steps
-    # reference rates at this shape over a batch in the step's Morton order
-    rates = tr.debug_hash_rates(batches[0][0].data_ptr(), n, sorted=True, reps=5)
+    fwd = (time.perf_counter() - t1) / fwd_iters
+    rates = tr.debug_hash_rates(x.data_ptr(), n, sorted=True, reps=5)
     losses = loss_dev.cpu().numpy()
-    fused = bool(tr.inspect_runtime().get("train_fused_scatter"))
     tr.close()
-    steps_prof = max(1, prof["steps"])
+    fused = bool(ins.get("train_fused_scatter"))
     inp = 32 if levels * feats <= 32 else 64
     mlp_params = (levels * feats * hidden + hidden + (nhl - 1) * (hidden * hidden + hidden)
                   + hidden * m + m)
     models = kernel_models(d, levels, feats, m, inp, hidden, nhl, levels * feats << log2t,
                            mlp_params)
-    mlp_name = {"c3": "mlp_train_kernel<64, 32, 1, 8, 3, 2>" if fused else
-                      "mlp_train_kernel<64, 32, 1, 8, 0, 0>",
-                "c4": "mlp_train_kernel<64, 64, 3, 4, 0, 0>", "c5": "wide_train_kernel<4>"}[which]
-    names = {"encode": f"encode_level_kernel<{d}, {feats}>", "mlp": mlp_name,
-             "scatter": f"hash_scatter_level_kernel<{d}, {feats}>",
-             "adam": f"finish_step_kernel<{feats}>"}
-    per_kernel = kernel_rooflines(prof, fused, models, names, n) if prof["steps"] else []
-    attach_achievable(per_kernel, rates)
-    print(json.dumps({
-        "metric": f"train samples/s ({which}); forward-only samples/s", "value": round(n * args.steps / el, 1),
-        "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(el * 1e3 / args.steps, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16 MFMA / f32 encode+Adam / i32 hash grads",
-        "data": "synthetic (see workload_batch)",
-        "config": {"workload": which, "batch": n, "encoding": f"{d}D L{levels} F{feats} T2^{log2t}",
-                   "mlp": f"{hidden}x{nhl}->{m}", "loss": loss},
-        "forward_samples_per_s": round(n / fwd, 1), "forward_ms": round(fwd * 1e3, 4),
-        "phase_us_per_step": {k: round(prof[k] / steps_prof, 2) for k in prof if k.startswith("gpu_")},
-        "kernel_rooflines": per_kernel,
-        "loss_first_last": [round(float(losses[0]), 6),
-                            round(float(losses[args.warmup + args.steps - 1]), 6)]}), flush=True)
+    lm = which in ("c3", "c4", "c5")
+    names = {"encode": f"encode_level_kernel<{d}, {feats}>" if lm
+             else f"encode_features_kernel<{d}, {feats}>",
+             "mlp": mlp_kernel_name(which, fused, precision),
+             "scatter": f"hash_scatter_level_kernel<{d}, {feats}>" if lm
+             else f"hash_scatter_kernel<{d}, {feats}>",
+             "adam": f"finish_step_kernel<{feats}, false>"}
+    ph = median_phases(samples)
+    per_kernel = kernel_rooflines(ph, models, names, n, fused, (inp, nhl, ins["waves_per_block_train"]),
+                                  lds_peak_gbs, rates, fp32=precision == "fp32")
+    return {"workload": which, "precision": precision, "batch": n,
+            "encoding": f"{d}D L{levels} F{feats} T2^{log2t} base{base:g} x{scale:g}",
+            "mlp": f"{inp}->{hidden}x{nhl}->{m}", "loss": loss,
+            "train_samples_per_s": round(n * steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+            "steps": steps, "warmup": warmup,
+            "forward_samples_per_s": round(n / fwd, 1), "forward_ms": round(fwd * 1e3, 4),
+            "phase_us_median": {k: round(v, 2) for k, v in ph.items()},
+            "profiled_steps": int(len(samples)),
+            "kernel_rooflines": per_kernel,
+            "loss_first_last": [round(float(losses[0]), 6),
+                                round(float(losses[warmup + steps + profiled - 1]), 6)]}
+
+
+def trace_summary(path: str) -> int:
+    """Per-kernel duration statistics of a rocprofv3 kernel trace CSV
+    (--kernel-trace --output-format csv): dispatch count, mean, median, min,
+    max in microseconds, and the median over the dispatches after each
+    kernel's first 20 (the warmup steps of a bench run)."""
+    import csv
+    rows = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r.get("Kernel_Name") or r.get("KernelName") or r.get("kernel_name")
+            t0 = int(r.get("Start_Timestamp") or r.get("BeginNs") or 0)
+            t1 = int(r.get("End_Timestamp") or r.get("EndNs") or 0)
+            rows.setdefault(name, []).append((t0, (t1 - t0) / 1e3))
+    print(f"# {path}")
+    print("| kernel | dispatches | mean us | median us | min us | max us | median us after first 20 |")
+    print("|---|---|---|---|---|---|---|")
+    for name, v in sorted(rows.items(), key=lambda kv: -sum(x for _, x in kv[1])):
+        v.sort()
+        us = np.array([x for _, x in v])
+        steady = us[20:] if len(us) > 20 else us
+        short = name if len(name) < 110 else name[:107] + "..."
+        print(f"| `{short}` | {len(us)} | {us.mean():.2f} | {np.median(us):.2f} | {us.min():.2f} | "
+              f"{us.max():.2f} | {np.median(steady):.2f} |")
     return 0
 
-
-def attach_achievable(per_kernel: list, rates: dict) -> None:
-    """Adds the reference-rate kernels' times (tmnn_debug_hash_rates at the
-    trainer's shape, over the step's Morton-ordered batch, walking the levels
-    as the kernel they stand for does) to the encode and scatter entries."""
-    for r in per_kernel:
-        if r["kernel"].startswith("encode"):
-            r["achievable"] = {"reference": "gather-only kernel (the encode's corner loads)",
-                               "us": round(rates["gather_us"], 2),
-                               "frac_of_achievable": round(rates["gather_us"] / r["kernel_avg_us"], 4)}
-        elif r["kernel"].startswith("hash_scatter") or "fused_scatter" in r:
-            r["achievable"] = {"reference": "flag-store-only and atomic-only kernels (the "
-                                            "scatter's memory operations: one per run of "
-                                            "lanes on the same entry, every corner and level)",
-                               "flag_us": round(rates["flag_us"], 2),
-                               "atomic_us": round(rates["atomic_us"], 2)}
 
 
 def make_image(torch, seed: int, device):
@@ -449,7 +570,6 @@ def traffic_from_profiles(key: str) -> float | None:
                 return None
     return None
 
-
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,12 +578,16 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
-    ap.add_argument("--profile-every", type=int, default=None, metavar="K",
-                    help="phase events on one timed step in K (0: none)")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the C2-fp32 and C3-C5 entries of the default line")
+    ap.add_argument("--trace-summary", metavar="CSV", default=None,
+                    help="print per-kernel duration statistics of a rocprofv3 kernel trace")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches): the "
                          "known-size reference for FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.trace_summary:
+        return trace_summary(args.trace_summary)
     if args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
@@ -487,15 +611,27 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
-    if args.workload != "c2":
-        return run_other_workload(args, args.workload)
     dev = torch.device("cuda:0")
+    if args.workload != "c2":
+        probe = Trainer.from_config(C2_CONFIG, n_input=2, n_output=3)
+        lds_peak = probe.debug_lds_rate(10) / 1e9
+        probe.close()
+        r = run_workload(torch, args.workload, args.steps, args.warmup, lds_peak)
+        print(json.dumps({
+            "metric": f"train samples/s ({args.workload}); forward-only samples/s",
+            "value": r["train_samples_per_s"], "unit": "samples/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f16 MFMA / f32 encode+Adam / i32 hash grads",
+            "data": "synthetic (see workload_batch)", "config": {"workload": args.workload},
+            "lds_peak_GBps": round(lds_peak, 1), **r}), flush=True)
+        return 0
     img = make_image(torch, 1234, dev)
     gen = torch.Generator(device=dev).manual_seed(7)
     nb = 4
     xs = [torch.rand(B_TRAIN, 2, device=dev, generator=gen) for _ in range(nb)]
     ys = [sample_bilinear(torch, img, x) for x in xs]
-    loss_dev = torch.zeros(args.steps + args.warmup + 1, device=dev)
+    loss_dev = torch.zeros(args.steps + args.warmup + PROFILED_STEPS + 1, device=dev)
     torch.cuda.synchronize()
 
     tr = Trainer.from_config(C2_CONFIG, n_input=2, n_output=3)
@@ -512,35 +648,37 @@ def main() -> int:
     torch.cuda.synchronize()
     print(f"# warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
-    # timed region: phase events on one step in `every` (the kernel durations),
-    # the rest run exactly as a caller runs them
-    every = profile_every(args.steps) if args.profile_every is None else args.profile_every
-    tr.set_training_step_profiling(every > 0, max(every, 1))
+    # timed region: the K steps exactly as a caller runs them
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(args.warmup + i)
     tr.synchronize()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    elapsed = t1 - t0
-    prof = tr.training_step_profile()
+    elapsed = time.perf_counter() - t0
+    train_sps = B_TRAIN * args.steps / elapsed
+    # kernel durations: PROFILED_STEPS more steps with every phase timed
+    tr.set_training_step_profiling(True, 1)
+    for i in range(PROFILED_STEPS):
+        step(args.warmup + args.steps + i)
+    samples = tr.training_step_profile_samples()
     tr.set_training_step_profiling(False)
     losses = loss_dev.cpu().numpy()
     first_loss = float(losses[0])
-    last_loss = float(losses[args.warmup + args.steps - 1])
+    last_loss = float(losses[args.warmup + args.steps + PROFILED_STEPS - 1])
     if not (math.isfinite(last_loss) and last_loss < first_loss):
         print(f"bench.py: training did not progress (loss {first_loss} -> {last_loss})",
               file=sys.stderr)
         return 1
-    train_sps = B_TRAIN * args.steps / elapsed
     print(f"# timed {args.steps} steps in {elapsed * 1e3:.1f} ms; loss {first_loss:.5f} -> "
-          f"{last_loss:.5f}; profile {prof}", file=sys.stderr, flush=True)
+          f"{last_loss:.5f}", file=sys.stderr, flush=True)
 
     # reference rates at this shape over a batch in the step's Morton order:
     # gather-only (the encode's loads), atomic-only and flag-store-only (the
-    # scatter's memory operations) -- the achievable denominators
+    # scatter's memory operations) -- the achievable denominators; the LDS
+    # read rate (the MLP kernel's LDS peak)
     rates = tr.debug_hash_rates(xs[0].data_ptr(), B_TRAIN, sorted=True, reps=20)
+    lds_peak = tr.debug_lds_rate(10) / 1e9
 
     # inference on the C1 shape (same field, fp32, 2^16 points per call)
     xi = torch.rand(B_INFER, 2, device=dev, generator=gen)
@@ -550,27 +688,40 @@ def main() -> int:
     tr.synchronize()
     torch.cuda.synchronize()
     iters = max(50, args.steps)
-    # five calls of the timed loop carry an event pair around the kernel
-    tr.set_training_step_profiling(True, max(1, iters // 5))
     t2 = time.perf_counter()
     for _ in range(iters):
         tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
     tr.synchronize()
     torch.cuda.synchronize()
     infer_sps = B_INFER * iters / (time.perf_counter() - t2)
+    # five more calls with an event pair around the kernel
+    tr.set_training_step_profiling(True, 1)
+    for _ in range(5):
+        tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
     iprof = tr.training_step_profile()
     tr.set_training_step_profiling(False)
     tr.close()
     infer_roof = infer_roofline(iprof)
 
-    steps_prof = max(1, prof["steps"])
     fused = bool(ins.get("train_fused_scatter"))
-    per_kernel = kernel_rooflines(prof, fused) if prof["steps"] else []
-    attach_achievable(per_kernel, rates)
-    roofline = max(per_kernel, key=lambda r: r["kernel_avg_us"]) if per_kernel else None
-    phases = {k: round(prof[k] / steps_prof, 2) for k in
-              ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us", "gpu_reduce_us",
-               "gpu_adam_us", "gpu_total_us")}
+    ph = median_phases(samples)
+    names = {"encode": "encode_features_kernel<2, 2>", "mlp": mlp_kernel_name("c2", fused, "fp16"),
+             "scatter": "hash_scatter_kernel<2, 2>", "adam": "finish_step_kernel<2, false>"}
+    traffic = {k: traffic_from_profiles(k) for k in ("encode", "mlp", "adam")}
+    per_kernel = kernel_rooflines(ph, kernel_models(), names, B_TRAIN, fused,
+                                  (32, 2, ins["waves_per_block_train"]), lds_peak, rates, traffic)
+    roofline = next((r for r in per_kernel if r["kernel"] == names["mlp"]), None)
+    if roofline is not None:
+        roofline = dict(roofline, statistic=f"median kernel duration over {len(samples)} profiled "
+                                            "steady-state steps after the timed region")
+
+    workloads = {}
+    if not args.no_workloads:
+        for which, prec in (("c2", "fp32"), ("c3", "fp16"), ("c4", "fp16"), ("c5", "fp16")):
+            batches = [(xs[k], ys[k]) for k in range(2)] if which == "c2" else None
+            key = which + ("_fp32" if prec == "fp32" else "")
+            workloads[key] = run_workload(torch, which, 20, 5, lds_peak, prec, batches)
+            print(f"# {key}: {workloads[key]['ms_per_step']} ms/step", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
@@ -597,13 +748,13 @@ def main() -> int:
         "infer_samples_per_s": round(infer_sps, 1),
         "infer_config": "C1 (configs[0]): same field, fp32, 2^16 points per call",
         "infer_roofline": infer_roof,
-        "phase_us_per_step": phases,
-        "profile_every": every,
-        "profiled_steps": int(prof["steps"]),
-        "profile_overhead_us_per_step": round(EVENT_COST_US * prof["steps"] / args.steps, 2),
+        "phase_us_median": {k: round(v, 2) for k, v in ph.items()},
+        "profiled_steps": int(len(samples)),
+        "lds_peak_GBps": round(lds_peak, 1),
         "loss_first_last": [round(first_loss, 6), round(last_loss, 6)],
         "roofline": roofline,
         "kernel_rooflines": per_kernel,
+        "workloads": workloads,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

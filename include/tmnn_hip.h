@@ -149,12 +149,49 @@ typedef struct tmnn_network_plan {
   tmnn_device_caps capabilities;
 } tmnn_network_plan;
 
-/* Result of one fused training step: TrainingStepResult (common.h:97-110). */
+/* NumericsReport (detail/runtime_stats.h:32-40), filled on sampled steps
+ * (tmnn_set_numerics_sampling). The reductions run on the device inside the
+ * step's own kernels: the training kernel keeps the largest |output| of its
+ * points, the finish kernel (dW reduction + Adam) the gradient and update
+ * terms. */
+typedef struct tmnn_numerics_report {
+  int32_t finite_forward;     /* the step's loss is finite */
+  int32_t finite_backward;    /* every gradient is finite (hash int32 / 65536, MLP fp32) */
+  int32_t finite_update;      /* every applied update (new weight, m, v, delta) is finite;
+                                 0 whenever finite_backward is 0, as in the reference */
+  float max_abs_activation;   /* largest |network output| over the batch's points (the
+                                 reference declares the field and leaves it 0) */
+  float max_abs_gradient;     /* largest |g| over the finite gradients */
+  float max_abs_update;       /* largest |w_before - w_after| over the applied updates (lazy
+                                 hash Adam: the visited entries; the reference's probe takes
+                                 the dense candidate update of every entry) */
+  uint32_t first_bad_layer;   /* 0, as the reference */
+} tmnn_numerics_report;
+
+/* Result of one fused training step: TrainingStepResult (common.h:97-110).
+ * The caller sets struct_size. */
 typedef struct tmnn_step_result {
+  uint32_t struct_size;       /* sizeof(tmnn_step_result), set by the caller */
   float loss;                 /* sum of per-point losses / N */
   uint32_t step;              /* step counter after the update */
   uint32_t batch_n;           /* points used (after the batch cap) */
+  float grad_norm;            /* sqrt(sum of g^2) over the step's gradients (reported steps) */
+  int32_t numerics_reported;  /* 1: `numerics` holds this step's report */
+  int32_t has_numerics_anomaly; /* a reported non-finite forward, backward or update */
+  tmnn_numerics_report numerics;
 } tmnn_step_result;
+
+/* NumericsSamplingMode (runtime_policy.h:13-18), same numbering; the
+ * sampling rule of NumericsGuard::should_sample (numerics_guard.cpp:12-36)
+ * on the step counter after the update: SAMPLED reports step 1, every
+ * interval-th step, a host-pointer step whose loss is not finite, and the
+ * step after a reported anomaly; PERIODIC every interval-th step and the step
+ * after an anomaly; FULL every step; DISABLED none (only a non-finite loss of
+ * a host-pointer step is still reported, as finite_forward = 0). */
+#define TMNN_NUMERICS_SAMPLED 0
+#define TMNN_NUMERICS_PERIODIC 1
+#define TMNN_NUMERICS_FULL 2
+#define TMNN_NUMERICS_DISABLED 3
 
 /* Realized kernel geometry: TrainerRuntimeInspection (trainer.h:63-87). */
 typedef struct tmnn_inspection {
@@ -224,11 +261,45 @@ int tmnn_training_step(tmnn_trainer *tr, const float *input,
                        const float *target, int32_t n, tmnn_step_result *out);
 
 /* Device-resident variant of training_step: input/target are device
- * pointers; the step is only enqueued. If loss_out (device pointer) is
- * non-null the step's loss is written there when the step executes. */
+ * pointers; the step is only enqueued, on the trainer's stream (and its Morton
+ * sort on a second stream of the trainer). The inputs must be complete when
+ * the call is made (nothing orders the step after work the caller has
+ * enqueued elsewhere): use tmnn_training_step_device_after for inputs a
+ * caller's stream is still producing. If loss_out (device pointer) is
+ * non-null the step's loss is written there when the step executes. On
+ * sampled steps the numerics report stays on the device until
+ * tmnn_get_last_numerics. */
 int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input,
                               const float *d_target, int32_t n,
                               float *d_loss_out);
+
+/* tmnn_training_step_device ordered after a caller's event: every stream of
+ * the trainer that reads the inputs (the sort's and the step's) waits for
+ * `wait_event` (a hipEvent_t of the trainer's device, recorded by the caller
+ * after the work producing d_input / d_target; NULL: no wait) before it
+ * reads them. No counterpart in the reference, whose steps take host
+ * memory. */
+int tmnn_training_step_device_after(tmnn_trainer *tr, const float *d_input,
+                                    const float *d_target, int32_t n,
+                                    float *d_loss_out, void *wait_event);
+
+/* Records `event` (a hipEvent_t of the trainer's device) on the trainer's
+ * stream after everything enqueued so far: a caller's stream that waits for
+ * it sees the outputs of the preceding *_device calls (loss, inference
+ * outputs, updated weights). */
+int tmnn_record_event(tmnn_trainer *tr, void *event);
+
+/* Numerics sampling of the training steps (RuntimePolicy::
+ * numerics_sampling_mode / numerics_sample_interval, runtime_policy.h:
+ * 30-38): mode TMNN_NUMERICS_*, interval >= 1 (reference default SAMPLED,
+ * 128). Resets the anomaly history. */
+int tmnn_set_numerics_sampling(tmnn_trainer *tr, int32_t mode, uint32_t interval);
+
+/* The report of the last sampled step (host-pointer or device step): waits
+ * for the trainer's stream, then fills out (out->struct_size set by the
+ * caller) with that step's loss, step counter, batch size, grad_norm and
+ * numerics; numerics_reported = 0 when no step has been sampled yet. */
+int tmnn_get_last_numerics(tmnn_trainer *tr, tmnn_step_result *out);
 
 /* Bytes of the per-device scratch behind tmnn_training_step_device_noalloc. */
 #define TMNN_NOALLOC_SCRATCH_BYTES (80u << 20)
@@ -260,9 +331,14 @@ int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
  * positions [N][spatial_dims] -> output [N][num_outputs], host memory. */
 int tmnn_inference(tmnn_trainer *tr, const float *positions, float *output,
                    int32_t n);
-/* Device-pointer variant; only enqueues. */
+/* Device-pointer variant; only enqueues, on the trainer's stream (the
+ * positions must be complete when the call is made). */
 int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions,
                           float *d_output, int32_t n);
+/* tmnn_inference_device ordered after a caller's event (NULL: no wait), as
+ * tmnn_training_step_device_after. */
+int tmnn_inference_device_after(tmnn_trainer *tr, const float *d_positions,
+                                float *d_output, int32_t n, void *wait_event);
 
 /* FieldEvaluator::evaluate_with_gradient (evaluator.h:41-50;
  * default_trainer.cpp:467-620): outputs [N][num_outputs] and the Jacobian
@@ -459,6 +535,23 @@ typedef struct tmnn_step_profile {
 int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled);
 int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
 
+/* Per-step phase times (GPU microseconds) of the profiled training steps
+ * since profiling was (re-)enabled, in step order: row i holds
+ * TMNN_PROFILE_PHASES floats indexed by TMNN_PROFILE_*. *count receives the
+ * number of profiled steps; at most `capacity` rows are written (out may be
+ * NULL to query). Waits for the stream. A phase without work (the fused
+ * step's scatter and reduce phases) reads 0. */
+#define TMNN_PROFILE_SORT 0
+#define TMNN_PROFILE_ENCODE 1
+#define TMNN_PROFILE_FWD_BWD 2
+#define TMNN_PROFILE_SCATTER 3
+#define TMNN_PROFILE_REDUCE 4
+#define TMNN_PROFILE_ADAM 5
+#define TMNN_PROFILE_TOTAL 6
+#define TMNN_PROFILE_PHASES 7
+int tmnn_get_step_profile_samples(tmnn_trainer *tr, float *out, uint32_t capacity,
+                                  uint32_t *count);
+
 /* ---- inspection hooks of the path (used by the parity tests) --------------- */
 /* Encode forward only (emitHashEncodeUnified, mlp_kernel_emitter.cpp:
  * 205-360): features [N][L*F] fp32; corner_index / corner_weight (nullable)
@@ -495,6 +588,22 @@ int tmnn_debug_encode_tiles(tmnn_trainer *tr, const float *positions, int32_t n,
 int tmnn_debug_hash_rates(tmnn_trainer *tr, const float *d_positions, int32_t n,
                           int32_t sorted, int32_t reps, double *gather_us,
                           double *atomic_us, double *flag_us);
+
+/* The training kernel's forward outputs of one fused step: runs a regular
+ * training step (Adam included, the step counter advances) on host-memory
+ * input/target and also writes the network outputs the step's own training
+ * kernel computed, [N][num_outputs] in the caller's row order. result as
+ * tmnn_training_step (nullable). No counterpart in the reference (a parity
+ * read-out of its fused step's forward). */
+int tmnn_debug_step_outputs(tmnn_trainer *tr, const float *input, const float *target,
+                            int32_t n, float *outputs, tmnn_step_result *result);
+
+/* LDS read bandwidth of the context's device, bytes per second: a kernel of
+ * conflict-free 16-byte lane reads (ds_read_b128, as the MLP kernels read
+ * their weight fragments and parked operands) on every CU, `reps` timed
+ * launches. The LDS peak of the MLP kernels' roofline; no counterpart in the
+ * reference. */
+int tmnn_debug_lds_rate(tmnn_context *ctx, int32_t reps, double *bytes_per_s);
 
 /* Accumulated gradients in reference layout: int32 fixed-point hash grads
  * [L][T][F] (scale 65536) and fp32 MLP grads. Either pointer may be null. */

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
     assert set(declared_symbols()) == set(_lib.SIGNATURES)
-    assert lib.tmnn_abi_version() == 2
+    assert lib.tmnn_abi_version() == 3
 
 
 def test_desc_defaults_and_struct_size():
@@ -138,6 +138,7 @@ def test_struct_layouts_match_the_header(tmp_path):
         pytest.skip("no host C compiler")
     structs = {"tmnn_model_desc": _lib.ModelDesc, "tmnn_device_caps": _lib.DeviceCaps,
                "tmnn_network_plan": _lib.NetworkPlan, "tmnn_step_result": _lib.StepResult,
+               "tmnn_numerics_report": _lib.NumericsReport,
                "tmnn_inspection": _lib.Inspection, "tmnn_step_profile": _lib.StepProfile,
                "tmnn_buffer_view": _lib.BufferView, "tmnn_parameter_layout_t": _lib.ParameterLayout,
                "tmnn_batch_plan_t": _lib.BatchPlan, "tmnn_storage_policy_t": _lib.StoragePolicy}

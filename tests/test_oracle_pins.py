@@ -357,6 +357,125 @@ def test_adam_first_step_closed_form(oracle):
     assert b1 == np.float32(1) - np.float32(0.9) and b2 == np.float32(1) - np.float32(0.99)
 
 
+def _two_adam_steps(oracle, a, w0, gh_steps, gm_steps, mask=None):
+    """Two Adam steps of the oracle on a 1-level model with every parameter
+    starting at w0 (hash w0[0] for entries 0..3, MLP w0[1] for all MLP
+    parameters unless w0 has more entries); returns the parameters after each
+    step."""
+    m = oracle.model(3, 1, 2, 10, 4.0, 2.0, 8, 1, 1)
+    nh, nm, _ = oracle.counts(m)
+    params = np.full(nh + nm, 0.5, np.float32)
+    for i, w in enumerate(w0):
+        params[i if i < 4 else nh + i - 4] = w
+    m1, m2 = np.zeros_like(params), np.zeros_like(params)
+    out = []
+    for step, (gh_vals, gm_vals) in enumerate(zip(gh_steps, gm_steps)):
+        gh = np.zeros(nh, np.int32)
+        gh[:len(gh_vals)] = gh_vals
+        gm = np.zeros(nm, np.float32)
+        gm[:len(gm_vals)] = gm_vals
+        oracle.adam_step(m, a, step, params, m1, m2, gh, gm, mask=mask)
+        out.append((params[:4].astype(np.float64).copy(), params[nh:nh + 4].astype(np.float64).copy()))
+    return out
+
+
+def _adam2(g1, g2, lr):
+    """Hand-evaluated second Adam step from zero moments (beta 0.9 / 0.99):
+    m = 0.09 g1 + 0.1 g2, v = 0.0099 g1^2 + 0.01 g2^2, bias corrections
+    0.19 and 0.0199; returns the two steps' moves (lr * m_hat / sqrt(v_hat))."""
+    d1 = lr * np.sign(g1) if g1 != 0 else 0.0
+    m = 0.09 * g1 + 0.1 * g2
+    v = 0.0099 * g1 * g1 + 0.01 * g2 * g2
+    return d1, lr * (m / 0.19) / np.sqrt(v / 0.0199)
+
+
+def test_adam_gradient_clip_two_steps(oracle):
+    """grad_clip (adam_kernel_msl.h:81-82): clamp(g, -c, c) before the
+    moments. A first gradient above the clip and a second below it make the
+    clip visible in the second step: with c = 0.5, hash g = 5 then 0.125 and
+    MLP g = -2 then 0.25 move like 0.5 then 0.125 and -0.5 then 0.25 (and not
+    like the raw values, whose second step differs by 17% and 60%)."""
+    a = oracle.adam(0.01, 0.01, grad_clip=0.5)
+    out = _two_adam_steps(oracle, a, [], [[5 * 65536], [8192]], [[-2.0], [0.25]])
+    dh1, dh2 = _adam2(0.5, 0.125, 0.01)
+    dm1, dm2 = _adam2(-0.5, 0.25, 0.01)
+    assert out[0][0][0] == pytest.approx(0.5 - dh1, abs=2e-7)
+    assert out[1][0][0] == pytest.approx(0.5 - dh1 - dh2, abs=2e-7)
+    assert out[0][1][0] == pytest.approx(0.5 - dm1, abs=2e-7)
+    assert out[1][1][0] == pytest.approx(0.5 - dm1 - dm2, abs=2e-7)
+    _, raw2 = _adam2(5.0, 0.125, 0.01)
+    assert abs(raw2 - dh2) > 0.1 * dh2  # the clip changed the second step
+
+
+def test_adam_l1_hash_regularisation_two_steps(oracle):
+    """l1_reg (adam_kernel_msl.h:89-92): g += l1 * sign(w) on hash entries
+    only, with the sign of the weight before the step. Zero gradients, l1 =
+    0.01, lr = 0.01: w = 0.5 and -0.5 each move lr toward 0, w = 0 stays; w =
+    0.005 crosses zero in step 1 (to -0.005), so step 2 sees g = -0.01:
+    m = 0.09 * 0.01 - 0.1 * 0.01, v = 0.0099e-4 + 0.01e-4, and w ends at
+    -0.005 + 0.01 * (1e-4 / 0.19) / sqrt(1.99e-6 / 0.0199). MLP parameters get
+    no L1 term (zero gradient, zero moments: unchanged)."""
+    a = oracle.adam(0.01, 0.01, l1_reg=0.01)
+    out = _two_adam_steps(oracle, a, [0.5, -0.5, 0.0, 0.005], [[], []], [[], []])
+    h1, m1_ = out[0]
+    h2, m2_ = out[1]
+    assert h1[0] == pytest.approx(0.49, abs=1e-7) and h1[1] == pytest.approx(-0.49, abs=1e-7)
+    assert h1[2] == 0.0 and h2[2] == 0.0
+    assert h1[3] == pytest.approx(-0.005, abs=1e-8)
+    want = -0.005 + 0.01 * (1e-4 / 0.19) / np.sqrt(1.99e-6 / 0.0199)
+    assert h2[3] == pytest.approx(want, abs=2e-8)
+    assert np.all(m1_ == np.float32(0.5)) and np.all(m2_ == np.float32(0.5))
+
+
+def test_adam_l2_mlp_regularisation_two_steps(oracle):
+    """l2_reg (adam_kernel_msl.h:93-95): g += l2 * w on MLP parameters only.
+    Zero gradients, l2 = 0.1, lr = 0.01, w = 0.5: step 1 sees g = 0.05 and
+    moves lr; step 2 sees g = 0.049 (w = 0.49): m = 0.0045 + 0.0049,
+    v = 0.0099 * 0.05^2 + 0.01 * 0.049^2, w = 0.49 - 0.01 * m_hat /
+    sqrt(v_hat). Hash entries get no L2 term (unchanged)."""
+    a = oracle.adam(0.01, 0.01, l2_reg=0.1)
+    out = _two_adam_steps(oracle, a, [], [[], []], [[], []])
+    m = 0.09 * 0.05 + 0.1 * 0.049
+    v = 0.0099 * 0.05 ** 2 + 0.01 * 0.049 ** 2
+    assert out[0][1][0] == pytest.approx(0.49, abs=1e-7)
+    assert out[1][1][0] == pytest.approx(0.49 - 0.01 * (m / 0.19) / np.sqrt(v / 0.0199), abs=2e-7)
+    assert np.all(out[1][0] == np.float32(0.5))
+
+
+def test_adamw_decay_first_and_suppresses_l1_l2(oracle):
+    """weight_decay (adam_kernel_msl.h:84-88): w -= lr * wd * w before the
+    Adam move, and L1/L2 are then not applied. wd = 0.1, lr = 0.01, l1 = l2 =
+    0.1 set as well: a hash entry with g = 0.25 goes 0.5 -> 0.4995 - 0.01; an
+    MLP parameter with g = 0 only decays (0.5 -> 0.4995, no L2 move); step 2
+    decays again before its move."""
+    a = oracle.adam(0.01, 0.01, l1_reg=0.1, l2_reg=0.1, weight_decay=0.1)
+    out = _two_adam_steps(oracle, a, [], [[16384], [16384]], [[], []])
+    assert out[0][0][0] == pytest.approx(0.4995 - 0.01, abs=1e-7)
+    assert out[0][1][0] == pytest.approx(0.4995, abs=1e-7)
+    w1 = 0.4995 - 0.01
+    assert out[1][0][0] == pytest.approx(w1 * (1 - 0.001) - 0.01, abs=2e-7)
+    assert out[1][1][0] == pytest.approx(0.4995 * (1 - 0.001), abs=1e-7)
+    # a zero-gradient hash entry decays only
+    assert out[0][0][1] == pytest.approx(0.4995, abs=1e-7)
+
+
+def test_lazy_adam_branches_match_dense_on_marked_entries(oracle):
+    """The sparse hash kernel (adam_kernel_msl.h:120-164) applies clip and
+    AdamW like the unified one: on marked entries the lazy and dense updates
+    agree bit for bit."""
+    a = oracle.adam(0.01, 0.01, grad_clip=0.5, weight_decay=0.05)
+    m = oracle.model(3, 1, 2, 10, 4.0, 2.0, 8, 1, 1)
+    nh, nm, nw = oracle.counts(m)
+    mask = np.zeros(nw, np.uint32)
+    mask[0] = 0b11  # slots 0 and 1 -> elements 0..3
+    dense = _two_adam_steps(oracle, a, [0.3, -0.2, 0.1, 0.0], [[5 * 65536, -8192, 3], [8192, 1, 0]],
+                            [[], []])
+    lazy = _two_adam_steps(oracle, a, [0.3, -0.2, 0.1, 0.0], [[5 * 65536, -8192, 3], [8192, 1, 0]],
+                           [[], []], mask=mask)
+    for (hd, _), (hl, _) in zip(dense, lazy):
+        assert np.array_equal(hd, hl)
+
+
 def test_lazy_adam_updates_only_marked_entries(oracle):
     """neural_sdf_adam_hash_sparse: unmarked entries keep w, m, v; marked
     entries with g = 0 still move by their momentum."""

@@ -2,9 +2,10 @@
 against the existing device entry point (tmnn_training_step_device) through
 the C-ABI: two trainers from the same seed take the same batches, one
 through each entry point, two calls in a row (the second with a smaller
-batch); losses and every parameter agree (fp32 tolerance 1e-6 on the loss,
-1e-5 relative per tensor on the weights; the kernels are the same, so the
-results are expected bit-identical). Marked gpu."""
+batch); losses and every parameter are bit-identical (the kernels and their
+order are the same). A second case alternates the two entry points on one
+trainer, which also meets the regular step's side-stream sort sets. Marked
+gpu."""
 from __future__ import annotations
 
 import sys
@@ -55,13 +56,46 @@ def test_noalloc_step_matches_device_step(case):
             ref.synchronize()
             tr.synchronize()
             a, b = loss_ref[i].item(), loss_na[i].item()
-            assert np.isfinite(a) and b == pytest.approx(a, rel=1e-6, abs=0.0), (i, a, b)
+            assert np.isfinite(a) and a == b, (i, a, b)
             hr, mr = ref.get_weights()
             hn, mn = tr.get_weights()
-            assert rel_tensor(mn, mr) <= 1e-5 and rel_tensor(hn, hr) <= 1e-5, i
+            assert np.array_equal(mn, mr) and np.array_equal(hn, hr), (
+                i, rel_tensor(mn, mr), rel_tensor(hn, hr))
             assert tr.step() == ref.step() == i + 1
-            _say(f"  call {i} n={n}: loss {a:.6f} / {b:.6f}, bit-identical weights "
-                 f"{np.array_equal(mn, mr) and np.array_equal(hn, hr)}")
+            _say(f"  call {i} n={n}: loss {a:.6f}, weights bit-identical")
+
+
+def test_noalloc_alternating_with_regular_steps_on_one_trainer():
+    """Regular, allocation-free, regular, allocation-free steps on one trainer
+    (the regular steps sort on the side stream into their buffer sets, the
+    allocation-free ones on the main stream into the scratch, lending and
+    restoring the trainer's batch buffers) against a trainer that takes only
+    regular steps: losses and weights bit-identical after every step."""
+    torch = pytest.importorskip("torch")
+    d, enc, net, m_out = GEOMS["2d_f2"]
+    _say("noalloc alternating")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(21)
+    sizes = (20000, 8192, 20000, 3001, 12345, 20000)
+    with make_trainer(d, m_out, enc, net, precision="fp16", batch=20000, hash_range=0.1) as ref, \
+            make_trainer(d, m_out, enc, net, precision="fp16", batch=20000, hash_range=0.1) as tr:
+        for i, n in enumerate(sizes):
+            x = torch.rand(n, d, device=dev, generator=g)
+            y = torch.rand(n, m_out, device=dev, generator=g)
+            lr_, lt = torch.zeros(1, device=dev), torch.zeros(1, device=dev)
+            torch.cuda.synchronize()
+            ref.training_step_device(x.data_ptr(), y.data_ptr(), n, lr_.data_ptr())
+            if i % 2:
+                tr.training_step_device_noalloc(x.data_ptr(), y.data_ptr(), n, lt.data_ptr())
+            else:
+                tr.training_step_device(x.data_ptr(), y.data_ptr(), n, lt.data_ptr())
+            ref.synchronize()
+            tr.synchronize()
+            assert lr_.item() == lt.item(), (i, lr_.item(), lt.item())
+            hr, mr = ref.get_weights()
+            hn, mn = tr.get_weights()
+            assert np.array_equal(mn, mr) and np.array_equal(hn, hr), i
+            _say(f"  step {i} n={n} {'noalloc' if i % 2 else 'regular'}: bit-identical")
 
 
 def test_noalloc_rejects_oversize_and_wide_without_running():

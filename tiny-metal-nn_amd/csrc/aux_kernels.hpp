@@ -121,6 +121,34 @@ struct AdamArgs {
   int32_t clear_mask;       // zero mask_next (the caller then swaps the buffers)
 };
 
+// Numerics probe of a training step, per thread (NumericsReport,
+// detail/runtime_stats.h:32-40; the terms of probe_backward_numerics and
+// accumulate_update_probe_for_range, training_step_execution.cpp:238-344,
+// taken from the values the Adam pass already holds instead of a host
+// read-back of every buffer).
+struct NumAcc {
+  float gmax = 0.0f;  // largest |g| over finite raw gradients
+  float g2 = 0.0f;    // sum of g^2 over them
+  float umax = 0.0f;  // largest |w_before - w_after| over finite updates
+  uint32_t bad = 0u;  // bit 0: a non-finite gradient; bit 1: a non-finite update
+  __device__ __forceinline__ void grad(float g) {
+    if (__builtin_isfinite(g)) {
+      gmax = fmaxf(gmax, fabsf(g));
+      g2 += g * g;
+    } else {
+      bad |= 1u;
+    }
+  }
+  __device__ __forceinline__ void update(float w0, float w, float mo, float ve) {
+    const float du = w0 - w;
+    if (__builtin_isfinite(w) && __builtin_isfinite(mo) && __builtin_isfinite(ve) &&
+        __builtin_isfinite(du))
+      umax = fmaxf(umax, fabsf(du));
+    else
+      bad |= 2u;
+  }
+};
+
 // One Adam element (adam_kernel_msl.h:67-108, :137-163, :183-202).
 __device__ __forceinline__ void adam_update(float &w, float &mo, float &ve,
                                             float g, float lr, const AdamArgs &a,
@@ -175,8 +203,9 @@ __device__ __forceinline__ void store_vec(T *p, const T (&in)[F]) {
 // MLP parameter each (neural_sdf_adam_mlp_dense, adam_kernel_msl.h:166-203).
 // Adam of hash entry j (its F floats): skipped in lazy mode unless visited;
 // zeroes the entry's flag in the next step's buffer.
-template <int F>
-__device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j) {
+template <int F, bool NUM = false>
+__device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j,
+                                                NumAcc *acc = nullptr) {
   bool visited = a.mask[j] != 0;
   if (a.partner_xor) {  // lifted 2D: also visited as some corner's z = 1 partner
     const uint32_t tmask = (1u << a.log2T) - 1u;
@@ -203,7 +232,12 @@ __device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j) {
 #pragma unroll
   for (int f = 0; f < F; ++f) {
     const float g = static_cast<float>(gi[f]) * (1.0f / 65536.0f);
+    const float w0 = w[f];
     adam_update(w[f], mo[f], ve[f], g, a.lr_hash, a, false);
+    if constexpr (NUM) {
+      acc->grad(g);
+      acc->update(w0, w[f], mo[f], ve[f]);
+    }
   }
   store_vec<F>(a.params + static_cast<size_t>(j) * F, w);
   store_vec<F>(a.m + static_cast<size_t>(j) * F, mo);
@@ -217,11 +251,17 @@ __device__ __forceinline__ void adam_hash_entry(const AdamArgs &a, uint32_t j) {
 }
 
 // Adam of MLP parameter k with gradient g; returns the new weight.
-template <int F>
-__device__ __forceinline__ float adam_mlp_param(const AdamArgs &a, uint32_t k, float g) {
+template <int F, bool NUM = false>
+__device__ __forceinline__ float adam_mlp_param(const AdamArgs &a, uint32_t k, float g,
+                                                NumAcc *acc = nullptr) {
   const size_t i = static_cast<size_t>(a.hash_entries) * F + k;
   float w = a.params[i], mo = a.m[i], ve = a.v[i];
+  const float w0 = w;
   adam_update(w, mo, ve, g, a.lr_mlp, a, true);
+  if constexpr (NUM) {
+    acc->grad(g);
+    acc->update(w0, w, mo, ve);
+  }
   a.params[i] = w;
   a.m[i] = mo;
   a.v[i] = ve;

@@ -76,6 +76,7 @@ struct FieldArgs {
   _Float16 *wide_act;       // wide kernel: hidden activations [NHL-1][n_tiles][128][32] (fp16 training)
   float *grad_partials;     // [gridDim.x][mlp_count]
   float *loss_partials;     // [gridDim.x]
+  float *amax_partials;     // nullable: [gridDim.x] largest |output| of the block's points
   // training kernels with the hash-grid backward fused (tile_scatter.hpp):
   const float *spos;        // [n][D] positions in tile order
   int32_t *grad_hash;       // [L][T][F] int32 fixed point
@@ -784,15 +785,36 @@ __device__ __forceinline__ void tile_loss(const FieldArgs &a, const f32x4 (&y)[1
 // mlp_kernel_emitter.cpp:562-670) in D layout: output 4*q + r of point
 // 16*nt + p. kModeInputGrad instead writes the outputs and seeds
 // d out_{grad_output} = 1; kModeTrainExtGrad takes d_out from Tv.
+// Training modes also keep the largest |output| of the lane's points in
+// lane_amax (the numerics report's activation term), and with a.out set
+// write the outputs to row a.out_index[pt] (or pt) of a.out (the parity
+// read-out of a training step's forward).
 template <int OKT, bool FAST_RCP = false>
 __device__ __forceinline__ void output_grad(const FieldArgs &a, const f32x4 (&y)[1][kNT],
                                             const float (&Tv)[kNT][4], const bool (&valid)[kNT],
                                             const int (&pt)[kNT], int q, float &lane_loss,
-                                            f32x4 (&g)[OKT][kNT]) {
+                                            float &lane_amax, f32x4 (&g)[OKT][kNT]) {
 #pragma unroll
   for (int t = 0; t < OKT; ++t)
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) g[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (a.mode != kModeInputGrad) {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (valid[nt] && 4 * q + r < a.M) lane_amax = fmaxf(lane_amax, fabsf(y[0][nt][r]));
+    if (a.out) {  // uniform
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        if (!valid[nt]) continue;
+        const size_t row = a.out_index ? a.out_index[pt[nt]] : static_cast<uint32_t>(pt[nt]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * q + r < a.M) a.out[row * a.M + 4 * q + r] = y[0][nt][r];
+      }
+    }
+  }
   if (a.mode == kModeInputGrad) {
     // evaluator gradient pass: outputs once, then d out_m = 1
 #pragma unroll
@@ -869,6 +891,37 @@ __device__ __forceinline__ void output_grad(const FieldArgs &a, const f32x4 (&y)
         tile_loss<kLossL2, FAST_RCP>(a, y, Tv, valid, q, lane_loss, g[0][0], g[0][1]);
         break;
     }
+  }
+}
+
+// End of a training launch: the block's loss partial (each wave's lane sum,
+// then the waves in order) into a.loss_partials[blockIdx.x] and, when
+// a.amax_partials is set, the largest |output| of the block's points. lred
+// holds one float per wave in LDS; every thread of the block calls this.
+__device__ __forceinline__ void block_loss_partials(const FieldArgs &a, float lane_loss,
+                                                    float lane_amax, float *lred, int lane,
+                                                    int wave, int waves) {
+  float v = lane_loss;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  if (lane == 0) lred[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.0f;
+    for (int w = 0; w < waves; ++w) t += lred[w];
+    a.loss_partials[blockIdx.x] = t;
+  }
+  if (a.amax_partials == nullptr) return;  // uniform
+  float m = lane_amax;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  __syncthreads();
+  if (lane == 0) lred[wave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.0f;
+    for (int w = 0; w < waves; ++w) t = fmaxf(t, lred[w]);
+    a.amax_partials[blockIdx.x] = t;
   }
 }
 
@@ -1004,7 +1057,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   unsigned char *Hs = wb + s.hs_off;
   unsigned char *Ds = wb + s.ds_off;
   const int hs_layer_bytes = HP * kPS * es;
-  float lane_loss = 0.0f;
+  float lane_loss = 0.0f, lane_amax = 0.0f;
 
   DwRegs<HT, KT0, NHLT> R;
   if constexpr (REGDW) {
@@ -1175,7 +1228,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       // ---- loss / output gradient
       const bool wgrads = a.mode != kModeInputGrad;  // accumulate dW / loss
       f32x4 g[OKT][kNT];
-      output_grad<OKT>(a, y, Tv, valid, pt, q, lane_loss, g);
+      output_grad<OKT>(a, y, Tv, valid, pt, q, lane_loss, lane_amax, g);
 
       // ---- output layer backward
       wave_lds_sync();
@@ -1352,17 +1405,8 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 
   if constexpr (TRAIN) {
     if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
-    float v = lane_loss;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
-    float *lred = reinterpret_cast<float *>(smem + s.red_off);
-    if (lane == 0) lred[wave] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = 0.0f;
-      for (int w = 0; w < a.waves_per_block; ++w) t += lred[w];
-      a.loss_partials[blockIdx.x] = t;
-    }
+    block_loss_partials(a, lane_loss, lane_amax, reinterpret_cast<float *>(smem + s.red_off), lane,
+                        wave, a.waves_per_block);
     float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
     if constexpr (REGDW) {
       // every wave is past its tiles (barrier above): reduce the waves'

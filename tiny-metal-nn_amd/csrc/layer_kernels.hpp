@@ -63,6 +63,9 @@ struct LwGemmArgs {
 };
 
 constexpr int kLwTile = 64;
+// Points per chunk of a layer-wise forward pass (inference has no batch cap):
+// two activation buffers of kLwForwardChunk x H floats.
+constexpr int kLwForwardChunk = 1 << 18;
 constexpr int kLwK = 16;
 
 __device__ __forceinline__ float lw_a(const LwGemmArgs &g, int r, int k) {
@@ -176,9 +179,12 @@ struct LwLossArgs {
   const float *y;            // [n][M]
   const float *target;       // [rows][M]: targets (TrainLoss) or d_out (TrainExtGrad)
   const uint32_t *tgt_index; // nullable: point i's row is tgt_index[i]
-  float *out;                // kModeInputGrad: outputs [n][M] written here (nullable)
+  float *out;                // nullable: outputs [n][M] (kModeInputGrad: row i; training
+                             // modes: row out_index[i] or i, the parity read-out of a step)
+  const uint32_t *out_index; // nullable: caller row of point i (training modes)
   float *g;                  // [n][M] output gradients
   float *loss_partials;      // [chunks]
+  float *amax_partials;      // nullable: [chunks] largest |output| of the chunk's points
 };
 
 // Output gradient and loss of each point (emitLoss, mlp_kernel_emitter.cpp:
@@ -186,7 +192,7 @@ struct LwLossArgs {
 // sum (threads in order, then lanes) -- a fixed order.
 __global__ void __launch_bounds__(256) lw_loss_kernel(LwLossArgs a) {
   const int i0 = blockIdx.x * a.chunk, i1 = min(a.n, i0 + a.chunk);
-  float lsum = 0.0f;
+  float lsum = 0.0f, amax = 0.0f;
   for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
     const float *y = a.y + static_cast<size_t>(i) * a.M;
     float *g = a.g + static_cast<size_t>(i) * a.M;
@@ -198,6 +204,11 @@ __global__ void __launch_bounds__(256) lw_loss_kernel(LwLossArgs a) {
       continue;
     }
     const size_t row = a.tgt_index ? a.tgt_index[i] : static_cast<uint32_t>(i);
+    const size_t orow = a.out_index ? a.out_index[i] : static_cast<uint32_t>(i);
+    for (int o = 0; o < a.M; ++o) {
+      amax = fmaxf(amax, fabsf(y[o]));
+      if (a.out) a.out[orow * a.M + o] = y[o];
+    }
     const float *t = a.target + row * a.M;
     if (a.mode == kModeTrainExtGrad) {
       for (int o = 0; o < a.M; ++o) g[o] = t[o] * a.loss_scale;
@@ -244,6 +255,15 @@ __global__ void __launch_bounds__(256) lw_loss_kernel(LwLossArgs a) {
     __syncthreads();
   }
   if (threadIdx.x == 0) a.loss_partials[blockIdx.x] = red[0];
+  if (a.amax_partials == nullptr) return;
+  __syncthreads();
+  red[threadIdx.x] = amax;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (static_cast<int>(threadIdx.x) < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) a.amax_partials[blockIdx.x] = red[0];
 }
 
 }  // namespace tmnn_hip

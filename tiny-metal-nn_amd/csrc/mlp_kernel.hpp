@@ -332,7 +332,7 @@ __global__ void __launch_bounds__(W * 64)
     for (int j = 0; j < kSlotsHid; ++j) accH[k][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < kSlots0; ++j) acc0[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float lane_loss = 0.0f;
+  float lane_loss = 0.0f, lane_amax = 0.0f;
   const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
   const bool has_target = a.mode != kModeInputGrad && a.target != nullptr;
   const bool dx_vec = (a.IN & 3) == 0;
@@ -482,7 +482,7 @@ __global__ void __launch_bounds__(W * 64)
 
     // ---- loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
     f32x4 g[2][kNT];
-    output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, g);
+    output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, lane_amax, g);
     fetch_targets();
     half8 gb[1][kNT];
     pack_tiles<2>(g, gb);
@@ -648,18 +648,9 @@ __global__ void __launch_bounds__(W * 64)
   }
 
   if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
-  // ---- loss partial of the block (wave order)
-  float v = lane_loss;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
-  float *lred = reinterpret_cast<float *>(smem + ml.loss);
-  if (lane == 0) lred[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.0f;
-    for (int w = 0; w < W; ++w) t += lred[w];
-    a.loss_partials[blockIdx.x] = t;
-  }
+  // ---- loss partial (wave order) and largest |output| of the block
+  block_loss_partials(a, lane_loss, lane_amax, reinterpret_cast<float *>(smem + ml.loss), lane,
+                      wave, W);
   // ---- owners write their tiles of the block's partial row (reference layout)
   float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
   const float sc = a.inv_loss_scale;

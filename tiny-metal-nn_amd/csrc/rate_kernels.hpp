@@ -160,4 +160,40 @@ __global__ void __launch_bounds__(256) hash_rate_level_kernel(HashRateArgs a) {
   }
 }
 
+// LDS read rate (debug entry tmnn_debug_lds_rate): the LDS bandwidth the
+// MLP kernels' weight fragments and parked operands are read at, as they read
+// them (ds_read_b128, one 16-byte slot per lane, consecutive lanes on
+// consecutive slots: conflict-free). Each 256-thread block fills 32 KB of LDS
+// (four blocks per CU fit), then every lane reads kLdsRateSlots slots per
+// iteration. The loaded registers are consumed by an empty asm statement that
+// also clobbers memory, so each iteration issues its loads again and no ALU
+// work competes with them; out is written only on an impossible value.
+constexpr int kLdsRateThreads = 256;
+constexpr int kLdsRateSlots = 8;
+
+typedef uint32_t rate_u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(kLdsRateThreads) lds_rate_kernel(int32_t iters, uint32_t *out) {
+  __shared__ rate_u32x4 buf[kLdsRateSlots * kLdsRateThreads];
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < kLdsRateSlots; ++k) {
+    rate_u32x4 w = {static_cast<uint32_t>(t), static_cast<uint32_t>(k),
+                    static_cast<uint32_t>(t ^ k), 1u};
+    buf[k * kLdsRateThreads + t] = w;
+  }
+  __syncthreads();
+  uint32_t acc = 0u;
+  for (int it = 0; it < iters; ++it) {
+    rate_u32x4 v[kLdsRateSlots];
+#pragma unroll
+    for (int k = 0; k < kLdsRateSlots; ++k) v[k] = buf[k * kLdsRateThreads + t];
+    asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]),
+                 "v"(v[6]), "v"(v[7])
+                 : "memory");
+    acc += v[it & (kLdsRateSlots - 1)].w;
+  }
+  if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
+}
+
 }  // namespace tmnn_hip

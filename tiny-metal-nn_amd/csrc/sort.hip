@@ -443,7 +443,8 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
                              int n, hipStream_t stream, const uint32_t **keys_sorted,
                              const uint32_t **vals_sorted) {
   size_t need = 0;
-  morton_sort_temp_bytes(n, &need);
+  const hipError_t need_err = morton_sort_temp_bytes(n, &need);
+  if (need_err != hipSuccess) return need_err;
   if (n <= 0 || tmp_bytes < need || dims < 2 || dims > 4) return hipErrorInvalidValue;
   // 2D codes interleave x and y only (the lifted z = 0 bits are all zero,
   // which leaves the order unchanged): 20 bits; 3D 30 bits; 4D 32 bits.

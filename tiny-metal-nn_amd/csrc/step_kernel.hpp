@@ -28,6 +28,11 @@ struct FinishArgs {
   FieldLayout s;               // layout of the image below (pack_image_kernel's)
   int32_t f16;                 // fp16 fragments (else fp32)
   unsigned char *image;        // the training plan's packed image, updated in place
+  // numerics probe (finish_step_kernel<F, true>): per block one row
+  // {max |g|, sum g^2, max |update|, non-finite bits}; the loss block's row
+  // is {max |output| over amax_partials, the loss, 0, 0}
+  const float *amax_partials;  // [part_blocks] largest |output| per training block
+  float4 *num_rows;            // [gridDim.x]
 };
 
 constexpr int kFinishThreads = kReduceCols * kReduceGroups;
@@ -79,9 +84,36 @@ __device__ __forceinline__ void write_image_param(const FinishArgs &a, int idx, 
   }
 }
 
-template <int F>
+// Block-wide reduction of the threads' numerics terms into row blockIdx.x.
+__device__ __forceinline__ void num_block_row(const FinishArgs &a, NumAcc acc) {
+  __shared__ float4 nred[kFinishThreads / 64];
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    acc.gmax = fmaxf(acc.gmax, __shfl_xor(acc.gmax, off));
+    acc.g2 += __shfl_xor(acc.g2, off);
+    acc.umax = fmaxf(acc.umax, __shfl_xor(acc.umax, off));
+    acc.bad |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc.bad), off));
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) nred[wave] = make_float4(acc.gmax, acc.g2, acc.umax, __uint_as_float(acc.bad));
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float4 r = nred[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x) / 64; ++w) {
+      const float4 o = nred[w];
+      r.x = fmaxf(r.x, o.x);
+      r.y += o.y;
+      r.z = fmaxf(r.z, o.z);
+      r.w = __uint_as_float(__float_as_uint(r.w) | __float_as_uint(o.w));
+    }
+    a.num_rows[blockIdx.x] = r;
+  }
+}
+
+template <int F, bool NUM = false>
 __global__ void __launch_bounds__(kFinishThreads) finish_step_kernel(FinishArgs a) {
   const AdamArgs &ad = a.adam;
+  NumAcc acc;
   if (blockIdx.x < static_cast<uint32_t>(a.mlp_blocks)) {
     __shared__ float red[kReduceGroups][kReduceCols + 1];
     const int c = threadIdx.x % kReduceCols;
@@ -100,9 +132,10 @@ __global__ void __launch_bounds__(kFinishThreads) finish_step_kernel(FinishArgs 
       float t = 0.0f;
 #pragma unroll
       for (int k = 0; k < kReduceGroups; ++k) t += red[k][c];
-      const float w = adam_mlp_param<F>(ad, col, ad.grad_mlp[col] + t);
+      const float w = adam_mlp_param<F, NUM>(ad, col, ad.grad_mlp[col] + t, &acc);
       if (a.image) write_image_param(a, col, w);
     }
+    if constexpr (NUM) num_block_row(a, acc);
     return;
   }
   if (blockIdx.x == static_cast<uint32_t>(a.mlp_blocks)) {
@@ -113,14 +146,23 @@ __global__ void __launch_bounds__(kFinishThreads) finish_step_kernel(FinishArgs 
       for (int32_t b = lane; b < a.part_blocks; b += 64) t += a.loss_partials[b];
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
-      if (lane == 0 && a.loss_out) *a.loss_out = a.n > 0 ? t / static_cast<float>(a.n) : 0.0f;
+      const float loss = a.n > 0 ? t / static_cast<float>(a.n) : 0.0f;
+      if (lane == 0 && a.loss_out) *a.loss_out = loss;
+      if constexpr (NUM) {
+        float m = 0.0f;
+        for (int32_t b = lane; b < a.part_blocks; b += 64) m = fmaxf(m, a.amax_partials[b]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (lane == 0) a.num_rows[blockIdx.x] = make_float4(m, loss, 0.0f, 0.0f);
+      }
     }
     return;
   }
   const uint32_t first = static_cast<uint32_t>(a.mlp_blocks) + 1u;
   const uint32_t stride = (gridDim.x - first) * blockDim.x;
   for (uint32_t j = (blockIdx.x - first) * blockDim.x + threadIdx.x; j < ad.hash_entries; j += stride)
-    adam_hash_entry<F>(ad, j);
+    adam_hash_entry<F, NUM>(ad, j, &acc);
+  if constexpr (NUM) num_block_row(a, acc);
 }
 
 }  // namespace tmnn_hip

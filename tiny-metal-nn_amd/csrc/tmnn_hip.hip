@@ -50,15 +50,25 @@ static __device__ __align__(256) unsigned char scratch[TMNN_NOALLOC_SCRATCH_BYTE
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 2u;
+constexpr uint32_t kAbiVersion = 3u;
 constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr uint32_t kOptimizerBlobVersion = 1u;  // detail/checkpoint_contract.h:14
 
 thread_local std::string g_last_error;
 
-// Device address of `scratch` per device ordinal, looked up once per device.
+// Per device ordinal: the device address of `scratch` (looked up once per
+// device) and the event that serialises the allocation-free steps of every
+// context on that device. Each such step waits for the event before its
+// first kernel and records it after its last, under g_scratch_mu, so steps
+// of trainers on different streams take the scratch one after another
+// instead of racing on it.
+struct ScratchDevice {
+  unsigned char *ptr = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+};
 std::mutex g_scratch_mu;
-std::vector<unsigned char *> g_scratch_dev;
+std::vector<ScratchDevice> g_scratch;
 
 int fail(int code, const std::string &msg) {
   g_last_error = msg;
@@ -313,11 +323,28 @@ struct tmnn_trainer {
   int prof_cur = -1;  // event set of the step being enqueued, or -1
   bool prof_suspended = false;  // allocation-free steps record no events
   tmnn_step_profile prof_acc{};
+  // per profiled step, in step order: the phase times (TMNN_PROFILE_*)
+  std::vector<std::array<float, TMNN_PROFILE_PHASES>> prof_samples;
   // inference calls while profiling is on: one event pair around the
   // forward kernel of one call in prof_every
   uint64_t prof_infer_seen = 0;
   std::vector<std::array<hipEvent_t, 2>> infer_events;
   size_t infer_used = 0;
+
+  // Numerics (NumericsGuard, numerics_guard.cpp:12-36): sampling mode and
+  // interval, the anomaly history, and the device rows of the last step whose
+  // report was computed (finish_step_kernel<F, true>: one float4 per block;
+  // num_loss_row holds the largest |output| and the loss).
+  int32_t num_mode = TMNN_NUMERICS_SAMPLED;
+  uint32_t num_interval = 128;
+  uint32_t num_anomalies = 0, num_last_anomaly = 0;
+  bool num_this_step = false;   // the step being enqueued computes its report
+  DevBuf num_rows, amax_partials;
+  int num_row_count = 0, num_loss_row = 0;
+  uint32_t num_step = 0;        // step counter after that step (0: none yet)
+  uint32_t num_batch = 0;
+  float *dbg_step_out = nullptr;  // tmnn_debug_step_outputs: the training kernel's outputs
+  hipEvent_t input_ready = nullptr;  // caller's event the side stream's sort waits for
 
   ~tmnn_trainer() {
     if (side) {
@@ -441,6 +468,14 @@ int prof_collect(tmnn_trainer *tr) {
     for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k) {
       ms[k] = 0.0f;
       if (at[k] != at[k + 1]) TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[at[k]], e[at[k + 1]]));
+    }
+    {
+      std::array<float, TMNN_PROFILE_PHASES> smp{};
+      for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k) smp[k] = 1e3f * ms[k];
+      float total = 0.0f;
+      for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k) total += smp[k];
+      smp[TMNN_PROFILE_TOTAL] = total;
+      tr->prof_samples.push_back(smp);
     }
     tr->prof_acc.gpu_sort_us += 1e3 * ms[0];
     tr->prof_acc.gpu_encode_us += 1e3 * ms[1];
@@ -893,19 +928,10 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
                      int prof_after_encode, bool reuse_x, const uint32_t *perm, float *pos_out) {
   int rc;
   const bool fwd_only = a.mode == kModeForward;
-  if (!reuse_x && (rc = launch_encode(tr, a.pos, n, perm, pos_out)) != TMNN_OK) return rc;
-  if (prof_after_encode >= 0 && (rc = prof_mark(tr, prof_after_encode)) != TMNN_OK) return rc;
   const int IN = tr->IN, H = tr->d.hidden_dim, NHL = tr->d.num_hidden_layers;
   const int M = tr->d.num_outputs;
-  const size_t N = static_cast<size_t>(n);
-  TMNN_HIP_TRY(tr->lw_act.ensure(N * H * NHL * sizeof(float)));
-  TMNN_HIP_TRY(tr->lw_y.ensure(N * M * sizeof(float)));
-  TMNN_HIP_TRY(tr->lw_g.ensure(N * M * sizeof(float)));
-  TMNN_HIP_TRY(tr->lw_d.ensure(2 * N * std::max(H, 1) * sizeof(float)));
   const FieldLayout lay = make_layout(tr->INP, tr->HP, IN, H, NHL, M, 0, false, false, 1);
   hipStream_t st = tr->ctx->stream;
-  float *act = tr->lw_act.as<float>();
-  auto act_k = [&](int k) { return act + static_cast<size_t>(k) * N * H; };
   auto gemm = [&](LwGemmArgs g, int chunks) -> int {
     if (g.R <= 0 || g.C <= 0) return TMNN_OK;
     const dim3 grid((g.R + kLwTile - 1) / kLwTile, (g.C + kLwTile - 1) / kLwTile, chunks);
@@ -916,6 +942,59 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
   LwGemmArgs base{};
   base.KT0 = tr->INP / 16;
   base.scale = 1.0f;
+  if (fwd_only) {
+    // Forward passes (inference has no batch cap) run in chunks of at most
+    // kLwForwardChunk points through two ping-pong activation buffers, so
+    // their memory is bounded whatever n is; the backward's buffers are not
+    // touched. Every forward caller hands over positions in output order
+    // (perm == nullptr) with an optional output row index.
+    const int chunk = std::min(n, kLwForwardChunk);
+    const size_t C = static_cast<size_t>(chunk);
+    TMNN_HIP_TRY(tr->lw_act.ensure(2 * C * H * sizeof(float)));
+    float *buf[2] = {tr->lw_act.as<float>(), tr->lw_act.as<float>() + C * H};
+    for (int c0 = 0; c0 < n; c0 += chunk) {
+      const int cn = std::min(chunk, n - c0);
+      if ((rc = launch_encode(tr, a.pos + static_cast<size_t>(c0) * tr->d.spatial_dims, cn)) !=
+          TMNN_OK)
+        return rc;
+      if (c0 == 0 && prof_after_encode >= 0 && (rc = prof_mark(tr, prof_after_encode)) != TMNN_OK)
+        return rc;
+      for (int k = 0; k <= NHL; ++k) {
+        LwGemmArgs g = base;
+        g.R = cn;
+        g.K = k == 0 ? IN : H;
+        g.C = k == NHL ? M : H;
+        g.k_chunk = g.K;
+        g.a_mode = k == 0 ? kLwAXTiles : kLwARow;
+        g.A = k == 0 ? tr->xfeat.as<float>() : buf[(k - 1) & 1];
+        g.lda = H;
+        g.B = a.mlp + lay.w_off(k);
+        g.ldb = g.C;
+        g.bias = a.mlp + lay.b_off(k);
+        if (k < NHL) {
+          g.epi = kLwEpiHidden;
+          g.out = buf[k & 1];
+          g.ldo = H;
+        } else {
+          g.epi = kLwEpiOutput;
+          g.out = a.out_index ? a.out : a.out + static_cast<size_t>(c0) * M;
+          g.out_index = a.out_index ? a.out_index + c0 : nullptr;
+          g.ldo = M;
+        }
+        if ((rc = gemm(g, 1)) != TMNN_OK) return rc;
+      }
+    }
+    return 1;
+  }
+  if (!reuse_x && (rc = launch_encode(tr, a.pos, n, perm, pos_out)) != TMNN_OK) return rc;
+  if (prof_after_encode >= 0 && (rc = prof_mark(tr, prof_after_encode)) != TMNN_OK) return rc;
+  const size_t N = static_cast<size_t>(n);
+  TMNN_HIP_TRY(tr->lw_act.ensure(N * H * NHL * sizeof(float)));
+  TMNN_HIP_TRY(tr->lw_y.ensure(N * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->lw_g.ensure(N * M * sizeof(float)));
+  TMNN_HIP_TRY(tr->lw_d.ensure(2 * N * std::max(H, 1) * sizeof(float)));
+  float *act = tr->lw_act.as<float>();
+  auto act_k = [&](int k) { return act + static_cast<size_t>(k) * N * H; };
   // ---- forward (kept when the caller re-runs the backward for another output)
   if (!(reuse_x && a.mode == kModeInputGrad)) {
     for (int k = 0; k <= NHL; ++k) {
@@ -936,7 +1015,7 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
         g.ldo = H;
       } else {
         g.epi = kLwEpiOutput;
-        g.out = fwd_only ? a.out : nullptr;
+        g.out = nullptr;
         g.out_index = a.out_index;
         g.ldo = M;
         g.out2 = tr->lw_y.as<float>();
@@ -945,7 +1024,6 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
       if ((rc = gemm(g, 1)) != TMNN_OK) return rc;
     }
   }
-  if (fwd_only) return 1;
   // ---- output gradient (and the loss), per batch chunk
   const int P = std::max(1, std::min(plan.max_blocks, (n + 255) / 256));
   const int chunk = (n + P - 1) / P;
@@ -962,9 +1040,11 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
   la.y = tr->lw_y.as<float>();
   la.target = a.target;
   la.tgt_index = a.tgt_index;
-  la.out = a.mode == kModeInputGrad ? a.out : nullptr;
+  la.out = a.out;
+  la.out_index = a.out_index;
   la.g = tr->lw_g.as<float>();
   la.loss_partials = a.loss_partials;
+  la.amax_partials = a.amax_partials;
   hipLaunchKernelGGL(lw_loss_kernel, dim3(P), dim3(256), 0, st, la);
   TMNN_HIP_TRY(hipGetLastError());
   // ---- backward: weight-gradient partial rows (training), deltas, dx
@@ -1190,6 +1270,7 @@ int sort_batch_overlapped(tmnn_trainer *tr, const float *d_pos, int n, bool stag
   auto &ss = tr->step_sort[k];
   hipStream_t sd = tr->side;
   if (tr->consumed_recorded[k]) TMNN_HIP_TRY(hipStreamWaitEvent(sd, tr->ev_consumed[k], 0));
+  if (tr->input_ready) TMNN_HIP_TRY(hipStreamWaitEvent(sd, tr->input_ready, 0));
   if (staged_on_main) {
     // the batch was copied in on the main stream: the sort reads it after
     // that (an event with the system-scope fence, as the copy came from host
@@ -1255,6 +1336,11 @@ int run_forward_backward(tmnn_trainer *tr, const float *d_pos, const float *d_tg
   float *sorted_pos = indexed ? tr->s_pos.as<float>() : nullptr;
   a.grad_partials = tr->partials.as<float>();
   a.loss_partials = tr->loss_partials.as<float>();
+  a.amax_partials = (!external_grad && tr->num_this_step) ? tr->amax_partials.as<float>() : nullptr;
+  if (tr->dbg_step_out) {  // parity read-out: outputs in the caller's row order
+    a.out = tr->dbg_step_out;
+    a.out_index = perm;
+  }
   a.dx_out = tr->dx.as<float>();
   const bool fused_scatter = tr->train_plan.tile_scatter;
   if (fused_scatter) {  // the training kernel runs the hash-grid backward per tile
@@ -1347,6 +1433,9 @@ int run_finish(tmnn_trainer *tr, int part_blocks, int n, float *d_loss) {
                     tr->d.num_outputs, static_cast<int>(tr->mlp_count), plan.f16, plan.train, 1);
   f.f16 = plan.f16 ? 1 : 0;
   f.image = image_current ? static_cast<unsigned char *>(plan.image) : nullptr;
+  const bool num = tr->num_this_step;
+  f.amax_partials = tr->amax_partials.as<float>();
+  f.num_rows = static_cast<float4 *>(tr->num_rows.ptr);
   // Hash blocks: large tables grid-stride over at most four blocks per CU;
   // a small table's blocks fill what the MLP and loss blocks leave of one
   // round of resident blocks (two 1024-thread blocks per CU) when that keeps
@@ -1359,12 +1448,27 @@ int run_finish(tmnn_trainer *tr, int part_blocks, int n, float *d_loss) {
   const uint32_t hash_blocks =
       needed > cap ? cap : std::max<uint32_t>({1u, std::min(needed, room), (needed + 1u) / 2u});
   const dim3 grid(static_cast<uint32_t>(f.mlp_blocks) + 1u + hash_blocks);
+  if (num && tr->num_rows.bytes < grid.x * sizeof(float4))
+    return fail(TMNN_ERR_RUNTIME, "numerics rows smaller than the finish grid");
+  hipStream_t st = tr->ctx->stream;
+#define TMNN_FINISH(ff)                                                                            \
+  if (num)                                                                                         \
+    hipLaunchKernelGGL((finish_step_kernel<ff, true>), grid, dim3(kFinishThreads), 0, st, f);      \
+  else                                                                                             \
+    hipLaunchKernelGGL((finish_step_kernel<ff, false>), grid, dim3(kFinishThreads), 0, st, f);
   switch (tr->d.features_per_level) {
-    case 1: hipLaunchKernelGGL(finish_step_kernel<1>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
-    case 2: hipLaunchKernelGGL(finish_step_kernel<2>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
-    default: hipLaunchKernelGGL(finish_step_kernel<4>, grid, dim3(kFinishThreads), 0, tr->ctx->stream, f); break;
+    case 1: TMNN_FINISH(1) break;
+    case 2: TMNN_FINISH(2) break;
+    default: TMNN_FINISH(4) break;
   }
+#undef TMNN_FINISH
   TMNN_HIP_TRY(hipGetLastError());
+  if (num) {
+    tr->num_row_count = static_cast<int>(grid.x);
+    tr->num_loss_row = f.mlp_blocks;
+    tr->num_step = tr->step + 1;
+    tr->num_batch = static_cast<uint32_t>(n);
+  }
   tr->mask_cur ^= 1;  // the zeroed buffer collects the next step
   ++tr->weights_version;
   if (image_current) plan.packed_version = tr->weights_version;
@@ -1389,24 +1493,96 @@ void prof_abort(tmnn_trainer *tr) {
   tr->prof_cur = -1;
 }
 
+// NumericsGuard::should_sample (numerics_guard.cpp:12-36) for the step
+// counter after the update.
+bool numerics_should_sample(const tmnn_trainer *tr, uint32_t step) {
+  const bool after_anomaly = tr->num_anomalies > 0 && step == tr->num_last_anomaly + 1;
+  switch (tr->num_mode) {
+    case TMNN_NUMERICS_DISABLED: return false;
+    case TMNN_NUMERICS_FULL: return true;
+    case TMNN_NUMERICS_PERIODIC:
+      return after_anomaly || (step != 0 && step % tr->num_interval == 0);
+    default:
+      return step == 0 || step == 1 || after_anomaly || step % tr->num_interval == 0;
+  }
+}
+
+// A report from the finish kernel's rows (host copies): the largest |output|
+// and the loss from the loss block's row, max / sum / OR over the others.
+void numerics_from_rows(const std::vector<float4> &rows, int loss_row, tmnn_step_result *out) {
+  float gmax = 0.0f, umax = 0.0f;
+  double g2 = 0.0;
+  uint32_t bad = 0u;
+  for (size_t b = 0; b < rows.size(); ++b) {
+    if (static_cast<int>(b) == loss_row) continue;
+    gmax = std::max(gmax, rows[b].x);
+    g2 += static_cast<double>(rows[b].y);
+    umax = std::max(umax, rows[b].z);
+    uint32_t w;
+    std::memcpy(&w, &rows[b].w, sizeof w);
+    bad |= w;
+  }
+  tmnn_numerics_report &r = out->numerics;
+  r = tmnn_numerics_report{};
+  const float loss = rows[loss_row].y;
+  r.finite_forward = std::isfinite(loss) ? 1 : 0;
+  r.finite_backward = (bad & 1u) ? 0 : 1;
+  r.finite_update = (r.finite_backward && !(bad & 2u)) ? 1 : 0;
+  r.max_abs_activation = rows[loss_row].x;
+  r.max_abs_gradient = gmax;
+  r.max_abs_update = umax;
+  r.first_bad_layer = 0u;
+  out->grad_norm = static_cast<float>(std::sqrt(g2));
+  out->numerics_reported = 1;
+  out->has_numerics_anomaly = (r.finite_forward && r.finite_backward && r.finite_update) ? 0 : 1;
+}
+
+// Copies the rows of the last computed report (enqueued on the trainer's
+// stream; the caller synchronizes).
+int numerics_rows_download(tmnn_trainer *tr, std::vector<float4> &rows) {
+  rows.resize(static_cast<size_t>(tr->num_row_count));
+  TMNN_HIP_TRY(hipMemcpyAsync(rows.data(), tr->num_rows.ptr, rows.size() * sizeof(float4),
+                              hipMemcpyDeviceToHost, tr->ctx->stream));
+  return TMNN_OK;
+}
+
+// NumericsGuard::record_step: an anomaly makes the next step sampled.
+void numerics_record(tmnn_trainer *tr, uint32_t step, const tmnn_step_result &r) {
+  if (r.has_numerics_anomaly) {
+    ++tr->num_anomalies;
+    tr->num_last_anomaly = step;
+  }
+}
+
 // overlap_sort: 0 sorts on the main stream (the step's buffers may be
 // borrowed scratch); 1 sorts on the side stream (the caller's batch is
 // ready); 2 as 1, the batch being staged on the main stream.
+// num: the finish kernel also computes the step's numerics report (rows on
+// the device). input_ready (nullable): an event of the caller's that every
+// stream reading the batch waits for first.
 int train_step_device(tmnn_trainer *tr, const float *d_pos, const float *d_tgt, int n,
-                      float *d_loss, int overlap_sort = 1) {
+                      float *d_loss, int overlap_sort = 1, bool num = false,
+                      hipEvent_t input_ready = nullptr) {
+  if (input_ready) TMNN_HIP_TRY(hipStreamWaitEvent(tr->ctx->stream, input_ready, 0));
   int rc = prof_begin_step(tr);
   if (rc != TMNN_OK) return rc;
   float *loss = d_loss ? d_loss : tr->loss_out.as<float>();
   const bool overlapped = overlap_sort && tr->d.morton_sort && n > 1 && tr->train_plan.xmem;
+  tr->num_this_step = num;
+  tr->input_ready = input_ready;
   const int blocks = run_forward_backward(tr, d_pos, d_tgt, n, false, loss, false, overlap_sort);
+  tr->input_ready = nullptr;
   if (blocks < 0) {
+    tr->num_this_step = false;
     prof_abort(tr);
     if (overlapped) (void)sort_set_consumed(tr);
     return blocks;
   }
   // dW reduction, loss and Adam in one kernel (the reduce phase is empty: no
   // boundary event)
-  if ((rc = run_finish(tr, blocks, n, loss)) != TMNN_OK || (rc = prof_mark(tr, 6)) != TMNN_OK) {
+  rc = run_finish(tr, blocks, n, loss);
+  tr->num_this_step = false;
+  if (rc != TMNN_OK || (rc = prof_mark(tr, 6)) != TMNN_OK) {
     prof_abort(tr);
     if (overlapped) (void)sort_set_consumed(tr);
     return rc;
@@ -1492,6 +1668,64 @@ uint32_t get_u32(const uint8_t *p) {
 }
 
 
+// The synchronous step of the host-pointer entry points: the batch staged
+// on the main stream, the fused device step, then the loss (and, on sampled
+// steps or when the loss is not finite, the numerics rows) read back. The
+// finish kernel computes the report on every such step, so a non-finite
+// loss is reported in full as the reference's forced probe does
+// (training_step_execution.cpp:1015-1043); only the read-back is sampled.
+// dbg_out (host, nullable): the training kernel's outputs, caller row order.
+int host_training_step(tmnn_trainer *tr, const float *input, const float *target, int32_t n,
+                       tmnn_step_result *out, float *dbg_out) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (out && out->struct_size != sizeof(tmnn_step_result))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_step_result.struct_size mismatch");
+  if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
+  if (!input || !target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int bn = std::min(n, tr->d.batch_size);
+  int rc = ensure_batch(tr, bn);
+  if (rc != TMNN_OK) return rc;
+  hipStream_t st = tr->ctx->stream;
+  const size_t M = tr->d.num_outputs;
+  if (dbg_out) TMNN_HIP_TRY(tr->out_buf.ensure(static_cast<size_t>(bn) * M * sizeof(float)));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, input,
+                              static_cast<size_t>(bn) * tr->d.spatial_dims * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_tgt.ptr, target, static_cast<size_t>(bn) * M * sizeof(float),
+                              hipMemcpyHostToDevice, st));
+  const uint32_t next = tr->step + 1;
+  const bool sampled = numerics_should_sample(tr, next);
+  tr->dbg_step_out = dbg_out ? tr->out_buf.as<float>() : nullptr;
+  rc = train_step_device(tr, tr->in_pos.as<float>(), tr->in_tgt.as<float>(), bn,
+                         tr->loss_out.as<float>(), 2, true);
+  tr->dbg_step_out = nullptr;
+  if (rc != TMNN_OK) return rc;
+  float loss = 0.0f;
+  TMNN_HIP_TRY(hipMemcpyAsync(&loss, tr->loss_out.ptr, sizeof(float), hipMemcpyDeviceToHost, st));
+  std::vector<float4> rows;
+  if (sampled && (rc = numerics_rows_download(tr, rows)) != TMNN_OK) return rc;
+  if (dbg_out)
+    TMNN_HIP_TRY(hipMemcpyAsync(dbg_out, tr->out_buf.ptr, static_cast<size_t>(bn) * M * sizeof(float),
+                                hipMemcpyDeviceToHost, st));
+  TMNN_HIP_TRY(hipStreamSynchronize(st));
+  if (!sampled && !std::isfinite(loss)) {  // forced report of a non-finite loss
+    if ((rc = numerics_rows_download(tr, rows)) != TMNN_OK) return rc;
+    TMNN_HIP_TRY(hipStreamSynchronize(st));
+  }
+  tmnn_step_result r{};
+  r.struct_size = sizeof r;
+  r.loss = loss;
+  r.step = tr->step;
+  r.batch_n = static_cast<uint32_t>(bn);
+  if (!rows.empty()) {
+    numerics_from_rows(rows, tr->num_loss_row, &r);
+    numerics_record(tr, r.step, r);
+  }
+  if (out) *out = r;
+  return TMNN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1518,15 +1752,25 @@ int tmnn_context_create(int32_t device, tmnn_context **out) {
   ctx->name = prop.gcnArchName;
   TMNN_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
   {
-    // this device's copy of the step scratch, with the device current
+    // This device's copy of the step scratch, with the device current, and
+    // the event that orders its users. Only the allocation-free step needs
+    // them: if either is unavailable the context is still created, and that
+    // entry point reports the missing scratch.
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (g_scratch_dev.size() < static_cast<size_t>(count)) g_scratch_dev.resize(count, nullptr);
-    if (!g_scratch_dev[device]) {
+    if (g_scratch.size() < static_cast<size_t>(count)) g_scratch.resize(count);
+    ScratchDevice &sd = g_scratch[device];
+    if (!sd.ptr) {
       void *p = nullptr;
-      TMNN_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-      g_scratch_dev[device] = static_cast<unsigned char *>(p);
+      hipEvent_t ev = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess && p &&
+          hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
+        sd.ptr = static_cast<unsigned char *>(p);
+        sd.done = ev;
+      } else {
+        (void)hipGetLastError();  // clear the sticky error of the failed lookup
+      }
     }
-    ctx->scratch = g_scratch_dev[device];
+    ctx->scratch = sd.ptr;
   }
   *out = ctx.release();
   return TMNN_OK;
@@ -1706,6 +1950,13 @@ int tmnn_trainer_create(tmnn_context *ctx, const tmnn_model_desc *desc, tmnn_tra
   TMNN_HIP_TRY(tr->loss_partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
                                         sizeof(float)));
   TMNN_HIP_TRY(tr->loss_out.ensure(sizeof(float)));
+  // numerics: one largest-|output| per training block, one row per finish
+  // block (MLP column blocks, the loss block, at most four hash blocks per CU)
+  TMNN_HIP_TRY(tr->amax_partials.ensure(static_cast<size_t>(tr->train_plan.max_blocks) *
+                                        sizeof(float)));
+  TMNN_HIP_TRY(tr->num_rows.ensure(
+      ((tr->mlp_count + kReduceCols - 1) / kReduceCols + 1 + static_cast<size_t>(ctx->cu_count) * 4) *
+      sizeof(float4)));
   if ((rc = init_weights(tr.get())) != TMNN_OK) return rc;
   if ((rc = reset_moments(tr.get())) != TMNN_OK) return rc;
   if ((rc = zero_training_state(tr.get())) != TMNN_OK) return rc;
@@ -1751,36 +2002,17 @@ int tmnn_trainer_inspect(tmnn_trainer *tr, tmnn_inspection *o) {
 
 int tmnn_training_step(tmnn_trainer *tr, const float *input, const float *target, int32_t n,
                        tmnn_step_result *out) {
-  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
-  if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
-  if (!input || !target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
-  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
-  const int bn = std::min(n, tr->d.batch_size);
-  int rc = ensure_batch(tr, bn);
-  if (rc != TMNN_OK) return rc;
-  hipStream_t st = tr->ctx->stream;
-  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_pos.ptr, input,
-                              static_cast<size_t>(bn) * tr->d.spatial_dims * sizeof(float),
-                              hipMemcpyHostToDevice, st));
-  TMNN_HIP_TRY(hipMemcpyAsync(tr->in_tgt.ptr, target,
-                              static_cast<size_t>(bn) * tr->d.num_outputs * sizeof(float),
-                              hipMemcpyHostToDevice, st));
-  rc = train_step_device(tr, tr->in_pos.as<float>(), tr->in_tgt.as<float>(), bn,
-                         tr->loss_out.as<float>(), 2);
-  if (rc != TMNN_OK) return rc;
-  float loss = 0.0f;
-  TMNN_HIP_TRY(hipMemcpyAsync(&loss, tr->loss_out.ptr, sizeof(float), hipMemcpyDeviceToHost, st));
-  TMNN_HIP_TRY(hipStreamSynchronize(st));
-  if (out) {
-    out->loss = loss;
-    out->step = tr->step;
-    out->batch_n = static_cast<uint32_t>(bn);
-  }
-  return TMNN_OK;
+  return host_training_step(tr, input, target, n, out, nullptr);
 }
 
 int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input, const float *d_target,
                               int32_t n, float *d_loss_out) {
+  return tmnn_training_step_device_after(tr, d_input, d_target, n, d_loss_out, nullptr);
+}
+
+int tmnn_training_step_device_after(tmnn_trainer *tr, const float *d_input,
+                                    const float *d_target, int32_t n, float *d_loss_out,
+                                    void *wait_event) {
   if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
   if (n <= 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "training_step: N must be > 0");
   if (!d_input || !d_target) return fail(TMNN_ERR_INVALID_ARGUMENT, "input/target is null");
@@ -1788,7 +2020,57 @@ int tmnn_training_step_device(tmnn_trainer *tr, const float *d_input, const floa
   const int bn = std::min(n, tr->d.batch_size);
   const int rc = ensure_batch(tr, bn);
   if (rc != TMNN_OK) return rc;
-  return train_step_device(tr, d_input, d_target, bn, d_loss_out);
+  // device steps are sampled by step only: their losses are not read back
+  return train_step_device(tr, d_input, d_target, bn, d_loss_out, 1,
+                           numerics_should_sample(tr, tr->step + 1),
+                           static_cast<hipEvent_t>(wait_event));
+}
+
+int tmnn_record_event(tmnn_trainer *tr, void *event) {
+  if (!tr || !event) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  TMNN_HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(event), tr->ctx->stream));
+  return TMNN_OK;
+}
+
+int tmnn_set_numerics_sampling(tmnn_trainer *tr, int32_t mode, uint32_t interval) {
+  if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
+  if (mode < TMNN_NUMERICS_SAMPLED || mode > TMNN_NUMERICS_DISABLED)
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "unknown numerics sampling mode");
+  tr->num_mode = mode;
+  tr->num_interval = interval > 0 ? interval : 1u;  // NumericsGuard::set_sample_interval
+  tr->num_anomalies = 0;
+  tr->num_last_anomaly = 0;
+  return TMNN_OK;
+}
+
+int tmnn_get_last_numerics(tmnn_trainer *tr, tmnn_step_result *out) {
+  if (!tr || !out) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (out->struct_size != sizeof(tmnn_step_result))
+    return fail(TMNN_ERR_INVALID_ARGUMENT, "tmnn_step_result.struct_size mismatch");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  tmnn_step_result r{};
+  r.struct_size = sizeof r;
+  if (tr->num_step > 0) {
+    std::vector<float4> rows;
+    const int rc = numerics_rows_download(tr, rows);
+    if (rc != TMNN_OK) return rc;
+    TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+    r.loss = rows[tr->num_loss_row].y;
+    r.step = tr->num_step;
+    r.batch_n = tr->num_batch;
+    numerics_from_rows(rows, tr->num_loss_row, &r);
+  } else {
+    TMNN_HIP_TRY(hipStreamSynchronize(tr->ctx->stream));
+  }
+  *out = r;
+  return TMNN_OK;
+}
+
+int tmnn_debug_step_outputs(tmnn_trainer *tr, const float *input, const float *target,
+                            int32_t n, float *outputs, tmnn_step_result *result) {
+  if (!outputs) return fail(TMNN_ERR_INVALID_ARGUMENT, "outputs is null");
+  return host_training_step(tr, input, target, n, result, outputs);
 }
 
 int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
@@ -1839,25 +2121,46 @@ int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
     bufs[r]->bytes = want[r];
     bufs[r]->borrowed = true;
   }
+  // steps of other contexts on this device may hold the scratch: this step's
+  // kernels start after the last one's (the event is re-recorded under the
+  // same lock, after this step's kernels)
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchDevice &sd = g_scratch[tr->ctx->device];
+  if (!sd.done) return fail(TMNN_ERR_RUNTIME, "device scratch event unavailable");
+  if (sd.recorded) TMNN_HIP_TRY(hipStreamWaitEvent(tr->ctx->stream, sd.done, 0));
   tr->prof_suspended = true;
-  const int rc = train_step_device(tr, d_input, d_target, bn, d_loss_out, 0);
+  int rc = train_step_device(tr, d_input, d_target, bn, d_loss_out, 0,
+                             numerics_should_sample(tr, tr->step + 1));
   tr->prof_suspended = false;
   for (int r = 0; r < kRegions; ++r) {
     bufs[r]->ptr = saved[r].ptr;
     bufs[r]->bytes = saved[r].bytes;
     bufs[r]->borrowed = saved[r].borrowed;
   }
+  // recorded even after a failed enqueue: whatever was enqueued is ordered
+  const hipError_t e = hipEventRecord(sd.done, tr->ctx->stream);
+  if (e == hipSuccess)
+    sd.recorded = true;
+  else if (rc == TMNN_OK)
+    rc = fail(TMNN_ERR_GPU, std::string("hipEventRecord: ") + hipGetErrorString(e));
   return rc;
 }
 
 int tmnn_inference_device(tmnn_trainer *tr, const float *d_positions, float *d_output,
                           int32_t n) {
+  return tmnn_inference_device_after(tr, d_positions, d_output, n, nullptr);
+}
+
+int tmnn_inference_device_after(tmnn_trainer *tr, const float *d_positions, float *d_output,
+                                int32_t n, void *wait_event) {
   if (!tr) return fail(TMNN_ERR_INVALID_ARGUMENT, "trainer is null");
   if (n < 0) return fail(TMNN_ERR_INVALID_ARGUMENT, "FieldEvaluator::evaluate: N must be non-negative");
   if (n == 0) return TMNN_OK;
   if (!d_positions || !d_output)
     return fail(TMNN_ERR_INVALID_ARGUMENT, "positions and output must be non-null when N > 0");
   TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  if (wait_event)
+    TMNN_HIP_TRY(hipStreamWaitEvent(tr->ctx->stream, static_cast<hipEvent_t>(wait_event), 0));
   FieldArgs a = base_args(tr);
   a.mode = kModeForward;
   a.pos = d_positions;
@@ -2208,6 +2511,7 @@ int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled) {
   const int rc = prof_collect(tr);  // drop what an earlier window recorded
   if (rc != TMNN_OK) return rc;
   tr->prof_acc = tmnn_step_profile{};
+  tr->prof_samples.clear();
   tr->prof_every = enabled;
   tr->prof_seen = 0;
   tr->prof_infer_seen = 0;
@@ -2508,6 +2812,56 @@ int tmnn_debug_hash_rates(tmnn_trainer *tr, const float *d_positions, int32_t n,
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   if (err != hipSuccess) return fail(TMNN_ERR_GPU, std::string("hash rates: ") + hipGetErrorString(err));
+  return TMNN_OK;
+}
+
+int tmnn_debug_lds_rate(tmnn_context *ctx, int32_t reps, double *bytes_per_s) {
+  if (!ctx || !bytes_per_s) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  if (reps < 1) return fail(TMNN_ERR_INVALID_ARGUMENT, "reps must be >= 1");
+  TMNN_HIP_TRY(hipSetDevice(ctx->device));
+  hipStream_t st = ctx->stream;
+  // four resident 32 KB blocks per CU, two rounds of them
+  const uint32_t blocks = static_cast<uint32_t>(ctx->cu_count) * 8u;
+  const int32_t iters = 4096;
+  uint32_t *sink = nullptr;
+  TMNN_HIP_TRY(hipMalloc(&sink, blocks * sizeof(uint32_t)));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t err = hipEventCreate(&e0);
+  if (err == hipSuccess) err = hipEventCreate(&e1);
+  // one untimed launch, then reps timed ones
+  for (int r = 0; r <= reps && err == hipSuccess; ++r) {
+    if (r == 1) err = hipEventRecord(e0, st);
+    if (err != hipSuccess) break;
+    hipLaunchKernelGGL(lds_rate_kernel, dim3(blocks), dim3(kLdsRateThreads), 0, st, iters, sink);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipEventRecord(e1, st);
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  float ms = 0.0f;
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipFree(sink);
+  if (err != hipSuccess) return fail(TMNN_ERR_GPU, std::string("lds rate: ") + hipGetErrorString(err));
+  const double bytes = static_cast<double>(blocks) * kLdsRateThreads * 16.0 * kLdsRateSlots *
+                       iters * reps;
+  *bytes_per_s = bytes / (1e-3 * static_cast<double>(ms));
+  return TMNN_OK;
+}
+
+int tmnn_get_step_profile_samples(tmnn_trainer *tr, float *out, uint32_t capacity,
+                                  uint32_t *count) {
+  if (!tr || !count) return fail(TMNN_ERR_INVALID_ARGUMENT, "null argument");
+  TMNN_HIP_TRY(hipSetDevice(tr->ctx->device));
+  const int rc = prof_collect(tr);
+  if (rc != TMNN_OK) return rc;
+  *count = static_cast<uint32_t>(tr->prof_samples.size());
+  if (out) {
+    const size_t k = std::min<size_t>(capacity, tr->prof_samples.size());
+    for (size_t i = 0; i < k; ++i)
+      std::memcpy(out + i * TMNN_PROFILE_PHASES, tr->prof_samples[i].data(),
+                  TMNN_PROFILE_PHASES * sizeof(float));
+  }
   return TMNN_OK;
 }
 

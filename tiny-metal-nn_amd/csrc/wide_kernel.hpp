@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 #pragma unroll
     for (int k = 0; k <= NHL; ++k) dbias[k] = 0.0f;
   }
-  float lane_loss = 0.0f;
+  float lane_loss = 0.0f, lane_amax = 0.0f;
   const int pt0 = wave * kTilePts;  // this wave's points inside the block stage
   const int n_btiles = (a.n_tiles + kWideWaves - 1) / kWideWaves;
   unsigned char *stage_d = smem;
@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
       continue;
     } else {
       f32x4 g[OKT][kNT];
-      output_grad<OKT>(a, y, Tv, valid, pt, q, lane_loss, g);
+      output_grad<OKT>(a, y, Tv, valid, pt, q, lane_loss, lane_amax, g);
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt)
         if (!valid[nt])
@@ -432,18 +432,9 @@ __global__ void __launch_bounds__(kWideWaves * 64)
 
   if constexpr (TRAIN) {
     if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
-    float v = lane_loss;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
-    float *lred = reinterpret_cast<float *>(smem + wl.red);
     __syncthreads();
-    if (lane == 0) lred[wave] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = 0.0f;
-      for (int w = 0; w < kWideWaves; ++w) t += lred[w];
-      a.loss_partials[blockIdx.x] = t;
-    }
+    block_loss_partials(a, lane_loss, lane_amax, reinterpret_cast<float *>(smem + wl.red), lane,
+                        wave, kWideWaves);
     if constexpr (kWgrad) {
       // each dW element has one owner: write this block's partial row directly
       float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;

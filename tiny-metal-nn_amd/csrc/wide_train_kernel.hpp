@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   for (int k = 0; k < NHL - 1; ++k)
 #pragma unroll
     for (int j = 0; j < kSlotsHid; ++j) accH[k][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float lane_loss = 0.0f;
+  float lane_loss = 0.0f, lane_amax = 0.0f;
   const f32x4 *xt = reinterpret_cast<const f32x4 *>(a.xfeat);
   half8 *act_store = reinterpret_cast<half8 *>(a.wide_act);
   const bool has_target = a.mode != kModeInputGrad && a.target != nullptr;
@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(kWideWaves * 64)
                                 bias_of(NHL), y, lane);
         // loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
         f32x4 g[2][kNT];
-        output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, g);
+        output_grad<2, true>(a, y, Tv, valid, pt, q, lane_loss, lane_amax, g);
         half8 gb[1][kNT];
         pack_tiles<2>(g, gb);
         {
@@ -462,19 +462,10 @@ __global__ void __launch_bounds__(kWideWaves * 64)
   }
 
   if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
-  // ---- loss partial of the block (wave order)
-  float v = lane_loss;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
-  float *lred = reinterpret_cast<float *>(smem + ml.loss);
+  // ---- loss partial (wave order) and largest |output| of the block
   __syncthreads();
-  if (lane == 0) lred[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.0f;
-    for (int w = 0; w < W; ++w) t += lred[w];
-    a.loss_partials[blockIdx.x] = t;
-  }
+  block_loss_partials(a, lane_loss, lane_amax, reinterpret_cast<float *>(smem + ml.loss), lane,
+                      wave, W);
   // ---- owners write their tiles of the block's partial row (reference layout)
   float *dst = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
   const float sc = a.inv_loss_scale;

@@ -93,12 +93,48 @@ PLAN_REASONS = {1: "NoGPUContext", 4: "ThreadgroupMemoryExceeded", 6: "Unsupport
                 11: "ForcedSafeDebug", 13: "NoFusedInstance"}
 
 
-class StepResult(ctypes.Structure):
+class NumericsReport(ctypes.Structure):
+    """NumericsReport (detail/runtime_stats.h:32-40)."""
     _fields_ = [
+        ("finite_forward", ctypes.c_int32),
+        ("finite_backward", ctypes.c_int32),
+        ("finite_update", ctypes.c_int32),
+        ("max_abs_activation", ctypes.c_float),
+        ("max_abs_gradient", ctypes.c_float),
+        ("max_abs_update", ctypes.c_float),
+        ("first_bad_layer", ctypes.c_uint32),
+    ]
+
+
+class StepResult(ctypes.Structure):
+    """TrainingStepResult (common.h:97-110); struct_size is set on creation."""
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
         ("loss", ctypes.c_float),
         ("step", ctypes.c_uint32),
         ("batch_n", ctypes.c_uint32),
+        ("grad_norm", ctypes.c_float),
+        ("numerics_reported", ctypes.c_int32),
+        ("has_numerics_anomaly", ctypes.c_int32),
+        ("numerics", NumericsReport),
     ]
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        self.struct_size = ctypes.sizeof(StepResult)
+
+    def to_dict(self) -> dict:
+        out = {k: getattr(self, k) for k, _ in self._fields_ if k not in ("struct_size", "numerics")}
+        out["numerics"] = {k: getattr(self.numerics, k) for k, _ in NumericsReport._fields_}
+        for k in ("finite_forward", "finite_backward", "finite_update"):
+            out["numerics"][k] = bool(out["numerics"][k])
+        out["numerics_reported"] = bool(out["numerics_reported"])
+        out["has_numerics_anomaly"] = bool(out["has_numerics_anomaly"])
+        return out
+
+
+# NumericsSamplingMode (runtime_policy.h:13-18), same numbering
+NUMERICS_MODES = {"Sampled": 0, "Periodic": 1, "FullPerStep": 2, "Disabled": 3}
 
 
 class Inspection(ctypes.Structure):
@@ -135,6 +171,10 @@ class StepProfile(ctypes.Structure):
         ("gpu_infer_us", ctypes.c_double),
     ]
 
+
+# columns of tmnn_get_step_profile_samples (TMNN_PROFILE_*)
+PROFILE_PHASES = ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us",
+                  "gpu_reduce_us", "gpu_adam_us", "gpu_total_us")
 
 # RuntimeBufferRole (runtime_authority.h:68-79), same numbering
 BUFFER_ROLES = {"ConfigWeights": 0, "HashWeights": 1, "MlpWeights": 2, "GradHash": 3,
@@ -209,9 +249,14 @@ SIGNATURES = {
                                          ctypes.POINTER(NetworkPlan)]),
     "tmnn_training_step": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(StepResult)]),
     "tmnn_training_step_device": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
+    "tmnn_training_step_device_after": (ctypes.c_int, [_V, _V, _V, _I32, _V, _V]),
+    "tmnn_record_event": (ctypes.c_int, [_V, _V]),
+    "tmnn_set_numerics_sampling": (ctypes.c_int, [_V, _I32, _U32]),
+    "tmnn_get_last_numerics": (ctypes.c_int, [_V, ctypes.POINTER(StepResult)]),
     "tmnn_training_step_device_noalloc": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
     "tmnn_inference": (ctypes.c_int, [_V, _V, _V, _I32]),
     "tmnn_inference_device": (ctypes.c_int, [_V, _V, _V, _I32]),
+    "tmnn_inference_device_after": (ctypes.c_int, [_V, _V, _V, _I32, _V]),
     "tmnn_evaluate_with_gradient": (ctypes.c_int, [_V, _V, _V, _V, _I32]),
     "tmnn_forward_for_training": (ctypes.c_int, [_V, _V, _V, _I32, ctypes.POINTER(_U32)]),
     "tmnn_zero_gradients": (ctypes.c_int, [_V]),
@@ -228,6 +273,8 @@ SIGNATURES = {
     "tmnn_set_learning_rate": (ctypes.c_int, [_V, _F, _F]),
     "tmnn_set_step_profiling": (ctypes.c_int, [_V, _I32]),
     "tmnn_get_step_profile": (ctypes.c_int, [_V, ctypes.POINTER(StepProfile)]),
+    "tmnn_get_step_profile_samples": (ctypes.c_int, [_V, _V, _U32, ctypes.POINTER(_U32)]),
+    "tmnn_debug_lds_rate": (ctypes.c_int, [_V, _I32, ctypes.POINTER(ctypes.c_double)]),
     "tmnn_runtime_buffer": (ctypes.c_int, [_V, _I32, ctypes.POINTER(BufferView)]),
     "tmnn_parameter_layout": (ctypes.c_int, [_V, ctypes.POINTER(ParameterLayout)]),
     "tmnn_storage_policy": (ctypes.c_int, [_V, ctypes.POINTER(StoragePolicy)]),
@@ -239,6 +286,7 @@ SIGNATURES = {
                                              ctypes.POINTER(ctypes.c_double),
                                              ctypes.POINTER(ctypes.c_double),
                                              ctypes.POINTER(ctypes.c_double)]),
+    "tmnn_debug_step_outputs": (ctypes.c_int, [_V, _V, _V, _I32, _V, ctypes.POINTER(StepResult)]),
     "tmnn_debug_get_gradients": (ctypes.c_int, [_V, _V, _SZ, _V, _SZ]),
     "tmnn_debug_get_active_mask": (ctypes.c_int, [_V, _V, _SZ]),
     "tmnn_debug_morton_sort": (ctypes.c_int, [_V, _V, _I32, _V, _V]),

@@ -55,6 +55,19 @@ def _as_f32_2d(x, name: str, cols: int | None = None) -> np.ndarray:
     return arr
 
 
+def _event_arg(event):
+    """A HIP event argument: None, an int address, or an object exposing a
+    ctypes `_as_parameter_` (torch.cuda.Event, once recorded)."""
+    if event is None:
+        return None
+    if isinstance(event, int):
+        return ctypes.c_void_p(event)
+    p = getattr(event, "_as_parameter_", None)
+    if p is None:
+        raise TypeError("event must be None, an address or an object with _as_parameter_")
+    return p if isinstance(p, ctypes.c_void_p) else ctypes.c_void_p(int(p))
+
+
 def _ptr(a: np.ndarray):
     return a.ctypes.data_as(ctypes.c_void_p)
 
@@ -190,11 +203,77 @@ class Trainer:
         y = _as_f32_2d(target, "target", self.n_output)
         if x.shape[0] != y.shape[0]:
             raise ValueError("input and target must have matching batch_size")
+        return self.training_step_result(x, y)["loss"]
+
+    def training_step_result(self, input, target) -> dict:
+        """One fused step; returns the C++ API's TrainingStepResult as a dict
+        (loss, step, batch_n, grad_norm, numerics_reported,
+        has_numerics_anomaly, numerics{finite_forward, finite_backward,
+        finite_update, max_abs_activation, max_abs_gradient, max_abs_update,
+        first_bad_layer}); the numerics are filled on sampled steps
+        (set_numerics_sampling) and whenever the loss is not finite."""
+        x = _as_f32_2d(input, "input", self.n_input)
+        y = _as_f32_2d(target, "target", self.n_output)
+        if x.shape[0] != y.shape[0]:
+            raise ValueError("input and target must have matching batch_size")
         with self._enter("training_step"):
             res = _lib.StepResult()
             _lib.check(self._lib.tmnn_training_step(self._h, _ptr(x), _ptr(y), x.shape[0],
                                                     ctypes.byref(res)))
-            return float(res.loss)
+            return res.to_dict()
+
+    def set_numerics_sampling(self, mode: str = "Sampled", interval: int = 128) -> None:
+        """NumericsSamplingMode ("Sampled", "Periodic", "FullPerStep",
+        "Disabled") and sample interval (runtime_policy.h:13-38)."""
+        if mode not in _lib.NUMERICS_MODES:
+            raise ValueError(f"unknown numerics sampling mode {mode!r}")
+        with self._enter("set_numerics_sampling"):
+            _lib.check(self._lib.tmnn_set_numerics_sampling(self._h, _lib.NUMERICS_MODES[mode],
+                                                            int(interval)))
+
+    def last_numerics(self) -> dict:
+        """Report of the last step whose numerics were computed (waits for the
+        trainer's stream): every host-pointer step, sampled device steps."""
+        with self._enter("last_numerics"):
+            res = _lib.StepResult()
+            _lib.check(self._lib.tmnn_get_last_numerics(self._h, ctypes.byref(res)))
+            return res.to_dict()
+
+    def debug_step_outputs(self, input, target) -> tuple[np.ndarray, dict]:
+        """A regular fused step that also returns the outputs its training
+        kernel computed ((N, n_output), caller row order) and the step result."""
+        x = _as_f32_2d(input, "input", self.n_input)
+        y = _as_f32_2d(target, "target", self.n_output)
+        n = min(x.shape[0], self.config["batch_size"])
+        out = np.empty((n, self.n_output), np.float32)
+        with self._enter("debug_step_outputs"):
+            res = _lib.StepResult()
+            _lib.check(self._lib.tmnn_debug_step_outputs(self._h, _ptr(x), _ptr(y), x.shape[0],
+                                                         _ptr(out), ctypes.byref(res)))
+            return out, res.to_dict()
+
+    def training_step_device_after(self, input_ptr: int, target_ptr: int, n: int,
+                                   wait_event=None, loss_ptr: int = 0) -> None:
+        """training_step_device ordered after a caller's HIP event (an object
+        with a ctypes `_as_parameter_`, e.g. torch.cuda.Event, or a raw
+        pointer); the trainer's streams wait for it before reading the batch."""
+        with self._enter("training_step_device_after"):
+            _lib.check(self._lib.tmnn_training_step_device_after(
+                self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(target_ptr), int(n),
+                ctypes.c_void_p(loss_ptr) if loss_ptr else None, _event_arg(wait_event)))
+
+    def inference_device_after(self, input_ptr: int, output_ptr: int, n: int,
+                               wait_event=None) -> None:
+        with self._enter("inference_device_after"):
+            _lib.check(self._lib.tmnn_inference_device_after(
+                self._h, ctypes.c_void_p(input_ptr), ctypes.c_void_p(output_ptr), int(n),
+                _event_arg(wait_event)))
+
+    def record_event(self, event) -> None:
+        """Record a caller's HIP event on the trainer's stream after every call
+        enqueued so far (outputs of *_device calls are complete when it is)."""
+        with self._enter("record_event"):
+            _lib.check(self._lib.tmnn_record_event(self._h, _event_arg(event)))
 
     def training_step_device(self, input_ptr: int, target_ptr: int, n: int,
                              loss_ptr: int = 0) -> None:
@@ -333,6 +412,26 @@ class Trainer:
         with self._enter("training_step_profile"):
             _lib.check(self._lib.tmnn_get_step_profile(self._h, ctypes.byref(p)))
         return {k: getattr(p, k) for k, _ in _lib.StepProfile._fields_}
+
+    def training_step_profile_samples(self) -> np.ndarray:
+        """Per profiled step (rows, step order) the phase GPU microseconds,
+        columns as _lib.PROFILE_PHASES."""
+        with self._enter("training_step_profile_samples"):
+            cnt = ctypes.c_uint32()
+            _lib.check(self._lib.tmnn_get_step_profile_samples(self._h, None, 0, ctypes.byref(cnt)))
+            out = np.zeros((cnt.value, len(_lib.PROFILE_PHASES)), np.float32)
+            if cnt.value:
+                _lib.check(self._lib.tmnn_get_step_profile_samples(self._h, _ptr(out), cnt.value,
+                                                                   ctypes.byref(cnt)))
+        return out
+
+    def debug_lds_rate(self, reps: int = 10) -> float:
+        """LDS read bandwidth of this trainer's device, bytes/s
+        (tmnn_debug_lds_rate)."""
+        b = ctypes.c_double()
+        with self._enter("debug_lds_rate"):
+            _lib.check(self._lib.tmnn_debug_lds_rate(self._ctx.handle, int(reps), ctypes.byref(b)))
+        return b.value
 
     # ---- runtime authority (RuntimeAuthority / batch_plan) ----------------------
     def runtime_buffer(self, role: str) -> dict:
