@@ -29,13 +29,21 @@ def _say(msg: str) -> None:
     sys.stdout.flush()
 
 
-def _update_check(got, before, g, lr, what):
+# Hash-table gradients are sums of int32(trunc(d * w * 65536)) per corner
+# contribution: besides the fp16 bar on d (2e-3 of the largest gradient),
+# each contribution whose fp32 and fp16 values straddle an integer truncates
+# differently, one unit of 2^-16 each; the fp32 fused-step test allows 16 such
+# units per entry and so does this one.
+G_ULP = 16.0 / 65536.0
+
+
+def _update_check(got, before, g, lr, what, slack=0.0):
     """One Adam step from zero moments moves each parameter by lr * g / |g|
-    (up to fp32 rounding): where the oracle's gradient is not small against
-    the tensor's largest (|g| >= 2e-3 max|g|, so an fp16 gradient cannot
-    change its sign) the new parameter equals the oracle's within 1e-6;
-    elsewhere a sign can differ, and the step is still at most lr."""
-    big = np.abs(g) >= 2e-3 * np.abs(g).max()
+    (up to fp32 rounding): where the oracle's gradient is larger than the
+    fp16 tolerance (2e-3 max|g| + slack), so that the GPU's cannot have the
+    other sign or be zero, the new parameter equals the oracle's within 1e-6;
+    elsewhere the step is still at most lr."""
+    big = np.abs(g) > 2e-3 * np.abs(g).max() + slack
     d = np.abs(got.astype(np.float64) - (before.astype(np.float64) - lr * np.sign(g)))
     assert d[big].max() <= 1e-6, (what, d[big].max())
     step = np.abs(got.astype(np.float64) - before.astype(np.float64))
@@ -78,16 +86,23 @@ def test_one_fused_fp16_step_state_matches_oracle(oracle, name):
         hw1, mw1 = tr.get_weights()
         assert rel_tensor(mm, m1[nh:]) <= 2e-3
         assert rel_tensor(vm, m2[nh:]) <= 2e-3
-        assert rel_tensor(mh, m1[:nh]) <= 2e-3
-        assert rel_tensor(vh, m2[:nh]) <= 2e-3
         g = m1 / (1.0 - BETA1)  # the oracle's gradients (first step: m = (1 - beta1) g)
+        gh_max = float(np.abs(g[:nh]).max())
+        delta = 2e-3 * gh_max + G_ULP  # per-entry hash gradient bound
+        dm = np.abs(mh.astype(np.float64) - m1[:nh])
+        dv = np.abs(vh.astype(np.float64) - m2[:nh])
+        _say(f"  hash m: max|diff| {dm.max() / (1 - BETA1) * 65536:.2f} units of 2^-16 "
+             f"(largest gradient {gh_max * 65536:.1f} units), exact on {(dm == 0).mean():.6f}")
+        assert dm.max() <= (1 - BETA1) * delta * 1.01
+        assert dv.max() <= (1 - BETA2) * delta * (2 * gh_max + delta) * 1.01
         _update_check(mw1, mw, g[nh:], LR, "mlp")
-        _update_check(hw1, hw, g[:nh], LR, "hash")
+        _update_check(hw1, hw, g[:nh], LR, "hash", G_ULP)
         touched_gpu, touched_orc = mh != 0, m1[:nh] != 0
         differ = touched_gpu != touched_orc
-        tiny = np.maximum(np.abs(mh), np.abs(m1[:nh])) <= 2e-3 * np.abs(m1[:nh]).max()
+        tiny = np.maximum(np.abs(mh), np.abs(m1[:nh])) <= (1 - BETA1) * delta * 1.01
         assert not (differ & ~tiny).any()
         _say(f"  touched sets agree on {1.0 - differ.mean():.6f} of {nh} entries")
+        assert 1.0 - differ.mean() >= 0.999
         # untouched entries keep their weights bit for bit (lazy hash Adam)
         keep = ~touched_gpu & ~touched_orc
         assert np.array_equal(hw1[keep], hw[keep])
@@ -98,11 +113,11 @@ def test_one_fused_fp16_step_state_matches_oracle(oracle, name):
         assert nr["max_abs_activation"] == np.abs(out).max()
         du = np.abs(np.concatenate([hw, mw]) - np.concatenate([hw1, mw1]))
         assert nr["max_abs_update"] == du.max()
-        # the report's gradient terms come from the GPU's own fp16 gradients
-        gmax = np.abs(g).max()
-        assert nr["max_abs_gradient"] == pytest.approx(gmax, rel=2e-3)
-        assert res["grad_norm"] == pytest.approx(np.sqrt((g.astype(np.float64) ** 2).sum()),
-                                                 rel=5e-3)
+        # the report's gradient terms are those of the gradients the step
+        # applied, which its first moments hold (m = (1 - beta1) g on step 1)
+        g_gpu = np.concatenate([mh, mm]).astype(np.float64) / (1.0 - BETA1)
+        assert nr["max_abs_gradient"] == pytest.approx(np.abs(g_gpu).max(), rel=1e-5)
+        assert res["grad_norm"] == pytest.approx(np.sqrt((g_gpu ** 2).sum()), rel=1e-4)
 
 
 def test_c5_step_at_baseline_geometry(oracle):

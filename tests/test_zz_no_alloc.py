@@ -3,9 +3,11 @@ against the existing device entry point (tmnn_training_step_device) through
 the C-ABI: two trainers from the same seed take the same batches, one
 through each entry point, two calls in a row (the second with a smaller
 batch); losses and every parameter are bit-identical (the kernels and their
-order are the same). A second case alternates the two entry points on one
-trainer, which also meets the regular step's side-stream sort sets. Marked
-gpu."""
+order are the same), except for the Tiled family's generic kernel, whose
+LDS weight-gradient accumulator adds with atomics in arrival order (loss and
+weights within 1e-6 there). A second case alternates the two entry points on
+one trainer, which also meets the regular step's side-stream sort sets.
+Marked gpu."""
 from __future__ import annotations
 
 import sys
@@ -56,13 +58,18 @@ def test_noalloc_step_matches_device_step(case):
             ref.synchronize()
             tr.synchronize()
             a, b = loss_ref[i].item(), loss_na[i].item()
-            assert np.isfinite(a) and a == b, (i, a, b)
             hr, mr = ref.get_weights()
             hn, mn = tr.get_weights()
-            assert np.array_equal(mn, mr) and np.array_equal(hn, hr), (
-                i, rel_tensor(mn, mr), rel_tensor(hn, hr))
+            if family == "Tiled":  # order-dependent LDS atomics in the dW accumulator
+                assert np.isfinite(a) and b == pytest.approx(a, rel=1e-6, abs=0.0), (i, a, b)
+                assert rel_tensor(mn, mr) <= 1e-6 and rel_tensor(hn, hr) <= 1e-6, i
+            else:
+                assert np.isfinite(a) and a == b, (i, a, b)
+                assert np.array_equal(mn, mr) and np.array_equal(hn, hr), (
+                    i, rel_tensor(mn, mr), rel_tensor(hn, hr))
             assert tr.step() == ref.step() == i + 1
-            _say(f"  call {i} n={n}: loss {a:.6f}, weights bit-identical")
+            _say(f"  call {i} n={n}: loss {a:.6f} / {b:.6f}, weights bit-identical "
+                 f"{np.array_equal(mn, mr) and np.array_equal(hn, hr)}")
 
 
 def test_noalloc_alternating_with_regular_steps_on_one_trainer():
