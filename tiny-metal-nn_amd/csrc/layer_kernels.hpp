@@ -8,16 +8,20 @@
 // KernelSpec shape (kernel_spec.cpp:12-44) runs.
 //
 // Products: C[r][c] = sum_k A(r, k) B(k, c) over 64 x 64 output tiles (row
-// tiles along blockIdx.x, column tiles along blockIdx.y), K in
-// steps of 16 staged through LDS, each thread 4 x 4 outputs in fp32 FMA. The
+// tiles along blockIdx.x, column tiles along blockIdx.y), K in steps of 16
+// staged through LDS, each of the block's four waves a 32 x 32 quadrant on
+// the matrix cores (v_mfma_f32_16x16x4_f32: fp32 operands, fp32
+// accumulation). The
 // operands are read in place: activations row-major, the input features as
 // X tiles (encode_kernel.hpp), the weights in the reference layout
 // W[in][out] (the backward reads them transposed), and for the weight
 // gradients the activations / deltas transposed with the points along K,
 // one partial row per chunk of the batch (the rows finish_step_kernel /
-// reduce_partials_kernel reduce in a fixed order). Epilogues fuse the bias
-// and ReLU (forward), the ReLU derivative [h > 0] of the stored activation
-// (backward), and the output scale.
+// reduce_partials_kernel reduce in a fixed order); the bias gradients are
+// the same product with an extra all-ones row of A (the reference layout
+// stores b right after W, so that row lands in the bias slots). Epilogues
+// fuse the bias and ReLU (forward), the ReLU derivative [h > 0] of the
+// stored activation (backward), and the output scale.
 #pragma once
 
 #include "encode_kernel.hpp"
@@ -60,6 +64,7 @@ struct LwGemmArgs {
   float *dst;                 // kLwEpiPartial
   int64_t dst_stride;
   int32_t dst_off;
+  int32_t ones_row;           // 1: A's last row (r == R - 1) is all ones (bias gradients)
 };
 
 constexpr int kLwTile = 64;
@@ -69,6 +74,7 @@ constexpr int kLwForwardChunk = 1 << 18;
 constexpr int kLwK = 16;
 
 __device__ __forceinline__ float lw_a(const LwGemmArgs &g, int r, int k) {
+  if (g.ones_row && r == g.R - 1) return 1.0f;
   switch (g.a_mode) {
     case kLwARow: return g.A[static_cast<size_t>(r) * g.lda + k];
     case kLwACol: return g.A[static_cast<size_t>(k) * g.lda + r];
@@ -81,96 +87,135 @@ __device__ __forceinline__ float lw_b(const LwGemmArgs &g, int k, int c) {
   return g.b_trans ? g.B[static_cast<size_t>(c) * g.ldb + k] : g.B[static_cast<size_t>(k) * g.ldb + c];
 }
 
+// LDS staging of one K step: row (or column) i of the tile holds its kLwK
+// operands contiguously (kLwKP floats per row: 16-byte aligned and padded),
+// so each lane reads the four K values of an MFMA A or B operand with one
+// ds_read_b128.
+constexpr int kLwKP = kLwK + 4;
+constexpr int kLwStage = kLwTile * kLwK / 256;  // operand elements per thread and K step
+
 __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
-  __shared__ float As[kLwK][kLwTile + 4];
-  __shared__ float Bs[kLwK][kLwTile + 4];
+  // the tile's A rows and B columns of the current K step, K innermost
+  __shared__ __align__(16) float As[kLwTile * kLwKP];
+  __shared__ __align__(16) float Bs[kLwTile * kLwKP];
   const int tid = threadIdx.x;
-  const int tx = tid & 15, ty = tid >> 4;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int p = lane & 15, q = lane >> 4;
+  // wave w computes the 32 x 32 quadrant (rows (w & 1) * 32, columns
+  // (w >> 1) * 32) of the 64 x 64 tile: 2 x 2 MFMA tiles of 16 x 16
+  const int wr = (wave & 1) * 32, wc = (wave >> 1) * 32;
   const int r0 = blockIdx.x * kLwTile, c0 = blockIdx.y * kLwTile;
   const int kb = blockIdx.z * g.k_chunk;
   const int ke = min(g.K, kb + g.k_chunk);
-  float acc[4][4];
+  f32x4 acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-  for (int k0 = kb; k0 < ke; k0 += kLwK) {
-    // stage a 64 x 16 slice of A and a 16 x 64 slice of B (zero outside)
-    // (consecutive threads walk the operand's contiguous index)
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Operand staging, software-pipelined: the next K step's slices are read
+  // from global memory into registers before the current step's products
+  // and stored to LDS after them. Consecutive threads walk the operand's
+  // contiguous index; elements outside the product are zero.
+  const bool a_k_fast = g.a_mode == kLwARow, b_k_fast = g.b_trans != 0;
+  float ra[kLwStage], rb[kLwStage];
+  auto load = [&](int k0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < kLwStage; ++e) {
       const int idx = tid + 256 * e;
-      const bool a_k_fast = g.a_mode == kLwARow;
-      const int rr = a_k_fast ? idx >> 4 : idx & 63, kk = a_k_fast ? idx & 15 : idx >> 6;
+      const int rr = a_k_fast ? idx / kLwK : idx % kLwTile;
+      const int kk = a_k_fast ? idx % kLwK : idx / kLwTile;
       const int r = r0 + rr, k = k0 + kk;
-      As[kk][rr] = (r < g.R && k < ke) ? lw_a(g, r, k) : 0.0f;
-      const int cc = g.b_trans ? idx >> 4 : idx & 63, kb2 = g.b_trans ? idx & 15 : idx >> 6;
-      const int c = c0 + cc, k2 = k0 + kb2;
-      Bs[kb2][cc] = (c < g.C && k2 < ke) ? lw_b(g, k2, c) : 0.0f;
+      ra[e] = (r < g.R && k < ke) ? lw_a(g, r, k) : 0.0f;
+      const int cc = b_k_fast ? idx / kLwK : idx % kLwTile;
+      const int kc = b_k_fast ? idx % kLwK : idx / kLwTile;
+      const int c = c0 + cc, k2 = k0 + kc;
+      rb[e] = (c < g.C && k2 < ke) ? lw_b(g, k2, c) : 0.0f;
     }
-    __syncthreads();
+  };
+  auto store = [&]() {
 #pragma unroll
-    for (int kk = 0; kk < kLwK; ++kk) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    for (int e = 0; e < kLwStage; ++e) {
+      const int idx = tid + 256 * e;
+      const int rr = a_k_fast ? idx / kLwK : idx % kLwTile;
+      const int kk = a_k_fast ? idx % kLwK : idx / kLwTile;
+      As[rr * kLwKP + kk] = ra[e];
+      const int cc = b_k_fast ? idx / kLwK : idx % kLwTile;
+      const int kc = b_k_fast ? idx % kLwK : idx / kLwTile;
+      Bs[cc * kLwKP + kc] = rb[e];
     }
-    __syncthreads();
+  };
+  if (kb < ke) {
+    load(kb);
+    store();
   }
+  __syncthreads();
+  for (int k0 = kb; k0 < ke; k0 += kLwK) {
+    const bool more = k0 + kLwK < ke;  // uniform over the block
+    if (more) load(k0 + kLwK);
+    // v_mfma_f32_16x16x4_f32: lane p + 16 q supplies A[row p][k] and
+    // B[k][column p] of K slot q; the four MFMAs of a 16-wide K group take K
+    // values 16 h + 4 q + e (e = 0..3), one ds_read_b128 per operand tile
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = r0 + ty * 4 + i;
-    if (r >= g.R) continue;
+    for (int h = 0; h < kLwK / 16; ++h) {
+      f32x4 av[2], bv[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = c0 + tx * 4 + j;
-      if (c >= g.C) continue;
-      const float v = acc[i][j];
-      switch (g.epi) {
-        case kLwEpiHidden:
-          g.out[static_cast<size_t>(r) * g.ldo + c] = fmaxf(v + g.bias[c], 0.0f);
-          break;
-        case kLwEpiOutput: {
-          const float y = v + g.bias[c];
-          if (g.out) {
-            const size_t row = g.out_index ? g.out_index[r] : static_cast<uint32_t>(r);
-            g.out[row * g.ldo + c] = y;
+      for (int i = 0; i < 2; ++i)
+        av[i] = *reinterpret_cast<const f32x4 *>(As + (wr + 16 * i + p) * kLwKP + 16 * h + 4 * q);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bv[j] = *reinterpret_cast<const f32x4 *>(Bs + (wc + 16 * j + p) * kLwKP + 16 * h + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      store();
+      __syncthreads();
+    }
+  }
+  // D layout: lane p + 16 q holds rows 4 q + rr, column p of each 16 x 16 tile
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int r = r0 + wr + 16 * i + 4 * q + rr;
+      if (r >= g.R) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = c0 + wc + 16 * j + p;
+        if (c >= g.C) continue;
+        const float v = acc[i][j][rr];
+        switch (g.epi) {
+          case kLwEpiHidden:
+            g.out[static_cast<size_t>(r) * g.ldo + c] = fmaxf(v + g.bias[c], 0.0f);
+            break;
+          case kLwEpiOutput: {
+            const float y = v + g.bias[c];
+            if (g.out) {
+              const size_t row = g.out_index ? g.out_index[r] : static_cast<uint32_t>(r);
+              g.out[row * g.ldo + c] = y;
+            }
+            if (g.out2) g.out2[static_cast<size_t>(r) * g.ldo2 + c] = y;
+            break;
           }
-          if (g.out2) g.out2[static_cast<size_t>(r) * g.ldo2 + c] = y;
-          break;
+          case kLwEpiMask:
+            g.out[static_cast<size_t>(r) * g.ldo + c] =
+                g.mask[static_cast<size_t>(r) * g.ldm + c] > 0.0f ? v : 0.0f;
+            break;
+          case kLwEpiScale:
+            g.out[static_cast<size_t>(r) * g.ldo + c] = v * g.scale;
+            break;
+          default:
+            g.dst[blockIdx.z * g.dst_stride + g.dst_off + static_cast<int64_t>(r) * g.C + c] = v;
+            break;
         }
-        case kLwEpiMask:
-          g.out[static_cast<size_t>(r) * g.ldo + c] =
-              g.mask[static_cast<size_t>(r) * g.ldm + c] > 0.0f ? v : 0.0f;
-          break;
-        case kLwEpiScale:
-          g.out[static_cast<size_t>(r) * g.ldo + c] = v * g.scale;
-          break;
-        default:
-          g.dst[blockIdx.z * g.dst_stride + g.dst_off + static_cast<int64_t>(r) * g.C + c] = v;
-          break;
       }
     }
-  }
-}
-
-// dst[z * dst_stride + dst_off + c] = sum over the rows of chunk z of
-// D[row][c] (bias gradients: column sums of a layer's deltas), rows in order.
-__global__ void __launch_bounds__(256) lw_colsum_kernel(const float *D, int32_t ldd, int32_t rows,
-                                                        int32_t cols, int32_t chunk, float *dst,
-                                                        int64_t dst_stride, int32_t dst_off) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  const int r0 = blockIdx.y * chunk, r1 = min(rows, r0 + chunk);
-  float s = 0.0f;
-  for (int r = r0; r < r1; ++r) s += D[static_cast<size_t>(r) * ldd + c];
-  dst[blockIdx.y * dst_stride + dst_off + c] = s;
 }
 
 struct LwLossArgs {

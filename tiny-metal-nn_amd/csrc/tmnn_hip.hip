@@ -518,11 +518,12 @@ ModelShape shape_of(const tmnn_model_desc &d) {
 // family's kernel for the shape, waves per block, LDS bytes against
 // lds_limit. Returns false with *why when the family has no kernel or its
 // LDS plan does not fit.
-// Batch chunks (partial dW rows) of the layer-wise path: at most 64, and at
-// most 64 MiB of partial rows.
+// Batch chunks (partial dW rows) of the layer-wise path: at most 256 (one
+// weight-gradient block per CU and 64 x 64 output tile at least), and at most
+// 64 MiB of partial rows.
 int lw_max_chunks(int mlp_count) {
   const int by_mem = static_cast<int>((64u << 20) / (4u * static_cast<unsigned>(std::max(1, mlp_count))));
-  return std::max(1, std::min(64, by_mem));
+  return std::max(1, std::min(256, by_mem));
 }
 
 bool size_plan_fused(const ModelShape &m, bool f16, bool train, int family, int lds_limit,
@@ -1051,10 +1052,14 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
   const bool wgrads = a.mode != kModeInputGrad;
   const int64_t row = a.mlp_count;
   float *dbuf[2] = {tr->lw_d.as<float>(), tr->lw_d.as<float>() + N * H};
+  // dW_k and b_k of one layer as one product: A's extra all-ones row (r = R)
+  // writes the column sums of D into row R of the partial, which is b_k's
+  // slot (b_off = w_off + R * C in the reference layout)
   auto partial_dw = [&](const float *A, int a_mode, int lda, int R, const float *D, int C,
-                        int w_off, int b_off) -> int {
+                        int w_off) -> int {
     LwGemmArgs g = base;
-    g.R = R;
+    g.R = R + 1;
+    g.ones_row = 1;
     g.C = C;
     g.K = n;
     g.k_chunk = chunk;
@@ -1067,12 +1072,7 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
     g.dst = a.grad_partials;
     g.dst_stride = row;
     g.dst_off = w_off;
-    int r = gemm(g, P);
-    if (r != TMNN_OK) return r;
-    hipLaunchKernelGGL(lw_colsum_kernel, dim3((C + 255) / 256, P), dim3(256), 0, st, D, C, n, C,
-                       chunk, a.grad_partials, row, b_off);
-    TMNN_HIP_TRY(hipGetLastError());
-    return TMNN_OK;
+    return gemm(g, P);
   };
   const float *dcur = tr->lw_g.as<float>();  // gradient at the current layer's output
   int dcols = M;
@@ -1080,10 +1080,9 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
     // layer k maps its input (X for k = 0, else h_{k-1}) to dcur
     if (wgrads) {
       if (k > 0)
-        rc = partial_dw(act_k(k - 1), kLwACol, H, H, dcur, dcols, lay.w_off(k), lay.b_off(k));
+        rc = partial_dw(act_k(k - 1), kLwACol, H, H, dcur, dcols, lay.w_off(k));
       else
-        rc = partial_dw(tr->xfeat.as<float>(), kLwAXTilesT, 0, IN, dcur, dcols, lay.w_off(0),
-                        lay.b_off(0));
+        rc = partial_dw(tr->xfeat.as<float>(), kLwAXTilesT, 0, IN, dcur, dcols, lay.w_off(0));
       if (rc != TMNN_OK) return rc;
     }
     LwGemmArgs g = base;
