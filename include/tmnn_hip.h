@@ -320,8 +320,11 @@ int tmnn_get_last_numerics(tmnn_trainer *tr, tmnn_step_result *out);
  * the C2 image-fit step (2D, 16x2 features, 3 outputs) fits 2^18 points.
  * Larger batches return TMNN_ERR_INVALID_ARGUMENT; hidden width 128 and the
  * layer-wise (Tiled) path return TMNN_ERR_UNSUPPORTED. Steps are not
- * profiled. Every call on one GPU shares that GPU's scratch: calls that
- * overlap on one GPU (trainers on different streams) race. */
+ * profiled. Every call on one GPU shares that GPU's scratch, which keeps the
+ * last call's contents: calls from trainers on different streams of one GPU
+ * are ordered by a per-device event (each waits for the previous call's
+ * kernels before its first kernel), so they take the scratch in turn;
+ * enqueue them from one host thread at a time per device. */
 int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
                                       const float *d_target, int32_t n,
                                       float *d_loss_out);
