@@ -20,9 +20,10 @@ starts.
 
 The timed region runs the K steps exactly as a caller runs them (no
 profiling events). After it, PROFILED_STEPS more steps run with timing-only
-HIP events around every phase of every step (tmnn_get_step_profile_samples);
-the MEDIAN of those per-step phase times is each kernel's duration behind
-`phase_us_per_step`, the roofline fractions (`kernel_rooflines`) and
+HIP events around every phase of every step and start / stop events recorded
+by the main kernels' own dispatches (tmnn_get_step_profile_samples); the
+MEDIAN of those per-step kernel durations is each kernel's duration behind
+`phase_us_median`, the roofline fractions (`kernel_rooflines`) and
 `roofline` (the MLP training kernel: max(FLOPs / fp16 MFMA peak, LDS bytes /
 LDS peak) over its duration, the LDS peak measured in the same run by
 tmnn_debug_lds_rate). The same statistic over the same kernel's dispatches
@@ -177,7 +178,8 @@ def lds_bytes_per_launch(kernel: str, n: int, inp: int, nhl: int, waves: int) ->
 
 
 def median_phases(samples) -> dict:
-    """Per-phase medians of the per-step samples (rows = steps)."""
+    """Per-column medians of the per-step samples (rows = steps): the step's
+    phases and its main kernels' own durations."""
     from tiny_metal_nn._lib import PROFILE_PHASES
     if len(samples) == 0:
         return {k: 0.0 for k in PROFILE_PHASES}
@@ -199,11 +201,15 @@ def kernel_rooflines(phase_us: dict, models: dict, names: dict, n: int, fused_sc
     input width, hidden layers, waves per block)."""
     out = []
     mfma_peak = FP32_MFMA_PEAK_TFLOPS if fp32 else MFMA_F16_PEAK_TFLOPS
-    for key, phase in (("encode", "gpu_encode_us"), ("mlp", "gpu_fwd_bwd_us"),
-                       ("scatter", "gpu_scatter_us"), ("adam", "gpu_adam_us")):
+    for key, phase, kern in (("encode", "gpu_encode_us", "gpu_encode_kernel_us"),
+                             ("mlp", "gpu_fwd_bwd_us", "gpu_train_kernel_us"),
+                             ("scatter", "gpu_scatter_us", "gpu_scatter_kernel_us"),
+                             ("adam", "gpu_adam_us", "gpu_finish_kernel_us")):
         if key == "scatter" and fused_scatter:
             continue
-        us = phase_us[phase]
+        # the kernel's own duration (dispatch timestamps); the phase (which
+        # also holds the launch gap) where the step runs several kernels
+        us = phase_us.get(kern, 0.0) or phase_us[phase]
         if us <= 0:
             continue
         model = models[key]

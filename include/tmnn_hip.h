@@ -529,6 +529,13 @@ typedef struct tmnn_step_profile {
   double gpu_encode_us;       /* hash-grid encode forward (features of the batch) */
   uint32_t infer_calls;       /* profiled inference calls summed below */
   double gpu_infer_us;        /* the inference forward kernel (tmnn_inference[_device]) */
+  /* the step's main kernels alone, from their dispatches' own start and end
+   * timestamps (a phase above also holds the launch gap before its kernel);
+   * 0 where the step has no such kernel or (layer-wise path) runs several */
+  double gpu_encode_kernel_us;
+  double gpu_train_kernel_us;   /* the MLP training kernel (with the fused hash-grid backward) */
+  double gpu_scatter_kernel_us;
+  double gpu_finish_kernel_us;
 } tmnn_step_profile;
 
 /* enabled: 0 off; k >= 1 profiles one training step in k (the first after
@@ -538,12 +545,14 @@ typedef struct tmnn_step_profile {
 int tmnn_set_step_profiling(tmnn_trainer *tr, int32_t enabled);
 int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
 
-/* Per-step phase times (GPU microseconds) of the profiled training steps
- * since profiling was (re-)enabled, in step order: row i holds
- * TMNN_PROFILE_PHASES floats indexed by TMNN_PROFILE_*. *count receives the
- * number of profiled steps; at most `capacity` rows are written (out may be
- * NULL to query). Waits for the stream. A phase without work (the fused
- * step's scatter and reduce phases) reads 0. */
+/* Per-step times (GPU microseconds) of the profiled training steps since
+ * profiling was (re-)enabled, in step order: row i holds
+ * TMNN_PROFILE_COLUMNS floats indexed by TMNN_PROFILE_*: the phases, their
+ * total, then the main kernels alone (as the *_kernel_us fields of
+ * tmnn_step_profile). *count receives the number of profiled steps; at most
+ * `capacity` rows are written (out may be NULL to query). Waits for the
+ * stream. A phase or kernel without work (the fused step's scatter and
+ * reduce phases and scatter kernel) reads 0. */
 #define TMNN_PROFILE_SORT 0
 #define TMNN_PROFILE_ENCODE 1
 #define TMNN_PROFILE_FWD_BWD 2
@@ -551,7 +560,11 @@ int tmnn_get_step_profile(tmnn_trainer *tr, tmnn_step_profile *out);
 #define TMNN_PROFILE_REDUCE 4
 #define TMNN_PROFILE_ADAM 5
 #define TMNN_PROFILE_TOTAL 6
-#define TMNN_PROFILE_PHASES 7
+#define TMNN_PROFILE_KERNEL_ENCODE 7
+#define TMNN_PROFILE_KERNEL_TRAIN 8
+#define TMNN_PROFILE_KERNEL_SCATTER 9
+#define TMNN_PROFILE_KERNEL_FINISH 10
+#define TMNN_PROFILE_COLUMNS 11
 int tmnn_get_step_profile_samples(tmnn_trainer *tr, float *out, uint32_t capacity,
                                   uint32_t *count);
 

@@ -582,3 +582,10 @@ def test_fused_step_profile_phases():
         parts = sum(prof[k] for k in ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us",
                                       "gpu_scatter_us", "gpu_reduce_us", "gpu_adam_us"))
         assert abs(parts - prof["gpu_total_us"]) <= 1e-3 * prof["gpu_total_us"], prof
+        # the main kernels' own durations (dispatch timestamps): positive, no
+        # scatter kernel, and each within its phase (which adds the launch gap)
+        assert prof["gpu_scatter_kernel_us"] == 0.0, prof
+        for kern, phase in (("gpu_encode_kernel_us", "gpu_encode_us"),
+                            ("gpu_train_kernel_us", "gpu_fwd_bwd_us"),
+                            ("gpu_finish_kernel_us", "gpu_adam_us")):
+            assert 0.0 < prof[kern] <= prof[phase] * 1.001, (kern, phase, prof)

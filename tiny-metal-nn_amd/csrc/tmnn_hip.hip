@@ -7,6 +7,7 @@
 //   (lazy hash + dense MLP) -> gradients and mask cleared -> step + 1.
 // Everything after the input copy runs on the trainer's HIP stream with no
 // host round trip; the host waits once, for the loss.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -312,9 +313,14 @@ struct tmnn_trainer {
   // recycled when the profile is read. prof_every: 0 off, k >= 1 one training
   // step in k (the first, then every k-th); prof_seen counts steps since on.
   static constexpr int kProfEvents = 7;  // sort | encode | fwd/bwd | scatter | reduce | adam |
+  // per profiled step also the start / stop events of its main kernels
+  // (encode, training kernel, scatter, finish), recorded by the dispatches
+  // themselves (launch_step_kernel)
+  static constexpr int kProfKernels = 4;
+  static constexpr int kProfSet = kProfEvents + 2 * kProfKernels;
   int32_t prof_every = 0;
   uint64_t prof_seen = 0;
-  std::vector<std::array<hipEvent_t, kProfEvents>> prof_events;
+  std::vector<std::array<hipEvent_t, kProfSet>> prof_events;
   // per event set: bit k set when boundary k was recorded; a boundary with
   // no work before it (the fused step's scatter and reduce phases) is not
   // recorded and reads as the previous one (a zero-length phase)
@@ -324,7 +330,7 @@ struct tmnn_trainer {
   bool prof_suspended = false;  // allocation-free steps record no events
   tmnn_step_profile prof_acc{};
   // per profiled step, in step order: the phase times (TMNN_PROFILE_*)
-  std::vector<std::array<float, TMNN_PROFILE_PHASES>> prof_samples;
+  std::vector<std::array<float, TMNN_PROFILE_COLUMNS>> prof_samples;
   // inference calls while profiling is on: one event pair around the
   // forward kernel of one call in prof_every
   uint64_t prof_infer_seen = 0;
@@ -407,7 +413,7 @@ int prof_begin_step(tmnn_trainer *tr) {
   if (tr->prof_every <= 0 || tr->prof_suspended) return TMNN_OK;
   if (tr->prof_seen++ % static_cast<uint64_t>(tr->prof_every) != 0) return TMNN_OK;
   if (tr->prof_used == tr->prof_events.size()) {
-    std::array<hipEvent_t, tmnn_trainer::kProfEvents> set{};
+    std::array<hipEvent_t, tmnn_trainer::kProfSet> set{};
     // timing-only events: no system-scope fence (cache writeback and
     // invalidate) at each record; prof_collect synchronizes the stream first
     for (hipEvent_t &e : set)
@@ -427,6 +433,25 @@ int prof_mark(tmnn_trainer *tr, int k) {
   tr->prof_recorded[tr->prof_cur] |= 1u << k;
   return TMNN_OK;
 }
+
+// The step's main kernels (kernel index k: 0 encode, 1 training kernel, 2
+// scatter, 3 finish): on a profiled step launched with start / stop events
+// that the dispatch itself records (hipExtLaunchKernel), i.e. the kernel's
+// own begin and end as a kernel trace reports them, without the launch
+// latency the phase boundaries include; otherwise a plain launch.
+template <typename K, typename... Args>
+void launch_step_kernel(tmnn_trainer *tr, int k, K kernel, dim3 grid, dim3 block, uint32_t shm,
+                        hipStream_t st, Args... args) {
+  if (tr->prof_cur >= 0) {
+    auto &e = tr->prof_events[tr->prof_cur];
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, st, e[tmnn_trainer::kProfEvents + 2 * k],
+                          e[tmnn_trainer::kProfEvents + 2 * k + 1], 0u, args...);
+    tr->prof_recorded[tr->prof_cur] |= 1u << (tmnn_trainer::kProfEvents + k);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, st, args...);
+  }
+}
+enum : int { kKernEncode = 0, kKernTrain = 1, kKernScatter = 2, kKernFinish = 3 };
 
 // Claims an event pair for a profiled inference call (nullptr when this
 // call is not sampled).
@@ -469,14 +494,27 @@ int prof_collect(tmnn_trainer *tr) {
       ms[k] = 0.0f;
       if (at[k] != at[k + 1]) TMNN_HIP_TRY(hipEventElapsedTime(&ms[k], e[at[k]], e[at[k + 1]]));
     }
+    float kms[tmnn_trainer::kProfKernels];
+    for (int k = 0; k < tmnn_trainer::kProfKernels; ++k) {
+      kms[k] = 0.0f;
+      if (tr->prof_recorded[i] & (1u << (tmnn_trainer::kProfEvents + k)))
+        TMNN_HIP_TRY(hipEventElapsedTime(&kms[k], e[tmnn_trainer::kProfEvents + 2 * k],
+                                         e[tmnn_trainer::kProfEvents + 2 * k + 1]));
+    }
     {
-      std::array<float, TMNN_PROFILE_PHASES> smp{};
+      std::array<float, TMNN_PROFILE_COLUMNS> smp{};
       for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k) smp[k] = 1e3f * ms[k];
       float total = 0.0f;
       for (int k = 0; k + 1 < tmnn_trainer::kProfEvents; ++k) total += smp[k];
       smp[TMNN_PROFILE_TOTAL] = total;
+      for (int k = 0; k < tmnn_trainer::kProfKernels; ++k)
+        smp[TMNN_PROFILE_KERNEL_ENCODE + k] = 1e3f * kms[k];
       tr->prof_samples.push_back(smp);
     }
+    tr->prof_acc.gpu_encode_kernel_us += 1e3 * kms[0];
+    tr->prof_acc.gpu_train_kernel_us += 1e3 * kms[1];
+    tr->prof_acc.gpu_scatter_kernel_us += 1e3 * kms[2];
+    tr->prof_acc.gpu_finish_kernel_us += 1e3 * kms[3];
     tr->prof_acc.gpu_sort_us += 1e3 * ms[0];
     tr->prof_acc.gpu_encode_us += 1e3 * ms[1];
     tr->prof_acc.gpu_fwd_bwd_us += 1e3 * ms[2];
@@ -865,9 +903,11 @@ int launch_encode(tmnn_trainer *tr, const float *pos, int n, const uint32_t *per
   const dim3 grid(bx, by_level ? static_cast<uint32_t>(e.L) : split);
 #define TMNN_ENCODE(d, f)                                                                     \
   if (by_level)                                                                               \
-    hipLaunchKernelGGL((encode_level_kernel<d, f>), grid, dim3(kEncodeThreads), 0, st, e);    \
+    launch_step_kernel(tr, kKernEncode, encode_level_kernel<d, f>, grid, dim3(kEncodeThreads), \
+                       0, st, e);                                                             \
   else                                                                                        \
-    hipLaunchKernelGGL((encode_features_kernel<d, f>), grid, dim3(kEncodeThreads), 0, st, e);
+    launch_step_kernel(tr, kKernEncode, encode_features_kernel<d, f>, grid,                   \
+                       dim3(kEncodeThreads), 0, st, e);
   switch (tr->d.spatial_dims * 8 + tr->d.features_per_level) {
     case 2 * 8 + 1: TMNN_ENCODE(2, 1) break;
     case 2 * 8 + 2: TMNN_ENCODE(2, 2) break;
@@ -913,8 +953,8 @@ int launch_field(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
   }
   const int need = (a.n_tiles + plan.wpb - 1) / plan.wpb;
   const int blocks = std::max(1, std::min(need, plan.max_blocks));
-  hipLaunchKernelGGL(plan.fn, dim3(blocks), dim3(64 * plan.wpb), plan.lds,
-                     tr->ctx->stream, a);
+  launch_step_kernel(tr, kKernTrain, plan.fn, dim3(blocks), dim3(64 * plan.wpb),
+                     static_cast<uint32_t>(plan.lds), tr->ctx->stream, a);
   TMNN_HIP_TRY(hipGetLastError());
   return blocks;
 }
@@ -1222,9 +1262,11 @@ int launch_scatter(tmnn_trainer *tr, const float *pos, int n) {
   hipStream_t st = tr->ctx->stream;
 #define TMNN_SCATTER(d, f)                                                                   \
   if (by_level)                                                                              \
-    hipLaunchKernelGGL((hash_scatter_level_kernel<d, f>), grid, dim3(kScatterThreads), 0, st, s); \
+    launch_step_kernel(tr, kKernScatter, hash_scatter_level_kernel<d, f>, grid,              \
+                       dim3(kScatterThreads), 0, st, s);                                     \
   else                                                                                       \
-    hipLaunchKernelGGL((hash_scatter_kernel<d, f>), grid, dim3(kScatterThreads), 0, st, s);
+    launch_step_kernel(tr, kKernScatter, hash_scatter_kernel<d, f>, grid,                    \
+                       dim3(kScatterThreads), 0, st, s);
   switch (tr->d.spatial_dims * 8 + tr->d.features_per_level) {
     case 2 * 8 + 1: TMNN_SCATTER(2, 1) break;
     case 2 * 8 + 2: TMNN_SCATTER(2, 2) break;
@@ -1452,9 +1494,11 @@ int run_finish(tmnn_trainer *tr, int part_blocks, int n, float *d_loss) {
   hipStream_t st = tr->ctx->stream;
 #define TMNN_FINISH(ff)                                                                            \
   if (num)                                                                                         \
-    hipLaunchKernelGGL((finish_step_kernel<ff, true>), grid, dim3(kFinishThreads), 0, st, f);      \
+    launch_step_kernel(tr, kKernFinish, finish_step_kernel<ff, true>, grid, dim3(kFinishThreads),  \
+                       0, st, f);                                                                  \
   else                                                                                             \
-    hipLaunchKernelGGL((finish_step_kernel<ff, false>), grid, dim3(kFinishThreads), 0, st, f);
+    launch_step_kernel(tr, kKernFinish, finish_step_kernel<ff, false>, grid, dim3(kFinishThreads), \
+                       0, st, f);
   switch (tr->d.features_per_level) {
     case 1: TMNN_FINISH(1) break;
     case 2: TMNN_FINISH(2) break;
@@ -2858,8 +2902,8 @@ int tmnn_get_step_profile_samples(tmnn_trainer *tr, float *out, uint32_t capacit
   if (out) {
     const size_t k = std::min<size_t>(capacity, tr->prof_samples.size());
     for (size_t i = 0; i < k; ++i)
-      std::memcpy(out + i * TMNN_PROFILE_PHASES, tr->prof_samples[i].data(),
-                  TMNN_PROFILE_PHASES * sizeof(float));
+      std::memcpy(out + i * TMNN_PROFILE_COLUMNS, tr->prof_samples[i].data(),
+                  TMNN_PROFILE_COLUMNS * sizeof(float));
   }
   return TMNN_OK;
 }

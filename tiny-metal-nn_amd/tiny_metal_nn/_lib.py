@@ -169,12 +169,17 @@ class StepProfile(ctypes.Structure):
         ("gpu_encode_us", ctypes.c_double),
         ("infer_calls", ctypes.c_uint32),
         ("gpu_infer_us", ctypes.c_double),
+        ("gpu_encode_kernel_us", ctypes.c_double),
+        ("gpu_train_kernel_us", ctypes.c_double),
+        ("gpu_scatter_kernel_us", ctypes.c_double),
+        ("gpu_finish_kernel_us", ctypes.c_double),
     ]
 
 
 # columns of tmnn_get_step_profile_samples (TMNN_PROFILE_*)
 PROFILE_PHASES = ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us",
-                  "gpu_reduce_us", "gpu_adam_us", "gpu_total_us")
+                  "gpu_reduce_us", "gpu_adam_us", "gpu_total_us", "gpu_encode_kernel_us",
+                  "gpu_train_kernel_us", "gpu_scatter_kernel_us", "gpu_finish_kernel_us")
 
 # RuntimeBufferRole (runtime_authority.h:68-79), same numbering
 BUFFER_ROLES = {"ConfigWeights": 0, "HashWeights": 1, "MlpWeights": 2, "GradHash": 3,
