@@ -323,8 +323,10 @@ int tmnn_get_last_numerics(tmnn_trainer *tr, tmnn_step_result *out);
  * profiled. Every call on one GPU shares that GPU's scratch, which keeps the
  * last call's contents: calls from trainers on different streams of one GPU
  * are ordered by a per-device event (each waits for the previous call's
- * kernels before its first kernel), so they take the scratch in turn;
- * enqueue them from one host thread at a time per device. */
+ * kernels before its first kernel; the enqueue itself holds a process-wide
+ * lock), so they take the scratch in turn, in the order the calls were
+ * made. A caller that needs a particular order across threads must impose
+ * it itself. */
 int tmnn_training_step_device_noalloc(tmnn_trainer *tr, const float *d_input,
                                       const float *d_target, int32_t n,
                                       float *d_loss_out);
