@@ -393,6 +393,33 @@ __global__ void __launch_bounds__(W * 64)
     fetch_rows(blockIdx.x * W + wave);
     fetch_targets();
   }
+  // 2D grids (four corners per level, a table the L2 holds): the fused
+  // hash-grid backward of the previous round's tile runs in three parts
+  // inside this round's forward (after the layer-0, layer-1 and output-layer
+  // products are issued), so its index arithmetic and stores use the VALU
+  // and memory pipes while the matrix cores run the products; the last
+  // round's runs after the loop. The int32 atomic sums and flag stores are
+  // order-free. 3D grids (eight corners into tables of tens of MB: a
+  // memory-bound backward) run it right after the tile's dW_0 owner jobs
+  // instead, where it overlaps other waves' owner jobs; deferred, its
+  // stores stalled the forward (C3 MLP kernel 257 -> 313 us).
+  constexpr bool kDeferScatter = SD == 2;
+  f32x4 sdx[KT0][kNT];
+  float sP[kNT][PD];
+  bool svalid[kNT];
+  bool spend = false;
+  const float *sres = reinterpret_cast<const float *>(smem + s.res_off);
+  // three parts in proportion to the products they sit behind (layer 0,
+  // layer 1, the output layer: 24, 48 and 12 MFMAs at C2): groups [0, G/4),
+  // [G/4, 3G/4), [3G/4, G) of the tile's G = 2 KT0 groups
+  auto scatter_part = [&](auto part) __attribute__((always_inline)) {
+    if constexpr (kDeferScatter) {
+      constexpr int G = 2 * KT0, i = decltype(part)::value;
+      constexpr int gb = i == 0 ? 0 : (i == 1 ? G / 4 : 3 * G / 4);
+      constexpr int ge = i == 0 ? G / 4 : (i == 1 ? 3 * G / 4 : G);
+      if (spend) tile_scatter<SD, SF, KT0, gb, ge>(a, sdx, sP, svalid, sres, q);
+    }
+  };
 
   for (int round = blockIdx.x; round < n_rounds; round += gridDim.x) {
     const int tile = round * W + wave;
@@ -444,6 +471,7 @@ __global__ void __launch_bounds__(W * 64)
       mma_split_packed<XS, HT>(smem + s.fwd_off(0), smem + s.fwd_lo_off(0), bh, bl,
                                reinterpret_cast<const float *>(smem + s.bias_off(0)), act, lane);
     }
+    scatter_part(std::integral_constant<int, 0>{});
     auto relu = [&]() {
 #pragma unroll
       for (int mt = 0; mt < HT; ++mt)
@@ -470,8 +498,10 @@ __global__ void __launch_bounds__(W * 64)
       pack_hidden(k - 1, bh, bl);
       mma_split_packed<HS, HT>(smem + s.fwd_off(k), smem + s.fwd_lo_off(k), bh, bl,
                                reinterpret_cast<const float *>(smem + s.bias_off(k)), act, lane);
+      if (k == 1) scatter_part(std::integral_constant<int, 1>{});
       relu();
     }
+    if constexpr (NHL == 1) scatter_part(std::integral_constant<int, 1>{});
     f32x4 y[1][kNT];
     {
       half8 bh[HS][kNT], bl[HS][kNT];
@@ -479,6 +509,8 @@ __global__ void __launch_bounds__(W * 64)
       mma_split_packed<HS, 1>(smem + s.fwd_off(NHL), smem + s.fwd_lo_off(NHL), bh, bl,
                               reinterpret_cast<const float *>(smem + s.bias_off(NHL)), y, lane);
     }
+    scatter_part(std::integral_constant<int, 2>{});
+    spend = false;
 
     // ---- loss / output gradient (outputs 0..15 in tile 0, tile 1 zero)
     f32x4 g[2][kNT];
@@ -539,6 +571,22 @@ __global__ void __launch_bounds__(W * 64)
     // h_{NHL-1}, which only its dW_out read; the others in slots of their
     // own), then meet once and run all layers' owner jobs in one phase.
     f32x4 dx[KT0][kNT];  // the input-feature gradients (k == 0)
+    // this tile's hash-grid backward: now, or kept for the next round
+    auto scatter_tile = [&]() __attribute__((always_inline)) {
+      if constexpr (kDeferScatter) {
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+#pragma unroll
+          for (int kt = 0; kt < KT0; ++kt) sdx[kt][nt] = dx[kt][nt];
+#pragma unroll
+          for (int k = 0; k < PD; ++k) sP[nt][k] = P[nt][k];
+          svalid[nt] = valid[nt];
+        }
+        spend = true;
+      } else if constexpr (SD > 0) {
+        tile_scatter<SD, SF, KT0>(a, dx, P, valid, sres, q);
+      }
+    };
     auto owners = [&](int k) __attribute__((always_inline)) {
       if (!wgrads) return;
       if (k > 0) {
@@ -630,9 +678,7 @@ __global__ void __launch_bounds__(W * 64)
         __syncthreads();
         owners(k);
         if constexpr (SD > 0)
-          if (k == 0)
-            tile_scatter<SD, SF, KT0>(a, dx, P, valid,
-                                      reinterpret_cast<const float *>(smem + s.res_off), q);
+          if (k == 0) scatter_tile();
         __syncthreads();
       }
     }
@@ -640,12 +686,13 @@ __global__ void __launch_bounds__(W * 64)
       __syncthreads();  // every wave's deltas are parked
 #pragma unroll
       for (int k = NHL - 1; k >= 0; --k) owners(k);
-      if constexpr (SD > 0)
-        tile_scatter<SD, SF, KT0>(a, dx, P, valid,
-                                  reinterpret_cast<const float *>(smem + s.res_off), q);
+      if constexpr (SD > 0) scatter_tile();
       __syncthreads();  // the next round parks its operands over these slots
     }
   }
+  scatter_part(std::integral_constant<int, 0>{});
+  scatter_part(std::integral_constant<int, 1>{});
+  scatter_part(std::integral_constant<int, 2>{});
 
   if (a.mode == kModeInputGrad) return;  // uniform: no loss, no weight gradients
   // ---- loss partial (wave order) and largest |output| of the block

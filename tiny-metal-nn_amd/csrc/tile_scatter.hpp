@@ -37,17 +37,20 @@ __host__ __device__ constexpr bool tile_scatter_shape(int D, int F) {
 // dx: the tile's input-feature gradients (fp32, still carrying the loss
 // scale); pos: the lane's point positions per column tile (sorted order);
 // res: the per-level resolution table (the LDS image's copy).
-template <int D, int F, int KT0>
+// GB, GE: the (K tile, pair) groups [GB, GE) of dx this call covers (group
+// 2 kt + h: levels 8 kt + 2 q + h), so a caller can spread one tile's
+// backward over several places.
+template <int D, int F, int KT0, int GB = 0, int GE = 2 * KT0>
 __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&dx)[KT0][kNT],
                                              const float (&pos)[kNT][D], const bool (&valid)[kNT],
                                              const float *res, int q) {
   static_assert(tile_scatter_shape(D, F), "fused scatter shape");
+  static_assert(0 <= GB && GB <= GE && GE <= 2 * KT0, "group range");
   const uint32_t tmask = (1u << a.log2T) - 1u;
   const __amdgpu_buffer_rsrc_t flags = flag_rsrc(a.mask, a.L, a.log2T);
 #pragma unroll
-  for (int kt = 0; kt < KT0; ++kt)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
+  for (int gi = GB; gi < GE; ++gi) {
+      const int kt = gi / 2, h = gi % 2;
       const int l = 8 * kt + 2 * q + h;
       const bool lv = l < a.L;
       const float rl = res[lv ? l : 0];
