@@ -589,3 +589,46 @@ def test_fused_step_profile_phases():
                             ("gpu_train_kernel_us", "gpu_fwd_bwd_us"),
                             ("gpu_finish_kernel_us", "gpu_adam_us")):
             assert 0.0 < prof[kern] <= prof[phase] * 1.001, (kern, phase, prof)
+
+
+def test_profile_samples_add_up_to_the_profile_and_lds_rate_is_sane():
+    """tmnn_get_step_profile_samples: one row per profiled step, in the
+    columns of PROFILE_PHASES, whose column sums are the aggregate profile
+    (tmnn_get_step_profile) and whose phases add up to each row's total;
+    reading keeps them, switching profiling off drops them.
+    tmnn_debug_lds_rate: between 1 TB/s and 1 PB/s (a few hundred CUs
+    reading at most a few hundred bytes per clock each)."""
+    torch = pytest.importorskip("torch")
+    from tiny_metal_nn._lib import PROFILE_PHASES
+    _say("profile samples, lds rate")
+    d, enc, net, m_out, loss = BASELINE["c2"]
+    n = 1 << 14
+    with make_trainer(d, m_out, enc, net, loss=loss, precision="fp16", batch=n) as tr:
+        x = torch.rand(n, d, device="cuda:0")
+        y = torch.rand(n, m_out, device="cuda:0")
+        torch.cuda.synchronize()
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), n)
+        tr.synchronize()
+        tr.set_training_step_profiling(True, 1)
+        for _ in range(4):
+            tr.training_step_device(x.data_ptr(), y.data_ptr(), n)
+        tr.synchronize()
+        rows = tr.training_step_profile_samples()
+        assert rows.shape == (4, len(PROFILE_PHASES)), rows.shape
+        col = {k: i for i, k in enumerate(PROFILE_PHASES)}
+        phases = ("gpu_sort_us", "gpu_encode_us", "gpu_fwd_bwd_us", "gpu_scatter_us",
+                  "gpu_reduce_us", "gpu_adam_us")
+        for r in rows:
+            total = r[col["gpu_total_us"]]
+            assert total > 0.0
+            assert abs(sum(r[col[k]] for k in phases) - total) <= 1e-3 * total, r
+            assert 0.0 < r[col["gpu_train_kernel_us"]] <= r[col["gpu_fwd_bwd_us"]] * 1.001, r
+        prof = tr.training_step_profile()
+        assert prof["steps"] == 4, prof
+        for k in PROFILE_PHASES:
+            assert abs(float(rows[:, col[k]].sum()) - prof[k]) <= 1e-3 * max(1.0, prof[k]), (k, prof)
+        assert np.array_equal(tr.training_step_profile_samples(), rows)
+        tr.set_training_step_profiling(False)
+        assert tr.training_step_profile_samples().shape[0] == 0
+        rate = tr.debug_lds_rate(3)
+        assert 1e12 < rate < 1e15, rate
