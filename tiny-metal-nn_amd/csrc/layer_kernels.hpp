@@ -65,6 +65,9 @@ struct LwGemmArgs {
   int64_t dst_stride;
   int32_t dst_off;
   int32_t ones_row;           // 1: A's last row (r == R - 1) is all ones (bias gradients)
+  // 16-byte accesses allowed (lw_vec_ok; set by lw_set_vec): A rows (kLwARow,
+  // kLwACol), B rows, and the epilogue's out / bias / mask rows
+  int32_t a_vec, b_vec, o_vec;
 };
 
 constexpr int kLwTile = 64;
@@ -73,18 +76,19 @@ constexpr int kLwTile = 64;
 constexpr int kLwForwardChunk = 1 << 18;
 constexpr int kLwK = 16;
 
+template <int AM>
 __device__ __forceinline__ float lw_a(const LwGemmArgs &g, int r, int k) {
   if (g.ones_row && r == g.R - 1) return 1.0f;
-  switch (g.a_mode) {
-    case kLwARow: return g.A[static_cast<size_t>(r) * g.lda + k];
-    case kLwACol: return g.A[static_cast<size_t>(k) * g.lda + r];
-    case kLwAXTiles: return g.A[xtile_offset(r, k >> 2, g.KT0) + (k & 3)];
-    default: return g.A[xtile_offset(k, r >> 2, g.KT0) + (r & 3)];
-  }
+  if constexpr (AM == kLwARow) return g.A[static_cast<size_t>(r) * g.lda + k];
+  if constexpr (AM == kLwACol) return g.A[static_cast<size_t>(k) * g.lda + r];
+  if constexpr (AM == kLwAXTiles) return g.A[xtile_offset(r, k >> 2, g.KT0) + (k & 3)];
+  return g.A[xtile_offset(k, r >> 2, g.KT0) + (r & 3)];
 }
 
+template <int BT>
 __device__ __forceinline__ float lw_b(const LwGemmArgs &g, int k, int c) {
-  return g.b_trans ? g.B[static_cast<size_t>(c) * g.ldb + k] : g.B[static_cast<size_t>(k) * g.ldb + c];
+  if constexpr (BT != 0) return g.B[static_cast<size_t>(c) * g.ldb + k];
+  return g.B[static_cast<size_t>(k) * g.ldb + c];
 }
 
 // LDS staging of one K step: row (or column) i of the tile holds its kLwK
@@ -92,12 +96,126 @@ __device__ __forceinline__ float lw_b(const LwGemmArgs &g, int k, int c) {
 // so each lane reads the four K values of an MFMA A or B operand with one
 // ds_read_b128.
 constexpr int kLwKP = kLwK + 4;
-constexpr int kLwStage = kLwTile * kLwK / 256;  // operand elements per thread and K step
+// The output tile is staged through LDS for the epilogue (kLwCP floats per
+// row), so each thread stores 16 consecutive columns of one row.
+constexpr int kLwCP = kLwTile + 4;
+constexpr int kLwSmem = kLwTile * kLwCP > 2 * kLwTile * kLwKP ? kLwTile * kLwCP : 2 * kLwTile * kLwKP;
+static_assert(kLwTile * kLwK == 256 * 4, "one four-element quad per thread and operand");
 
+// Whether A's and B's rows (of the layouts read with 16-byte loads: lda /
+// ldb floats apart, 16-byte aligned) allow vector loads (host-side check).
+inline bool lw_vec_ok(const float *ptr, int ld) {
+  return ptr != nullptr && (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0 && ld % 4 == 0;
+}
+
+// One thread's quad of an operand tile for one K step. k-fast layouts (A
+// rows, X tiles, B read transposed): quad = four consecutive K of one tile
+// row, thread t takes row t / 4, K offset 4 (t % 4). Row-fast layouts (A
+// read by columns, transposed X tiles, B in [K][C]): quad = four consecutive
+// rows at one K, thread t takes K offset t / 16, rows 4 (t % 16) .. + 3.
+// The four values of a quad lie contiguous in memory; a quad wholly inside
+// the product (and aligned) is one 16-byte load, else four bounded scalar
+// reads. Elements outside the product are zero.
+template <int AM>
+__device__ __forceinline__ f32x4 lw_load_a(const LwGemmArgs &g, int r0, int k0, int ke, bool &kfast,
+                                           int &rr, int &kk) {
+  const int t = threadIdx.x;
+  kfast = AM == kLwARow || AM == kLwAXTiles;
+  rr = kfast ? t >> 2 : (t & 15) * 4;
+  kk = kfast ? (t & 3) * 4 : t >> 4;
+  const int r = r0 + rr, k = k0 + kk;
+  const int real_rows = g.R - (g.ones_row ? 1 : 0);  // rows read from A
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (kfast) {
+    if (r >= g.R || k >= ke) return v;
+    if (r < real_rows && k + 3 < ke && (AM == kLwAXTiles || g.a_vec)) {
+      const float *src = AM == kLwAXTiles ? g.A + xtile_offset(r, k >> 2, g.KT0)
+                                          : g.A + static_cast<size_t>(r) * g.lda + k;
+      return *reinterpret_cast<const f32x4 *>(src);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (k + e < ke) v[e] = lw_a<AM>(g, r, k + e);
+    return v;
+  }
+  if (k >= ke || r >= g.R) return v;
+  if (r + 3 < real_rows && (AM == kLwAXTilesT || g.a_vec)) {
+    const float *src = AM == kLwAXTilesT ? g.A + xtile_offset(k, r >> 2, g.KT0)
+                                         : g.A + static_cast<size_t>(k) * g.lda + r;
+    return *reinterpret_cast<const f32x4 *>(src);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (r + e < g.R) v[e] = lw_a<AM>(g, r + e, k);
+  return v;
+}
+
+template <int BT>
+__device__ __forceinline__ f32x4 lw_load_b(const LwGemmArgs &g, int c0, int k0, int ke, bool &kfast,
+                                           int &cc, int &kk) {
+  const int t = threadIdx.x;
+  kfast = BT != 0;
+  cc = kfast ? t >> 2 : (t & 15) * 4;
+  kk = kfast ? (t & 3) * 4 : t >> 4;
+  const int c = c0 + cc, k = k0 + kk;
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (kfast) {
+    if (c >= g.C || k >= ke) return v;
+    if (k + 3 < ke && g.b_vec)
+      return *reinterpret_cast<const f32x4 *>(g.B + static_cast<size_t>(c) * g.ldb + k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (k + e < ke) v[e] = lw_b<BT>(g, k + e, c);
+    return v;
+  }
+  if (k >= ke || c >= g.C) return v;
+  if (c + 3 < g.C && g.b_vec)
+    return *reinterpret_cast<const f32x4 *>(g.B + static_cast<size_t>(k) * g.ldb + c);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c + e < g.C) v[e] = lw_b<BT>(g, k, c + e);
+  return v;
+}
+
+// Stores a quad into the LDS tile (row i's K values contiguous).
+__device__ __forceinline__ void lw_stage(float *S, f32x4 v, bool kfast, int i, int kk) {
+  if (kfast) {
+    *reinterpret_cast<f32x4 *>(S + i * kLwKP + kk) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) S[(i + e) * kLwKP + kk] = v[e];
+  }
+}
+
+// Epilogue of one output element (row r, column c, product value v).
+template <int EPI>
+__device__ __forceinline__ void lw_epilogue(const LwGemmArgs &g, int r, int c, float v) {
+  if constexpr (EPI == kLwEpiHidden) {
+    g.out[static_cast<size_t>(r) * g.ldo + c] = fmaxf(v + g.bias[c], 0.0f);
+  } else if constexpr (EPI == kLwEpiOutput) {
+    const float y = v + g.bias[c];
+    if (g.out) {
+      const size_t row = g.out_index ? g.out_index[r] : static_cast<uint32_t>(r);
+      g.out[row * g.ldo + c] = y;
+    }
+    if (g.out2) g.out2[static_cast<size_t>(r) * g.ldo2 + c] = y;
+  } else if constexpr (EPI == kLwEpiMask) {
+    g.out[static_cast<size_t>(r) * g.ldo + c] = g.mask[static_cast<size_t>(r) * g.ldm + c] > 0.0f ? v : 0.0f;
+  } else if constexpr (EPI == kLwEpiScale) {
+    g.out[static_cast<size_t>(r) * g.ldo + c] = v * g.scale;
+  } else {
+    g.dst[blockIdx.z * g.dst_stride + g.dst_off + static_cast<int64_t>(r) * g.C + c] = v;
+  }
+}
+
+// One instance per (A layout, B orientation, epilogue) the layer-wise path
+// uses (lw_gemm_fn): compiled without the other modes' registers and branches.
+template <int AM, int BT, int EPI>
 __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
-  // the tile's A rows and B columns of the current K step, K innermost
-  __shared__ __align__(16) float As[kLwTile * kLwKP];
-  __shared__ __align__(16) float Bs[kLwTile * kLwKP];
+  // the tile's A rows and B columns of the current K step, K innermost; after
+  // the products the same memory holds the output tile
+  __shared__ __align__(16) float smem[kLwSmem];
+  float *As = smem, *Bs = smem + kLwTile * kLwKP, *Cs = smem;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int p = lane & 15, q = lane >> 4;
@@ -112,46 +230,25 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Operand staging, software-pipelined: the next K step's slices are read
+  // Operand staging, software-pipelined: the next K step's quads are read
   // from global memory into registers before the current step's products
-  // and stored to LDS after them. Consecutive threads walk the operand's
-  // contiguous index; elements outside the product are zero.
-  const bool a_k_fast = g.a_mode == kLwARow, b_k_fast = g.b_trans != 0;
-  float ra[kLwStage], rb[kLwStage];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int e = 0; e < kLwStage; ++e) {
-      const int idx = tid + 256 * e;
-      const int rr = a_k_fast ? idx / kLwK : idx % kLwTile;
-      const int kk = a_k_fast ? idx % kLwK : idx / kLwTile;
-      const int r = r0 + rr, k = k0 + kk;
-      ra[e] = (r < g.R && k < ke) ? lw_a(g, r, k) : 0.0f;
-      const int cc = b_k_fast ? idx / kLwK : idx % kLwTile;
-      const int kc = b_k_fast ? idx % kLwK : idx / kLwTile;
-      const int c = c0 + cc, k2 = k0 + kc;
-      rb[e] = (c < g.C && k2 < ke) ? lw_b(g, k2, c) : 0.0f;
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int e = 0; e < kLwStage; ++e) {
-      const int idx = tid + 256 * e;
-      const int rr = a_k_fast ? idx / kLwK : idx % kLwTile;
-      const int kk = a_k_fast ? idx % kLwK : idx / kLwTile;
-      As[rr * kLwKP + kk] = ra[e];
-      const int cc = b_k_fast ? idx / kLwK : idx % kLwTile;
-      const int kc = b_k_fast ? idx % kLwK : idx / kLwTile;
-      Bs[cc * kLwKP + kc] = rb[e];
-    }
-  };
+  // and stored to LDS after them.
+  bool akf, bkf;
+  int ai, ak, bi, bk;
+  f32x4 ra, rb;
   if (kb < ke) {
-    load(kb);
-    store();
+    ra = lw_load_a<AM>(g, r0, kb, ke, akf, ai, ak);
+    rb = lw_load_b<BT>(g, c0, kb, ke, bkf, bi, bk);
+    lw_stage(As, ra, akf, ai, ak);
+    lw_stage(Bs, rb, bkf, bi, bk);
   }
   __syncthreads();
   for (int k0 = kb; k0 < ke; k0 += kLwK) {
     const bool more = k0 + kLwK < ke;  // uniform over the block
-    if (more) load(k0 + kLwK);
+    if (more) {
+      ra = lw_load_a<AM>(g, r0, k0 + kLwK, ke, akf, ai, ak);
+      rb = lw_load_b<BT>(g, c0, k0 + kLwK, ke, bkf, bi, bk);
+    }
     // v_mfma_f32_16x16x4_f32: lane p + 16 q supplies A[row p][k] and
     // B[k][column p] of K slot q; the four MFMAs of a 16-wide K group take K
     // values 16 h + 4 q + e (e = 0..3), one ds_read_b128 per operand tile
@@ -174,48 +271,73 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
     }
     __syncthreads();
     if (more) {
-      store();
+      lw_stage(As, ra, akf, ai, ak);
+      lw_stage(Bs, rb, bkf, bi, bk);
       __syncthreads();
     }
   }
-  // D layout: lane p + 16 q holds rows 4 q + rr, column p of each 16 x 16 tile
+  // the output tile through LDS (D layout: lane p + 16 q holds rows 4 q + rr,
+  // column p of each 16 x 16 tile), then row-contiguous stores
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int r = r0 + wr + 16 * i + 4 * q + rr;
-      if (r >= g.R) continue;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int c = c0 + wc + 16 * j + p;
-        if (c >= g.C) continue;
-        const float v = acc[i][j][rr];
-        switch (g.epi) {
-          case kLwEpiHidden:
-            g.out[static_cast<size_t>(r) * g.ldo + c] = fmaxf(v + g.bias[c], 0.0f);
-            break;
-          case kLwEpiOutput: {
-            const float y = v + g.bias[c];
-            if (g.out) {
-              const size_t row = g.out_index ? g.out_index[r] : static_cast<uint32_t>(r);
-              g.out[row * g.ldo + c] = y;
-            }
-            if (g.out2) g.out2[static_cast<size_t>(r) * g.ldo2 + c] = y;
-            break;
-          }
-          case kLwEpiMask:
-            g.out[static_cast<size_t>(r) * g.ldo + c] =
-                g.mask[static_cast<size_t>(r) * g.ldm + c] > 0.0f ? v : 0.0f;
-            break;
-          case kLwEpiScale:
-            g.out[static_cast<size_t>(r) * g.ldo + c] = v * g.scale;
-            break;
-          default:
-            g.dst[blockIdx.z * g.dst_stride + g.dst_off + static_cast<int64_t>(r) * g.C + c] = v;
-            break;
-        }
+      for (int rr = 0; rr < 4; ++rr)
+        Cs[(wr + 16 * i + 4 * q + rr) * kLwCP + wc + 16 * j + p] = acc[i][j][rr];
+  __syncthreads();
+  const int er = tid >> 2, ecol = (tid & 3) * 16;  // this thread: 16 columns of one row
+  const int r = r0 + er;
+  if (r >= g.R) return;
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    const int c = c0 + ecol + 4 * gq;
+    if (c >= g.C) break;
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(Cs + er * kLwCP + ecol + 4 * gq);
+    constexpr bool kVecEpi = EPI == kLwEpiHidden || EPI == kLwEpiMask || EPI == kLwEpiScale;
+    if (kVecEpi && c + 3 < g.C && g.o_vec) {
+      f32x4 o;
+      const size_t oi = static_cast<size_t>(r) * g.ldo + c;
+      if constexpr (EPI == kLwEpiHidden) {
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(g.bias + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = fmaxf(v[e] + b[e], 0.0f);
+      } else if constexpr (EPI == kLwEpiMask) {
+        const f32x4 m = *reinterpret_cast<const f32x4 *>(g.mask + static_cast<size_t>(r) * g.ldm + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = m[e] > 0.0f ? v[e] : 0.0f;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = v[e] * g.scale;
       }
+      *reinterpret_cast<f32x4 *>(g.out + oi) = o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c + e < g.C) lw_epilogue<EPI>(g, r, c + e, v[e]);
     }
+  }
+}
+
+using LwGemmFn = void (*)(LwGemmArgs);
+
+// The lw_gemm_kernel instance for g's modes (nullptr: a combination the
+// layer-wise path does not use).
+inline LwGemmFn lw_gemm_fn(const LwGemmArgs &g) {
+  if (g.b_trans == 0 && g.epi == kLwEpiHidden)
+    return g.a_mode == kLwAXTiles ? lw_gemm_kernel<kLwAXTiles, 0, kLwEpiHidden>
+                                  : lw_gemm_kernel<kLwARow, 0, kLwEpiHidden>;
+  if (g.b_trans == 0 && g.epi == kLwEpiOutput)
+    return g.a_mode == kLwAXTiles ? lw_gemm_kernel<kLwAXTiles, 0, kLwEpiOutput>
+                                  : lw_gemm_kernel<kLwARow, 0, kLwEpiOutput>;
+  if (g.b_trans == 0 && g.epi == kLwEpiPartial)
+    return g.a_mode == kLwAXTilesT ? lw_gemm_kernel<kLwAXTilesT, 0, kLwEpiPartial>
+                                   : lw_gemm_kernel<kLwACol, 0, kLwEpiPartial>;
+  if (g.b_trans != 0 && g.a_mode == kLwARow && g.epi == kLwEpiMask)
+    return lw_gemm_kernel<kLwARow, 1, kLwEpiMask>;
+  if (g.b_trans != 0 && g.a_mode == kLwARow && g.epi == kLwEpiScale)
+    return lw_gemm_kernel<kLwARow, 1, kLwEpiScale>;
+  return nullptr;
 }
 
 struct LwLossArgs {

@@ -975,8 +975,17 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
   hipStream_t st = tr->ctx->stream;
   auto gemm = [&](LwGemmArgs g, int chunks) -> int {
     if (g.R <= 0 || g.C <= 0) return TMNN_OK;
+    // 16-byte operand loads and epilogue stores where rows are aligned
+    g.a_vec = (g.a_mode == kLwARow || g.a_mode == kLwACol) && lw_vec_ok(g.A, g.lda);
+    g.b_vec = lw_vec_ok(g.B, g.ldb);
+    const bool bias_ok = g.bias && (reinterpret_cast<uintptr_t>(g.bias) & 15u) == 0;
+    g.o_vec = lw_vec_ok(g.out, g.ldo) &&
+              (g.epi == kLwEpiScale || (g.epi == kLwEpiHidden && bias_ok) ||
+               (g.epi == kLwEpiMask && lw_vec_ok(g.mask, g.ldm)));
     const dim3 grid((g.R + kLwTile - 1) / kLwTile, (g.C + kLwTile - 1) / kLwTile, chunks);
-    hipLaunchKernelGGL(lw_gemm_kernel, grid, dim3(256), 0, st, g);
+    const LwGemmFn fn = lw_gemm_fn(g);
+    if (!fn) return fail(TMNN_ERR_RUNTIME, "layer-wise product of an unexpected form");
+    hipLaunchKernelGGL(fn, grid, dim3(256), 0, st, g);
     TMNN_HIP_TRY(hipGetLastError());
     return TMNN_OK;
   };
