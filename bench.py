@@ -37,12 +37,14 @@ step and forward-only pass over the same batch, timed separately) under
 `workloads`, and the CPU restatement of the reference math timed on this
 host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|tiled_*]
        python bench.py --trace-summary KERNEL_TRACE_CSV
 
 --workload c3/c4/c5 print the one JSON line of that config alone; the
 default, c2, is the headline line above with every config under
-`workloads`.
+`workloads`. --workload tiled_h512_2d / tiled_w128_fp32_4d / tiled_h256_3d
+time a layer-wise (Tiled family) shape at 2^16 points: shapes no fused
+kernel instantiates, outside the BASELINE configs.
 """
 from __future__ import annotations
 
@@ -306,6 +308,65 @@ OTHER_WORKLOADS = {
     "c4": (3, 16, 4, 21, 16.0, 1.5, 64, 3, 1, "L1", 1 << 19),
     "c5": (4, 16, 2, 22, 8.0, 1.4, 128, 4, 4, "L2", 1 << 20),
 }
+
+
+TILED_WORKLOADS = {
+    # Layer-wise (Tiled family) shapes, the ones no fused kernel instantiates:
+    # D, levels, feats, log2T, base, scale, hidden, hidden layers, outputs
+    # (fp32 training, L2 loss, B_TILED points)
+    "tiled_h512_2d": (2, 16, 2, 14, 16.0, 1.5, 512, 1, 3),
+    "tiled_w128_fp32_4d": (4, 16, 2, 16, 8.0, 1.4, 128, 4, 4),
+    "tiled_h256_3d": (3, 8, 2, 14, 8.0, 2.0, 256, 2, 4),
+}
+B_TILED = 1 << 16
+
+
+def run_tiled(torch, which: str, steps: int, warmup: int) -> dict:
+    """A layer-wise (Tiled family) shape: `steps` timed fp32 training steps over
+    B_TILED seeded uniform random points with uniform random targets in [0,1)
+    (after `warmup` untimed ones), then forward-only passes over the same batch,
+    timed separately. Exits if the planner does not select the Tiled family."""
+    from tiny_metal_nn import Trainer
+    d, levels, feats, log2t, base, scale, hidden, nhl, m = TILED_WORKLOADS[which]
+    n = B_TILED
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    x = torch.rand(n, d, device=dev, generator=gen)
+    y = torch.rand(n, m, device=dev, generator=gen)
+    loss_dev = torch.zeros(steps + warmup, device=dev)
+    torch.cuda.synchronize()
+    tr = Trainer.from_config(_config(d, levels, feats, log2t, base, scale, hidden, nhl, "L2", n, "fp32"),
+                             n_input=d, n_output=m)
+    family = tr.inspect_runtime()["family_name"]
+    if family != "Tiled":
+        tr.close()
+        raise SystemExit(f"bench.py: {which} planned as {family}, not Tiled")
+    for i in range(warmup):
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[i].data_ptr())
+    tr.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tr.training_step_device(x.data_ptr(), y.data_ptr(), n, loss_dev[warmup + i].data_ptr())
+    tr.synchronize()
+    el = time.perf_counter() - t0
+    out = torch.empty(n, m, device=dev)
+    for _ in range(3):
+        tr.inference_device(x.data_ptr(), out.data_ptr(), n)
+    tr.synchronize()
+    fwd_iters = max(5, steps)
+    t1 = time.perf_counter()
+    for _ in range(fwd_iters):
+        tr.inference_device(x.data_ptr(), out.data_ptr(), n)
+    tr.synchronize()
+    fwd = (time.perf_counter() - t1) / fwd_iters
+    losses = loss_dev.cpu().numpy()
+    tr.close()
+    return {"workload": which, "family": family, "precision": "fp32", "batch": n,
+            "encoding": f"{d}D L{levels} F{feats} T2^{log2t} base{base:g} x{scale:g}",
+            "mlp": f"{levels * feats}->{hidden}x{nhl}->{m}", "loss": "L2",
+            "train_samples_per_s": round(n * steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+            "forward_samples_per_s": round(n / fwd, 1), "forward_ms": round(fwd * 1e3, 4),
+            "loss_first_last": [round(float(losses[0]), 6), round(float(losses[-1]), 6)]}
 
 
 def workload_batch(torch, which: str, n: int, gen, dev):
@@ -590,7 +651,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", *TILED_WORKLOADS])
     ap.add_argument("--no-workloads", action="store_true",
                     help="skip the C2-fp32 and C3-C5 entries of the default line")
     ap.add_argument("--trace-summary", metavar="CSV", default=None,
@@ -625,6 +686,17 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.workload in TILED_WORKLOADS:
+        r = run_tiled(torch, args.workload, args.steps, args.warmup)
+        print(json.dumps({
+            "metric": f"train samples/s ({args.workload}); forward-only samples/s",
+            "value": r["train_samples_per_s"], "unit": "samples/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32 MFMA (fp32 accumulate) / f32 encode+Adam / i32 hash grads",
+            "data": "synthetic (see run_tiled)", "config": {"workload": args.workload}, **r}),
+            flush=True)
+        return 0
     if args.workload != "c2":
         probe = Trainer.from_config(C2_CONFIG, n_input=2, n_output=3)
         lds_peak = probe.debug_lds_rate(10) / 1e9

@@ -49,6 +49,11 @@ LW_GEOMS = {
     "h96_8layers": (3, dict(n_levels=4, n_features_per_level=1, log2_hashmap_size=10,
                             base_resolution=4.0, per_level_scale=2.0),
                     dict(n_neurons=96, n_hidden_layers=8), 1, "fp32"),
+    # a width that is not a multiple of 4: rows unaligned for 16-byte access,
+    # so the output layer's products take the tile kernel, not the narrow ones
+    "h98_2d": (2, dict(n_levels=8, n_features_per_level=2, log2_hashmap_size=12,
+                       base_resolution=8.0, per_level_scale=1.5),
+               dict(n_neurons=98, n_hidden_layers=2), 3, "fp32"),
 }
 
 
@@ -106,7 +111,8 @@ def test_tiled_backward_matches_oracle(oracle, name):
         assert (diff == 0).mean() > exact and diff.max() <= 16, int(diff.max())
 
 
-@pytest.mark.parametrize("name", ["h256_3d", "in128_2d", "m32_3d", "w128_fp32_4d", "h96_8layers"])
+@pytest.mark.parametrize("name", ["h256_3d", "in128_2d", "m32_3d", "w128_fp32_4d", "h96_8layers",
+                                  "h98_2d"])
 @pytest.mark.parametrize("loss", ["L2", "L1"])
 def test_tiled_training_loss_tracks_oracle(oracle, name, loss):
     _say(f"tiled training {name} {loss}")

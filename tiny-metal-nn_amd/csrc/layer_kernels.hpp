@@ -340,6 +340,220 @@ inline LwGemmFn lw_gemm_fn(const LwGemmArgs &g) {
   return nullptr;
 }
 
+// ---- Narrow products: the output layer's three products have at most 16
+// output columns (forward, weight gradient) or at most 16 K (delta), where a
+// 64 x 64 tile would multiply 48 or more zero columns. Each is memory-bound
+// (one pass over the batch's activations) and gets a kernel of its own
+// shape; the host picks them (lw_narrow_*_ok) and falls back to
+// lw_gemm_kernel otherwise. Their loads come from clamped, always valid
+// addresses and out-of-range values are replaced by zeros afterwards, so
+// the loads carry no branches and are issued in batches ahead of their use.
+constexpr int kLwNarrow = 16;       // at most this many columns (forward, weight gradient) or K (delta)
+constexpr int kLwNarrowMaxK = 512;  // forward: longest K whose B^T fits the block's LDS
+constexpr int kLwNarrowKStep = 128; // forward: K per batch of A loads (8 quads per lane)
+
+// Forward output layer y = A B + bias (kLwEpiOutput; A row-major with
+// 16-byte aligned rows and K % 4 == 0, B[K][C], C <= 16, K <=
+// kLwNarrowMaxK). B^T sits in LDS ([16][KP], KP = round128(K) + 4, zero
+// beyond C and K). Each wave computes 16 rows x 16 columns with
+// v_mfma_f32_16x16x4_f32, reading A straight from global memory into the
+// operand registers: for each 32 K, lane p + 16 q loads K values 8 q .. + 7
+// of row p (the four lanes of a row read 128 contiguous bytes) and MFMA e of
+// the eight takes K value 8 q + e in K slot q (a permutation of K applied to
+// A and B alike). Two register sets of 128 K each alternate: one is loaded
+// while the other feeds the MFMAs.
+__global__ void __launch_bounds__(256) lw_narrow_out_kernel(LwGemmArgs g) {
+  extern __shared__ __align__(16) float Bt[];
+  const int Kr = (g.K + kLwNarrowKStep - 1) / kLwNarrowKStep * kLwNarrowKStep, KP = Kr + 4;
+  for (int i = threadIdx.x; i < kLwNarrow * Kr; i += 256) {
+    const int k = i / kLwNarrow, c = i % kLwNarrow;  // c fastest: B's rows are contiguous
+    Bt[c * KP + k] = (c < g.C && k < g.K) ? g.B[static_cast<size_t>(k) * g.ldb + c] : 0.0f;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = lane & 15, q = lane >> 4;
+  const int groups = (g.R + 15) / 16;
+  const int kmax = g.K - 4;  // last quad of a row
+  const float *brow = Bt + p * KP + 8 * q;
+  for (int grp = blockIdx.x * 4 + wave; grp < groups; grp += gridDim.x * 4) {
+    // rows past R read row R - 1 and are not stored (row p of A feeds only
+    // output row p)
+    const float *arow = g.A + static_cast<size_t>(min(grp * 16 + p, g.R - 1)) * g.lda;
+    auto load = [&](f32x4(&a)[8], int kb) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = kb + 32 * (i >> 1) + 8 * q + 4 * (i & 1);
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(arow + min(k, kmax));
+        a[i] = k < g.K ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto product = [&](const f32x4(&a)[8], int kb) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(brow + kb + 32 * (i >> 1) + 4 * (i & 1));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[e], acc, 0, 0, 0);
+      }
+    };
+    f32x4 x[8], y[8];
+    load(x, 0);
+    for (int kb = 0; kb < Kr; kb += 2 * kLwNarrowKStep) {
+      if (kb + kLwNarrowKStep < Kr) load(y, kb + kLwNarrowKStep);
+      product(x, kb);
+      if (kb + kLwNarrowKStep >= Kr) break;
+      if (kb + 2 * kLwNarrowKStep < Kr) load(x, kb + 2 * kLwNarrowKStep);
+      product(y, kb + kLwNarrowKStep);
+    }
+    // D layout: lane p + 16 q holds rows 4 q + v, column p
+    if (p < g.C) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = grp * 16 + 4 * q + v;
+        if (row < g.R) lw_epilogue<kLwEpiOutput>(g, row, p, acc[v]);
+      }
+    }
+  }
+}
+
+// Weight-gradient partial rows of the output layer (kLwEpiPartial, A read by
+// columns: A(r, k) = act[k][r] with 16-byte aligned rows, B(k, c) = D[k][c],
+// C <= 16, the rows read from A a multiple of 4, an all-ones last row when
+// ones_row). Block (x, z): output rows 64 x .. + 63 over the points of
+// chunk z; wave w takes the groups of four points 4 w + 16 j of the chunk,
+// eight groups per batch of loads, and the four waves' sums are added in
+// wave order at the end. Lane p + 16 q loads rows 4 p .. + 3 of point k + q
+// (one 16-byte load; the 16 lanes of a point read 256 contiguous bytes) and
+// feeds row 4 p + e to MFMA tile e, so output row 4 (4 q + v) + e of the
+// block comes back in lane p + 16 q, element v of tile e. A and D are read
+// through raw buffer resources over the chunk's points: points past the
+// chunk, rows past A's and columns past C lie outside the range and read as
+// zeros (chunk bytes < 2^31, a host check).
+constexpr uint32_t kLwOutside = 0x80000000u;  // a buffer offset past every range
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lw_rsrc(const float *base, int64_t bytes) {
+  // dword 3: 32-bit data format, the raw-buffer setting of gfx9 parts
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+__global__ void __launch_bounds__(256) lw_narrow_wgrad_kernel(LwGemmArgs g) {
+  __shared__ f32x4 red[3][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = lane & 15, q = lane >> 4;
+  const int real_rows = g.R - (g.ones_row ? 1 : 0);  // rows read from A
+  const int u = blockIdx.x * 64 + 4 * p;              // this lane's first row
+  const bool ones = g.ones_row && u == real_rows;     // element 0 is the all-ones row
+  const bool col = p < g.C;
+  const int kb = blockIdx.z * g.k_chunk;
+  const int ke = min(g.K, kb + g.k_chunk);
+  const int64_t points = max(ke - kb, 0);  // an empty last chunk reads nothing
+  const __amdgpu_buffer_rsrc_t ar = lw_rsrc(g.A + static_cast<size_t>(kb) * g.lda, points * g.lda * 4);
+  const __amdgpu_buffer_rsrc_t br = lw_rsrc(g.B + static_cast<size_t>(kb) * g.ldb, points * g.ldb * 4);
+  // byte offsets of point kb + q; rows past A and columns past C never in range
+  const uint32_t a_off = u < real_rows ? static_cast<uint32_t>(q * g.lda + u) * 4u : kLwOutside;
+  const uint32_t b_off = col ? static_cast<uint32_t>(q * g.ldb + p) * 4u : kLwOutside;
+  f32x4 acc[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 4 * wave; k0 < ke - kb; k0 += 128) {
+    f32x4 a[8];
+    float b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int kr = k0 + 16 * j;  // chunk-relative point of K slot 0
+      const uint32_t ka = static_cast<uint32_t>(kr * g.lda) * 4u, kbo = static_cast<uint32_t>(kr * g.ldb) * 4u;
+      a[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, a_off + ka, 0, 0));
+      b[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, b_off + kbo, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (ones) a[j][0] = kb + k0 + 16 * j + q < ke ? 1.0f : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][e], b[j], acc[e], 0, 0, 0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[wave - 1][e][lane] = acc[e];
+  }
+  __syncthreads();
+  if (wave > 0 || !col) return;
+  float *dst = g.dst + blockIdx.z * g.dst_stride + g.dst_off;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const f32x4 s = acc[e] + red[0][e][lane] + red[1][e][lane] + red[2][e][lane];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = blockIdx.x * 64 + 4 * (4 * q + v) + e;
+      if (r < g.R) dst[static_cast<int64_t>(r) * g.C + p] = s[v];
+    }
+  }
+}
+
+// Delta through the output layer: out[r][c] = mask[r][c] > 0 ? sum_{k < K}
+// A[r][k] B(k, c) : 0 with B read transposed (B(k, c) = W[c][k]), K <= 16,
+// C % 4 == 0 and 16-byte aligned out / mask rows. Block (x, y): rows
+// kLwNarrowRows x .. + kLwNarrowRows - 1 and columns 256 y .. + 255, whose A
+// rows and W slice sit in LDS; thread t takes the column quad 4 (t % 64) of
+// the rows t / 64 + 4 j (j = 0 .. 7), all eight mask loads issued first.
+constexpr int kLwNarrowRows = 32;
+__global__ void __launch_bounds__(256) lw_narrow_mask_kernel(LwGemmArgs g) {
+  __shared__ __align__(16) float Ws[kLwNarrow][256];
+  __shared__ float As[kLwNarrowRows][kLwNarrow];
+  const int c0 = blockIdx.y * 256, rb = blockIdx.x * kLwNarrowRows;
+  for (int i = threadIdx.x; i < kLwNarrow * 256; i += 256) {
+    const int cc = i / kLwNarrow, k = i % kLwNarrow;  // k fastest: W's rows are contiguous
+    Ws[k][cc] = (k < g.K && c0 + cc < g.C) ? g.B[static_cast<size_t>(c0 + cc) * g.ldb + k] : 0.0f;
+  }
+  for (int i = threadIdx.x; i < kLwNarrowRows * kLwNarrow; i += 256) {
+    const int rr = i / kLwNarrow, k = i % kLwNarrow;
+    As[rr][k] = (k < g.K && rb + rr < g.R) ? g.A[static_cast<size_t>(rb + rr) * g.lda + k] : 0.0f;
+  }
+  __syncthreads();
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = c0 + 4 * tx;
+  if (c >= g.C) return;
+  constexpr int kRows = kLwNarrowRows / 4;
+  f32x4 m[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int r = min(rb + ty + 4 * j, g.R - 1);
+    m[j] = *reinterpret_cast<const f32x4 *>(g.mask + static_cast<size_t>(r) * g.ldm + c);
+  }
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int rr = ty + 4 * j;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < g.K; ++k) {
+      const float a = As[rr][k];
+      const f32x4 w = *reinterpret_cast<const f32x4 *>(&Ws[k][4 * tx]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = fmaf(a, w[e], s[e]);
+    }
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = m[j][e] > 0.0f ? s[e] : 0.0f;
+    if (rb + rr < g.R) *reinterpret_cast<f32x4 *>(g.out + static_cast<size_t>(rb + rr) * g.ldo + c) = o;
+  }
+}
+
+// Host-side checks that a product has the narrow kernels' form (a_vec / o_vec
+// as set for the generic kernel).
+inline bool lw_narrow_out_ok(const LwGemmArgs &g) {
+  return g.epi == kLwEpiOutput && g.a_mode == kLwARow && g.b_trans == 0 && g.C <= kLwNarrow &&
+         g.K >= 4 && g.K % 4 == 0 && g.K <= kLwNarrowMaxK && g.k_chunk >= g.K && g.a_vec &&
+         !g.ones_row;
+}
+inline bool lw_narrow_wgrad_ok(const LwGemmArgs &g) {
+  const int real_rows = g.R - (g.ones_row ? 1 : 0);
+  const int64_t chunk_bytes = static_cast<int64_t>(g.k_chunk + 128) * std::max(g.lda, g.ldb) * 4;
+  return g.epi == kLwEpiPartial && g.a_mode == kLwACol && g.b_trans == 0 && g.C <= kLwNarrow &&
+         real_rows >= 4 && real_rows % 4 == 0 && g.a_vec && chunk_bytes < (int64_t{1} << 31);
+}
+inline bool lw_narrow_mask_ok(const LwGemmArgs &g) {
+  return g.epi == kLwEpiMask && g.a_mode == kLwARow && g.b_trans != 0 && g.K <= kLwNarrow &&
+         g.C % 4 == 0 && g.o_vec && !g.ones_row && g.k_chunk >= g.K;
+}
+
 struct LwLossArgs {
   int32_t n, M, mode, loss_kind, grad_output, chunk;
   float huber_delta, inv_n, loss_scale;

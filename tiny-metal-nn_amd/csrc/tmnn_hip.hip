@@ -982,6 +982,27 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
     g.o_vec = lw_vec_ok(g.out, g.ldo) &&
               (g.epi == kLwEpiScale || (g.epi == kLwEpiHidden && bias_ok) ||
                (g.epi == kLwEpiMask && lw_vec_ok(g.mask, g.ldm)));
+    if (lw_narrow_out_ok(g)) {
+      const int groups = (g.R + 15) / 16;
+      const int blocks = std::min((groups + 3) / 4, 8 * tr->ctx->cu_count);
+      const int kr = (g.K + kLwNarrowKStep - 1) / kLwNarrowKStep * kLwNarrowKStep;
+      const size_t lds = sizeof(float) * kLwNarrow * (kr + 4);
+      hipLaunchKernelGGL(lw_narrow_out_kernel, dim3(blocks), dim3(256), lds, st, g);
+      TMNN_HIP_TRY(hipGetLastError());
+      return TMNN_OK;
+    }
+    if (lw_narrow_wgrad_ok(g)) {
+      const dim3 grid((g.R + 63) / 64, 1, chunks);
+      hipLaunchKernelGGL(lw_narrow_wgrad_kernel, grid, dim3(256), 0, st, g);
+      TMNN_HIP_TRY(hipGetLastError());
+      return TMNN_OK;
+    }
+    if (chunks == 1 && lw_narrow_mask_ok(g)) {
+      const dim3 grid((g.R + kLwNarrowRows - 1) / kLwNarrowRows, (g.C + 255) / 256);
+      hipLaunchKernelGGL(lw_narrow_mask_kernel, grid, dim3(256), 0, st, g);
+      TMNN_HIP_TRY(hipGetLastError());
+      return TMNN_OK;
+    }
     const dim3 grid((g.R + kLwTile - 1) / kLwTile, (g.C + kLwTile - 1) / kLwTile, chunks);
     const LwGemmFn fn = lw_gemm_fn(g);
     if (!fn) return fail(TMNN_ERR_RUNTIME, "layer-wise product of an unexpected form");
