@@ -1095,8 +1095,10 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
       if ((rc = gemm(g, 1)) != TMNN_OK) return rc;
     }
   }
-  // ---- output gradient (and the loss), per batch chunk
-  const int P = std::max(1, std::min(plan.max_blocks, (n + 255) / 256));
+  // ---- output gradient (and the loss), per batch chunk: chunks of at least
+  // 512 points (2^16 points: 128 chunks; 256 points per chunk wrote twice the
+  // partial rows for a slower step at every measured width)
+  const int P = std::max(1, std::min(plan.max_blocks, (n + 511) / 512));
   const int chunk = (n + P - 1) / P;
   LwLossArgs la{};
   la.n = n;
