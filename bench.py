@@ -33,9 +33,9 @@ prints.
 Also reported: inference samples/s on configs[0] ("C1": the same field shape,
 fp32, 2^16 points per call), the C2 step in fp32 (the reference's own
 training precision), the other BASELINE training configs C3-C5 (training
-step and forward-only pass over the same batch, timed separately) under
-`workloads`, and the CPU restatement of the reference math timed on this
-host.
+step and forward-only pass over the same batch, timed separately) and three
+layer-wise (Tiled family) shapes under `workloads`, and the CPU restatement
+of the reference math timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|tiled_*]
        python bench.py --trace-summary KERNEL_TRACE_CSV
@@ -653,7 +653,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", *TILED_WORKLOADS])
     ap.add_argument("--no-workloads", action="store_true",
-                    help="skip the C2-fp32 and C3-C5 entries of the default line")
+                    help="skip the C2-fp32, C3-C5 and Tiled entries of the default line")
     ap.add_argument("--trace-summary", metavar="CSV", default=None,
                     help="print per-kernel duration statistics of a rocprofv3 kernel trace")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -808,6 +808,9 @@ def main() -> int:
             key = which + ("_fp32" if prec == "fp32" else "")
             workloads[key] = run_workload(torch, which, 20, 5, lds_peak, prec, batches)
             print(f"# {key}: {workloads[key]['ms_per_step']} ms/step", file=sys.stderr, flush=True)
+        for which in TILED_WORKLOADS:
+            workloads[which] = run_tiled(torch, which, 50, 5)
+            print(f"# {which}: {workloads[which]['ms_per_step']} ms/step", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
