@@ -168,18 +168,25 @@ __device__ __forceinline__ uint32_t expand_bits_2d(uint32_t v) {
 // or 8-bit (4D) quantisation. 2D points are the reference's lifted
 // (x, y, 0); their z bits are all zero, so the code keeps only the x/y
 // interleave (20 bits), which sorts identically.
-__device__ __forceinline__ uint32_t morton_code(const float *p, int dims) {
-  if (dims == 4)
+template <int D>
+__device__ __forceinline__ uint32_t morton_code_of(const float *p) {
+  if constexpr (D == 4)
     return (expand_bits_4d(morton_quant(p[3], 256.0f, 255.0f)) << 3) |
            (expand_bits_4d(morton_quant(p[2], 256.0f, 255.0f)) << 2) |
            (expand_bits_4d(morton_quant(p[1], 256.0f, 255.0f)) << 1) |
            expand_bits_4d(morton_quant(p[0], 256.0f, 255.0f));
-  if (dims == 3)
+  else if constexpr (D == 3)
     return (expand_bits_3d(morton_quant(p[2], 1024.0f, 1023.0f)) << 2) |
            (expand_bits_3d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
            expand_bits_3d(morton_quant(p[0], 1024.0f, 1023.0f));
-  return (expand_bits_2d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
-         expand_bits_2d(morton_quant(p[0], 1024.0f, 1023.0f));
+  else
+    return (expand_bits_2d(morton_quant(p[1], 1024.0f, 1023.0f)) << 1) |
+           expand_bits_2d(morton_quant(p[0], 1024.0f, 1023.0f));
+}
+__device__ __forceinline__ uint32_t morton_code(const float *p, int dims) {
+  if (dims == 4) return morton_code_of<4>(p);
+  if (dims == 3) return morton_code_of<3>(p);
+  return morton_code_of<2>(p);
 }
 
 }  // namespace tmnn_hip

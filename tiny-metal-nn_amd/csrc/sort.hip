@@ -21,6 +21,7 @@
 #include "sort.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.hpp"
 
@@ -64,13 +65,35 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum,
   return before + inc - v;
 }
 
-// key of chunk-local element li: the Morton code of the position (first
-// pass) or the previous pass's output
-template <bool FIRST>
-__device__ __forceinline__ uint32_t load_key(const uint32_t *keys, const float *pos, int dims,
-                                             size_t i) {
-  if constexpr (FIRST) return morton_code(pos + i * dims, dims);
-  return keys[i];
+// The keys of a thread's KPT elements at global indices gi[r] (each a valid
+// index): the Morton codes of the positions (first pass) or the previous
+// pass's output. Every load is issued before the first code is formed (the
+// uniform branch on dims sits outside the loads), so a thread waits for its
+// KPT loads once instead of once per key.
+template <bool FIRST, int KPT>
+__device__ __forceinline__ void load_keys(const uint32_t *keys, const float *pos, int dims,
+                                          const size_t (&gi)[KPT], uint32_t (&key)[KPT]) {
+  if constexpr (FIRST) {
+    auto codes = [&](auto dc) __attribute__((always_inline)) {
+      constexpr int D = decltype(dc)::value;
+      float p[KPT][D];
+#pragma unroll
+      for (int r = 0; r < KPT; ++r)
+#pragma unroll
+        for (int k = 0; k < D; ++k) p[r][k] = pos[gi[r] * D + k];
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) key[r] = morton_code_of<D>(p[r]);
+    };
+    if (dims == 4)
+      codes(std::integral_constant<int, 4>{});
+    else if (dims == 3)
+      codes(std::integral_constant<int, 3>{});
+    else
+      codes(std::integral_constant<int, 2>{});
+  } else {
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) key[r] = keys[gi[r]];
+  }
 }
 
 template <int RB, bool FIRST, int KPT>
@@ -84,14 +107,19 @@ __global__ void __launch_bounds__(kSortThreads)
   for (int j = 0; j < BPT; ++j) cnt[t + kSortThreads * j] = 0u;
   __syncthreads();
   const int base = blockIdx.x * chunk_keys(KPT);
+  size_t gi[KPT];
+  bool ok[KPT];
 #pragma unroll
   for (int r = 0; r < KPT; ++r) {
     const int i = base + r * kSortThreads + t;
-    if (i < n) {
-      const uint32_t key = load_key<FIRST>(keys, pos, dims, static_cast<size_t>(i));
-      atomicAdd(&cnt[(key >> shift) & (kBins - 1)], 1u);
-    }
+    ok[r] = i < n;
+    gi[r] = static_cast<size_t>(ok[r] ? i : 0);
   }
+  uint32_t key[KPT];
+  load_keys<FIRST, KPT>(keys, pos, dims, gi, key);
+#pragma unroll
+  for (int r = 0; r < KPT; ++r)
+    if (ok[r]) atomicAdd(&cnt[(key[r] >> shift) & (kBins - 1)], 1u);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
@@ -249,18 +277,23 @@ __global__ void __launch_bounds__(kSortThreads)
 
   // all loads are issued before the ranking
   uint32_t key[KPT], val[KPT], piw[KPT];
+  size_t gi[KPT];
 #pragma unroll
   for (int r = 0; r < KPT; ++r) {
     const int li = chunk_index<KPT>(r);
-    const bool valid = li < nblk;
-    const size_t gi = static_cast<size_t>(base + (valid ? li : 0));
+    gi[r] = static_cast<size_t>(base + (li < nblk ? li : 0));
+  }
+  load_keys<FIRST, KPT>(keys_in, pos, dims, gi, key);
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) {
+    const bool valid = chunk_index<KPT>(r) < nblk;
     if constexpr (FIRST) {
-      key[r] = valid ? load_key<true>(nullptr, pos, dims, gi) : 0u;
-      val[r] = static_cast<uint32_t>(gi);
+      val[r] = static_cast<uint32_t>(gi[r]);
     } else {
-      key[r] = valid ? keys_in[gi] : 0u;
-      val[r] = valid ? vals_in[gi] : 0u;
+      const uint32_t v = vals_in[gi[r]];
+      val[r] = valid ? v : 0u;
     }
+    key[r] = valid ? key[r] : 0u;
   }
   rank_in_waves(L, key, nblk, shift, piw);
   __syncthreads();
