@@ -54,6 +54,14 @@ LW_GEOMS = {
     "h98_2d": (2, dict(n_levels=8, n_features_per_level=2, log2_hashmap_size=12,
                        base_resolution=8.0, per_level_scale=1.5),
                dict(n_neurons=98, n_hidden_layers=2), 3, "fp32"),
+    # the output layer at the narrow kernels' limit (16 outputs) and one past
+    # it (17: the tile kernel)
+    "m16_h96_2d": (2, dict(n_levels=8, n_features_per_level=2, log2_hashmap_size=12,
+                           base_resolution=8.0, per_level_scale=1.5),
+                   dict(n_neurons=96, n_hidden_layers=1), 16, "fp32"),
+    "m17_h96_2d": (2, dict(n_levels=8, n_features_per_level=2, log2_hashmap_size=12,
+                           base_resolution=8.0, per_level_scale=1.5),
+                   dict(n_neurons=96, n_hidden_layers=1), 17, "fp32"),
 }
 
 
@@ -84,6 +92,30 @@ def test_tiled_plan_and_inference(oracle, name):
         a = tr.forward_for_training(pos)
         tol = 1e-5 * (np.abs(ref) + np.sqrt((ref.astype(np.float64) ** 2).mean()))
         assert np.all(np.abs(a - ref) <= tol)
+
+
+def test_tiled_inference_beyond_one_forward_chunk(oracle):
+    """A forward pass over more points than one layer-wise forward chunk
+    (2^18 points, two ping-pong activation buffers): the second chunk's
+    outputs land in the right rows (bit-identical to separate calls over the
+    same two ranges, which run the same kernels on the same points) and a
+    random sample matches the oracle within 1e-5."""
+    name = "in128_2d"
+    _say(f"tiled inference beyond one chunk {name}")
+    d = LW_GEOMS[name][0]
+    rng = np.random.default_rng(17)
+    n = (1 << 18) + 3001
+    with _trainer(name, hash_range=0.5) as tr:
+        pos = rng.random((n, d), dtype=np.float32)
+        out = tr.inference(pos)
+        first = tr.inference(pos[: 1 << 18])
+        rest = tr.inference(pos[1 << 18:])
+        assert np.array_equal(out, np.concatenate([first, rest]))
+        hw, mw = tr.get_weights()
+        idx = np.sort(rng.choice(n, 2048, replace=False))
+        ref = oracle.forward(omodel(oracle, tr), hw, mw, pos[idx])
+        tol = 1e-5 * (np.abs(ref) + np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        assert np.all(np.abs(out[idx] - ref) <= tol)
 
 
 @pytest.mark.parametrize("name", list(LW_GEOMS))
