@@ -91,15 +91,30 @@ __device__ __forceinline__ float lw_b(const LwGemmArgs &g, int k, int c) {
   return g.B[static_cast<size_t>(k) * g.ldb + c];
 }
 
-// LDS staging of one K step: row (or column) i of the tile holds its kLwK
-// operands contiguously (kLwKP floats per row: 16-byte aligned and padded),
-// so each lane reads the four K values of an MFMA A or B operand with one
-// ds_read_b128.
-constexpr int kLwKP = kLwK + 4;
+// LDS staging of one K step, laid out so that neither the stores nor the
+// MFMA operand reads meet a bank conflict (64 banks of 4 bytes). A k-fast
+// operand (A rows, X tiles, B read transposed: a quad is four consecutive K
+// of one row) sits row-major, [row][16], the four quads of a row permuted by
+// an XOR with (row / 4) % 4: the 16 lanes that store four rows' quads and
+// the 16 lanes that read one quad of 16 consecutive rows (ds_read_b128) each
+// cover the 64 banks once. A row-fast operand (A read by columns,
+// transposed X tiles, B in [K][C]: a quad is four consecutive rows at one
+// K) sits K-major, [16][kLwRS]: a quad is one 16-byte store, and a lane
+// reads its row's four K values with four scalar reads that, over the
+// wave, cover the 64 banks once each.
+constexpr int kLwRS = kLwTile + 4;         // row-fast K-major row stride (floats)
+constexpr int kLwOpFloats = kLwK * kLwRS;  // one operand's region (>= kLwTile * kLwK)
 // The output tile is staged through LDS for the epilogue (kLwCP floats per
 // row), so each thread stores 16 consecutive columns of one row.
 constexpr int kLwCP = kLwTile + 4;
-constexpr int kLwSmem = kLwTile * kLwCP > 2 * kLwTile * kLwKP ? kLwTile * kLwCP : 2 * kLwTile * kLwKP;
+constexpr int kLwSmem = kLwTile * kLwCP > 2 * kLwOpFloats ? kLwTile * kLwCP : 2 * kLwOpFloats;
+static_assert(kLwOpFloats >= kLwTile * kLwK, "operand region");
+
+// Float offset of quad kq (K values 4 kq .. 4 kq + 3) of row `row` of a
+// k-fast operand.
+__device__ __forceinline__ int lw_kfast_off(int row, int kq) {
+  return row * kLwK + 4 * (kq ^ ((row >> 2) & 3));
+}
 static_assert(kLwTile * kLwK == 256 * 4, "one four-element quad per thread and operand");
 
 // Whether A's and B's rows (of the layouts read with 16-byte loads: lda /
@@ -177,13 +192,23 @@ __device__ __forceinline__ f32x4 lw_load_b(const LwGemmArgs &g, int c0, int k0, 
   return v;
 }
 
-// Stores a quad into the LDS tile (row i's K values contiguous).
+// Stores a quad into an operand's LDS region (k-fast: row i, K kk .. kk +
+// 3; row-fast: rows i .. i + 3 at K kk).
 __device__ __forceinline__ void lw_stage(float *S, f32x4 v, bool kfast, int i, int kk) {
-  if (kfast) {
-    *reinterpret_cast<f32x4 *>(S + i * kLwKP + kk) = v;
+  if (kfast)
+    *reinterpret_cast<f32x4 *>(S + lw_kfast_off(i, kk >> 2)) = v;
+  else
+    *reinterpret_cast<f32x4 *>(S + kk * kLwRS + i) = v;
+}
+
+// The MFMA operand of lane p + 16 q for row `row`: K values 4 q .. 4 q + 3.
+template <bool KFAST>
+__device__ __forceinline__ f32x4 lw_frag(const float *S, int row, int q) {
+  if constexpr (KFAST) {
+    return *reinterpret_cast<const f32x4 *>(S + lw_kfast_off(row, q));
   } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) S[(i + e) * kLwKP + kk] = v[e];
+    return f32x4{S[(4 * q) * kLwRS + row], S[(4 * q + 1) * kLwRS + row], S[(4 * q + 2) * kLwRS + row],
+                 S[(4 * q + 3) * kLwRS + row]};
   }
 }
 
@@ -215,7 +240,8 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
   // the tile's A rows and B columns of the current K step, K innermost; after
   // the products the same memory holds the output tile
   __shared__ __align__(16) float smem[kLwSmem];
-  float *As = smem, *Bs = smem + kLwTile * kLwKP, *Cs = smem;
+  float *As = smem, *Bs = smem + kLwOpFloats, *Cs = smem;
+  constexpr bool kAKFast = AM == kLwARow || AM == kLwAXTiles, kBKFast = BT != 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int p = lane & 15, q = lane >> 4;
@@ -250,17 +276,15 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
       rb = lw_load_b<BT>(g, c0, k0 + kLwK, ke, bkf, bi, bk);
     }
     // v_mfma_f32_16x16x4_f32: lane p + 16 q supplies A[row p][k] and
-    // B[k][column p] of K slot q; the four MFMAs of a 16-wide K group take K
-    // values 16 h + 4 q + e (e = 0..3), one ds_read_b128 per operand tile
-#pragma unroll
-    for (int h = 0; h < kLwK / 16; ++h) {
+    // B[k][column p] of K slot q; the four MFMAs of the K step take K values
+    // 4 q + e (e = 0..3)
+    static_assert(kLwK == 16, "one 16-wide K group per step");
+    {
       f32x4 av[2], bv[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        av[i] = *reinterpret_cast<const f32x4 *>(As + (wr + 16 * i + p) * kLwKP + 16 * h + 4 * q);
+      for (int i = 0; i < 2; ++i) av[i] = lw_frag<kAKFast>(As, wr + 16 * i + p, q);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bv[j] = *reinterpret_cast<const f32x4 *>(Bs + (wc + 16 * j + p) * kLwKP + 16 * h + 4 * q);
+      for (int j = 0; j < 2; ++j) bv[j] = lw_frag<kBKFast>(Bs, wc + 16 * j + p, q);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -501,7 +525,7 @@ __global__ void __launch_bounds__(256) lw_narrow_mask_kernel(LwGemmArgs g) {
   __shared__ float As[kLwNarrowRows][kLwNarrow];
   const int c0 = blockIdx.y * 256, rb = blockIdx.x * kLwNarrowRows;
   for (int i = threadIdx.x; i < kLwNarrow * 256; i += 256) {
-    const int cc = i / kLwNarrow, k = i % kLwNarrow;  // k fastest: W's rows are contiguous
+    const int k = i / 256, cc = i % 256;  // columns fastest: conflict-free LDS stores
     Ws[k][cc] = (k < g.K && c0 + cc < g.C) ? g.B[static_cast<size_t>(c0 + cc) * g.ldb + k] : 0.0f;
   }
   for (int i = threadIdx.x; i < kLwNarrowRows * kLwNarrow; i += 256) {
