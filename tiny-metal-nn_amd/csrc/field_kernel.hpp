@@ -42,7 +42,11 @@ enum : int32_t {
 
 constexpr int kNT = 2;             // 16-point MFMA column tiles per wave tile
 constexpr int kTilePts = 16 * kNT; // points per wave tile
-constexpr int kPS = 40;            // LDS row stride (elements) of [unit][point]
+// LDS row stride (elements) of the [unit][point] staging arrays. fp32: 36
+// floats, so the D-layout stores (lanes 16q + p at rows 4q + r, column p) and
+// the dW operand reads (rows p, column 4ks + q) each hit 64 distinct banks;
+// fp16: 40 halves, keeping every row 16-byte aligned for the 8-half reads.
+__host__ __device__ constexpr int lds_pitch(bool f16) { return f16 ? 40 : 36; }
 constexpr int kMaxLayers = 9;      // up to 8 hidden layers + the output layer
 constexpr int kBlockThreads = 256;
 
@@ -95,7 +99,7 @@ struct FieldLayout {
   int32_t red_off;              // LDS bytes: fp32 per-wave reduction slots
   int32_t wave_off;             // LDS bytes: first wave's activation region
   int32_t wave_bytes;
-  int32_t xs_off, hs_off, ds_off;  // within a wave region
+  int32_t xs_off, hs_off, ds_off;  // within a wave region: X, hidden layers, output grad
   int32_t dw_global;            // 1: dW accumulates in the block's global partial row
   int32_t total;
 
@@ -159,9 +163,13 @@ __host__ __device__ __forceinline__ FieldLayout make_layout(int INP, int HP, int
   off = round_up(off, 16);
   s.wave_off = off;
   s.xs_off = 0;
-  s.hs_off = INP * kPS * s.es;
-  s.ds_off = s.hs_off + NHL * HP * kPS * s.es;
-  s.wave_bytes = train ? round_up(s.ds_off + HP * kPS * s.es, 16) : 0;
+  const int pitch = lds_pitch(f16) * s.es;
+  s.hs_off = INP * pitch;
+  s.ds_off = s.hs_off + NHL * HP * pitch;
+  // the delta region holds the output gradient's 16-row tile only: a hidden
+  // layer's delta is staged over that layer's activations (their ReLU mask is
+  // applied before the delta is stored)
+  s.wave_bytes = train ? round_up(s.ds_off + 16 * pitch, 16) : 0;
   off += wpb * s.wave_bytes;
   // Register-accumulated dW is reduced across the block's waves through LDS
   // at the end of the kernel, over the then idle weight/activation space.
@@ -329,16 +337,18 @@ __device__ __forceinline__ f32x4 dw_tile(const unsigned char *A, int row0,
                                          int p, int q,
                                          f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}) {
   if constexpr (F16) {
-    const half8 av = *reinterpret_cast<const half8 *>(A + ((row0 + p) * kPS + 8 * q) * 2);
-    const half8 bv = *reinterpret_cast<const half8 *>(B + ((col0 + p) * kPS + 8 * q) * 2);
+    constexpr int ps = lds_pitch(true);
+    const half8 av = *reinterpret_cast<const half8 *>(A + ((row0 + p) * ps + 8 * q) * 2);
+    const half8 bv = *reinterpret_cast<const half8 *>(B + ((col0 + p) * ps + 8 * q) * 2);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
   } else {
     const float *Af = reinterpret_cast<const float *>(A);
     const float *Bf = reinterpret_cast<const float *>(B);
+    constexpr int ps = lds_pitch(false);
 #pragma unroll
     for (int ks = 0; ks < kTilePts / 4; ++ks)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Af[(row0 + p) * kPS + 4 * ks + q],
-                                                 Bf[(col0 + p) * kPS + 4 * ks + q],
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Af[(row0 + p) * ps + 4 * ks + q],
+                                                 Bf[(col0 + p) * ps + 4 * ks + q],
                                                  acc, 0, 0, 0);
   }
   return acc;
@@ -355,7 +365,7 @@ __device__ __forceinline__ void store_tiles(unsigned char *dst,
     for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int idx = (16 * mt + 4 * q + r) * kPS + 16 * nt + p;
+        const int idx = (16 * mt + 4 * q + r) * lds_pitch(F16) + 16 * nt + p;
         if constexpr (F16)
           reinterpret_cast<_Float16 *>(dst)[idx] = static_cast<_Float16>(t[mt][nt][r]);
         else
@@ -374,7 +384,7 @@ __device__ __forceinline__ void relu_mask(f32x4 (&t)[MT][kNT],
     for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int idx = (16 * mt + 4 * q + r) * kPS + 16 * nt + p;
+        const int idx = (16 * mt + 4 * q + r) * lds_pitch(F16) + 16 * nt + p;
         float hv;
         if constexpr (F16)
           hv = static_cast<float>(reinterpret_cast<const _Float16 *>(h)[idx]);
@@ -1056,7 +1066,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
   unsigned char *Xs = wb + s.xs_off;
   unsigned char *Hs = wb + s.hs_off;
   unsigned char *Ds = wb + s.ds_off;
-  const int hs_layer_bytes = HP * kPS * es;
+  const int hs_layer_bytes = HP * lds_pitch(F16) * es;
   float lane_loss = 0.0f, lane_amax = 0.0f;
 
   DwRegs<HT, KT0, NHLT> R;
@@ -1281,8 +1291,10 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       auto hidden_bwd = [&](auto kc) {
         constexpr int KC = decltype(kc)::value;  // compile-time layer (REGDW) or 0
         const int k = KC > 0 ? KC : kc.runtime;
+        // layer k's activations are dead (dl is masked): dl takes their slot
+        unsigned char *Dk = Hs + k * hs_layer_bytes;
         wave_lds_sync();
-        store_tiles<F16, HT>(Ds, dl, p, q);
+        store_tiles<F16, HT>(Dk, dl, p, q);
         wave_lds_sync();
         const unsigned char *Hin = Hs + (k - 1) * hs_layer_bytes;
         if (!wgrads) {
@@ -1292,7 +1304,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 #pragma unroll
             for (int it = 0; it < HT; ++it)
               R.wh[KC - 1][mt][it] =
-                  dw_tile<F16>(Ds, 16 * mt, Hin, 16 * it, p, q, R.wh[KC - 1][mt][it]);
+                  dw_tile<F16>(Dk, 16 * mt, Hin, 16 * it, p, q, R.wh[KC - 1][mt][it]);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -1304,7 +1316,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
           for (int mt = 0; mt < HT; ++mt) {
 #pragma unroll
             for (int it = 0; it < HT; ++it) {
-              const f32x4 acc = dw_tile<F16>(Ds, 16 * mt, Hin, 16 * it, p, q);
+              const f32x4 acc = dw_tile<F16>(Dk, 16 * mt, Hin, 16 * it, p, q);
               const int i = 16 * it + p;
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
@@ -1338,8 +1350,9 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       }
 
       // ---- layer 0: dW0, db0, input-feature gradient, hash scatter
+      unsigned char *D0 = Hs;  // over layer 0's activations, as above
       wave_lds_sync();
-      store_tiles<F16, HT>(Ds, dl, p, q);
+      store_tiles<F16, HT>(D0, dl, p, q);
       wave_lds_sync();
       if (!wgrads) {
       } else if constexpr (REGDW) {
@@ -1347,7 +1360,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         for (int mt = 0; mt < HT; ++mt) {
 #pragma unroll
           for (int ft = 0; ft < KT0; ++ft)
-            R.w0[mt][ft] = dw_tile<F16>(Ds, 16 * mt, Xs, 16 * ft, p, q, R.w0[mt][ft]);
+            R.w0[mt][ft] = dw_tile<F16>(D0, 16 * mt, Xs, 16 * ft, p, q, R.w0[mt][ft]);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -1359,7 +1372,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         for (int mt = 0; mt < HT; ++mt) {
 #pragma unroll
           for (int ft = 0; ft < KT0; ++ft) {
-            const f32x4 acc = dw_tile<F16>(Ds, 16 * mt, Xs, 16 * ft, p, q);
+            const f32x4 acc = dw_tile<F16>(D0, 16 * mt, Xs, 16 * ft, p, q);
             const int f = 16 * ft + p;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
