@@ -42,11 +42,18 @@ enum : int32_t {
 
 constexpr int kNT = 2;             // 16-point MFMA column tiles per wave tile
 constexpr int kTilePts = 16 * kNT; // points per wave tile
-// LDS row stride (elements) of the [unit][point] staging arrays. fp32: 36
-// floats, so the D-layout stores (lanes 16q + p at rows 4q + r, column p) and
-// the dW operand reads (rows p, column 4ks + q) each hit 64 distinct banks;
-// fp16: 40 halves, keeping every row 16-byte aligned for the 8-half reads.
-__host__ __device__ constexpr int lds_pitch(bool f16) { return f16 ? 40 : 36; }
+// LDS row stride (elements) of the [unit][point] staging arrays. fp32: 32
+// floats, point index c of row `row` stored at c ^ stage_swz(row); fp16: 40
+// halves, rows 16-byte aligned for the 8-half dW operand reads.
+__host__ __device__ constexpr int lds_pitch(bool f16) { return f16 ? 40 : 32; }
+// fp32 point swizzle (a multiple of 4: 16-byte quads stay whole). The LDS
+// serves 4-byte accesses 32 lanes per cycle over 32 banks and 16-byte reads
+// 16 lanes per cycle over 64 banks (lane quads of even, then odd, bit parity
+// among lanes 0-31, then the same in 32-63). The D-layout stores and ReLU'
+// reads (lane p + 16 q: row 4 q + r, point 16 nt + p) and the dW operand
+// reads (lane p + 16 q: row p, points 8 q .. 8 q + 7 as two 16-byte reads)
+// then each meet every bank of a cycle once.
+__device__ __forceinline__ int stage_swz(int row) { return ((row << 1) & 4) | ((row << 2) & 16); }
 constexpr int kMaxLayers = 9;      // up to 8 hidden layers + the output layer
 constexpr int kBlockThreads = 256;
 
@@ -173,7 +180,8 @@ __host__ __device__ __forceinline__ FieldLayout make_layout(int INP, int HP, int
   off += wpb * s.wave_bytes;
   // Register-accumulated dW is reduced across the block's waves through LDS
   // at the end of the kernel, over the then idle weight/activation space.
-  if (train && reg_dw) off = off > mlp_count * 4 ? off : mlp_count * 4;
+  // (red_slot permutes within 64-float rows, so the array spans whole rows)
+  if (train && reg_dw) off = off > round_up(mlp_count, 64) * 4 ? off : round_up(mlp_count, 64) * 4;
   s.total = off;
   return s;
 }
@@ -342,14 +350,19 @@ __device__ __forceinline__ f32x4 dw_tile(const unsigned char *A, int row0,
     const half8 bv = *reinterpret_cast<const half8 *>(B + ((col0 + p) * ps + 8 * q) * 2);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
   } else {
-    const float *Af = reinterpret_cast<const float *>(A);
-    const float *Bf = reinterpret_cast<const float *>(B);
+    // K slot q of MFMA step 4 h + e takes point 8 q + 4 h + e (the same
+    // permutation of the 32 points in both operands)
     constexpr int ps = lds_pitch(false);
+    const float *Ar = reinterpret_cast<const float *>(A) + (row0 + p) * ps;
+    const float *Br = reinterpret_cast<const float *>(B) + (col0 + p) * ps;
+    const int sa = stage_swz(row0 + p), sb = stage_swz(col0 + p);
 #pragma unroll
-    for (int ks = 0; ks < kTilePts / 4; ++ks)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Af[(row0 + p) * ps + 4 * ks + q],
-                                                 Bf[(col0 + p) * ps + 4 * ks + q],
-                                                 acc, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 av = *reinterpret_cast<const f32x4 *>(Ar + ((8 * q + 4 * h) ^ sa));
+      const f32x4 bv = *reinterpret_cast<const f32x4 *>(Br + ((8 * q + 4 * h) ^ sb));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[e], acc, 0, 0, 0);
+    }
   }
   return acc;
 }
@@ -365,11 +378,12 @@ __device__ __forceinline__ void store_tiles(unsigned char *dst,
     for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int idx = (16 * mt + 4 * q + r) * lds_pitch(F16) + 16 * nt + p;
+        const int row = 16 * mt + 4 * q + r, pt = 16 * nt + p;
         if constexpr (F16)
-          reinterpret_cast<_Float16 *>(dst)[idx] = static_cast<_Float16>(t[mt][nt][r]);
+          reinterpret_cast<_Float16 *>(dst)[row * lds_pitch(true) + pt] =
+              static_cast<_Float16>(t[mt][nt][r]);
         else
-          reinterpret_cast<float *>(dst)[idx] = t[mt][nt][r];
+          reinterpret_cast<float *>(dst)[row * lds_pitch(false) + (pt ^ stage_swz(row))] = t[mt][nt][r];
       }
 }
 
@@ -384,12 +398,12 @@ __device__ __forceinline__ void relu_mask(f32x4 (&t)[MT][kNT],
     for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int idx = (16 * mt + 4 * q + r) * lds_pitch(F16) + 16 * nt + p;
+        const int row = 16 * mt + 4 * q + r, pt = 16 * nt + p;
         float hv;
         if constexpr (F16)
-          hv = static_cast<float>(reinterpret_cast<const _Float16 *>(h)[idx]);
+          hv = static_cast<float>(reinterpret_cast<const _Float16 *>(h)[row * lds_pitch(true) + pt]);
         else
-          hv = reinterpret_cast<const float *>(h)[idx];
+          hv = reinterpret_cast<const float *>(h)[row * lds_pitch(false) + (pt ^ stage_swz(row))];
         t[mt][nt][r] = hv > 0.0f ? t[mt][nt][r] : 0.0f;
       }
 }
@@ -973,10 +987,20 @@ struct DwRegs {
   float bo[4];
 };
 
+// LDS slot of parameter e in the block's reduction array: a bijection within
+// each 64-float row that XORs bits 6-7 of e into bits 0-1 and bits 8-9 into
+// bits 3-4. A dW tile's stores (lane p + 16 q: parameter row 16 t + p,
+// column 16 m + 4 q + r; rows 64 floats apart at H = 64) then meet 32
+// distinct banks in each half wave (unswizzled: 16 lanes per bank).
+__device__ __forceinline__ int red_slot(int e) {
+  return e ^ (((e >> 6) & 3) | (((e >> 8) & 3) << 3));
+}
+
 // red[idx] (+)= v over the block's waves in wave order: wave 0 stores, the
 // others add, one wave at a time (deterministic).
 __device__ __forceinline__ void red_put(float *red, int idx, float v, bool first) {
-  red[idx] = first ? v : red[idx] + v;
+  const int i = red_slot(idx);
+  red[i] = first ? v : red[i] + v;
 }
 
 template <int HT, int KT0, int NHLT>
@@ -1430,7 +1454,7 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         if (wave == w) dw_regs_to_lds<HT, KT0, NHLT>(R, a, s, red, p, q, w == 0, a.inv_loss_scale);
         __syncthreads();
       }
-      for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = red[e];
+      for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = red[red_slot(e)];
     } else if (!s.dw_global) {
       for (int e = threadIdx.x; e < a.mlp_count; e += blockDim.x) dst[e] = dw[e];
     }

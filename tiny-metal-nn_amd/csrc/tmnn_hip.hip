@@ -986,7 +986,7 @@ int launch_layerwise(tmnn_trainer *tr, KernelPlan &plan, FieldArgs a, int n,
       const int groups = (g.R + 15) / 16;
       const int blocks = std::min((groups + 3) / 4, 8 * tr->ctx->cu_count);
       const int kr = (g.K + kLwNarrowKStep - 1) / kLwNarrowKStep * kLwNarrowKStep;
-      const size_t lds = sizeof(float) * kLwNarrow * (kr + 4);
+      const size_t lds = sizeof(float) * kLwNarrow * kr;
       hipLaunchKernelGGL(lw_narrow_out_kernel, dim3(blocks), dim3(256), lds, st, g);
       TMNN_HIP_TRY(hipGetLastError());
       return TMNN_OK;
