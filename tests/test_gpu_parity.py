@@ -399,17 +399,23 @@ def _compact_2d(code3):
     return out
 
 
-@pytest.mark.parametrize("d,n", [(2, 1), (2, 2), (2, 1536), (2, 1537), (2, 2048), (2, 2049),
-                                 (2, 3073), (2, 4097), (2, 70000), (2, 1 << 18), (3, 12345),
-                                 (3, 1 << 20), (4, 9000), (4, 300001)])
-def test_morton_sort_matches_oracle_codes_and_stable_order(oracle, d, n):
+@pytest.mark.parametrize("d,n,span", [(2, 1, 1.0), (2, 2, 1.0), (2, 1536, 1.0), (2, 1537, 1.0),
+                                      (2, 2048, 1.0), (2, 2049, 1.0), (2, 3073, 1.0),
+                                      (2, 4097, 1.0), (2, 70000, 1.0), (2, 1 << 18, 1.0),
+                                      (2, 1 << 18, 0.5), (2, 1 << 18, 0.35), (3, 12345, 1.0),
+                                      (3, 1 << 20, 1.0), (4, 9000, 1.0), (4, 300001, 1.0)])
+def test_morton_sort_matches_oracle_codes_and_stable_order(oracle, d, n, span):
     """morton_sort.h: same codes as the oracle (the reference's quantisation),
-    and the permutation is the stable argsort of those codes."""
-    _say(f"morton sort d={d} n={n}")
+    and the permutation is the stable argsort of those codes. 2D sorts each
+    top-10-bit bucket in one block; positions in [0, span)^2 set the bucket
+    sizes: span 1 ~n/1024 per bucket (up to 512: ranked by comparison), 0.5
+    ~n/256 (513-1536: one chunk), 0.35 ~n/125 (several chunks), and the
+    quarter of the points tied at one position make one bucket of n/4."""
+    _say(f"morton sort d={d} n={n} span={span}")
     name = {2: "2d_f2", 3: "3d_f2", 4: "4d_f2"}[d]
     _, enc, net, m_out = GEOMS[name]
     rng = np.random.default_rng(n)
-    pos = rng.random((n, d), dtype=np.float32)
+    pos = rng.random((n, d), dtype=np.float32) * np.float32(span)
     pos[: n // 4] = pos[0]  # ties
     with make_trainer(d, m_out, enc, net, batch=1 << 20) as tr:
         codes, perm = tr.debug_morton_sort(pos)
