@@ -114,7 +114,10 @@ constexpr int kLwOpFloats = kLwK * kLwRS;  // one operand's region (>= kLwTile *
 // The output tile is staged through LDS for the epilogue (kLwCP floats per
 // row), so each thread stores 16 consecutive columns of one row.
 constexpr int kLwCP = kLwTile + 4;
-constexpr int kLwSmem = kLwTile * kLwCP > 2 * kLwOpFloats ? kLwTile * kLwCP : 2 * kLwOpFloats;
+// Two K steps (A and B regions each) are staged per pair of barriers.
+constexpr int kLwSteps = 2;
+constexpr int kLwSmem = kLwTile * kLwCP > 2 * kLwSteps * kLwOpFloats ? kLwTile * kLwCP
+                                                                     : 2 * kLwSteps * kLwOpFloats;
 static_assert(kLwOpFloats >= kLwTile * kLwK, "operand region");
 
 // Float offset of quad kq (K values 4 kq .. 4 kq + 3) of row `row` of a
@@ -247,7 +250,8 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
   // the tile's A rows and B columns of the current K step, K innermost; after
   // the products the same memory holds the output tile
   __shared__ __align__(16) float smem[kLwSmem];
-  float *As = smem, *Bs = smem + kLwOpFloats, *Cs = smem;
+  // step h of a staged pair: A at smem + 2 h kLwOpFloats, B right after it
+  float *Cs = smem;
   constexpr bool kAKFast = AM == kLwARow || AM == kLwAXTiles, kBKFast = BT != 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -263,30 +267,42 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Operand staging, software-pipelined: the next K step's quads are read
-  // from global memory into registers before the current step's products
-  // and stored to LDS after them.
+  // Operand staging, software-pipelined: the next pair of K steps' quads are
+  // read from global memory into registers before the current pair's
+  // products and stored to LDS after them (K past ke loads as zeros, so a
+  // pair's second step may be empty).
   bool akf, bkf;
   int ai, ak, bi, bk;
-  f32x4 ra, rb;
+  f32x4 ra[kLwSteps], rb[kLwSteps];
+  auto load_pair = [&](int k) {
+#pragma unroll
+    for (int h = 0; h < kLwSteps; ++h) {
+      ra[h] = lw_load_a<AM>(g, r0, k + h * kLwK, ke, akf, ai, ak);
+      rb[h] = lw_load_b<BT>(g, c0, k + h * kLwK, ke, bkf, bi, bk);
+    }
+  };
+  auto stage_pair = [&]() {
+#pragma unroll
+    for (int h = 0; h < kLwSteps; ++h) {
+      lw_stage(smem + 2 * h * kLwOpFloats, ra[h], akf, ai, ak);
+      lw_stage(smem + (2 * h + 1) * kLwOpFloats, rb[h], bkf, bi, bk);
+    }
+  };
   if (kb < ke) {
-    ra = lw_load_a<AM>(g, r0, kb, ke, akf, ai, ak);
-    rb = lw_load_b<BT>(g, c0, kb, ke, bkf, bi, bk);
-    lw_stage(As, ra, akf, ai, ak);
-    lw_stage(Bs, rb, bkf, bi, bk);
+    load_pair(kb);
+    stage_pair();
   }
   __syncthreads();
-  for (int k0 = kb; k0 < ke; k0 += kLwK) {
-    const bool more = k0 + kLwK < ke;  // uniform over the block
-    if (more) {
-      ra = lw_load_a<AM>(g, r0, k0 + kLwK, ke, akf, ai, ak);
-      rb = lw_load_b<BT>(g, c0, k0 + kLwK, ke, bkf, bi, bk);
-    }
+  for (int k0 = kb; k0 < ke; k0 += kLwSteps * kLwK) {
+    const bool more = k0 + kLwSteps * kLwK < ke;  // uniform over the block
+    if (more) load_pair(k0 + kLwSteps * kLwK);
     // v_mfma_f32_16x16x4_f32: lane p + 16 q supplies A[row p][k] and
-    // B[k][column p] of K slot q; the four MFMAs of the K step take K values
+    // B[k][column p] of K slot q; the four MFMAs of a K step take K values
     // 4 q + e (e = 0..3)
     static_assert(kLwK == 16, "one 16-wide K group per step");
-    {
+#pragma unroll
+    for (int h = 0; h < kLwSteps; ++h) {
+      const float *As = smem + 2 * h * kLwOpFloats, *Bs = As + kLwOpFloats;
       f32x4 av[2], bv[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) av[i] = lw_frag<kAKFast>(As, wr + 16 * i + p, q);
@@ -302,8 +318,7 @@ __global__ void __launch_bounds__(256) lw_gemm_kernel(LwGemmArgs g) {
     }
     __syncthreads();
     if (more) {
-      lw_stage(As, ra, akf, ai, ak);
-      lw_stage(Bs, rb, bkf, bi, bk);
+      stage_pair();
       __syncthreads();
     }
   }
