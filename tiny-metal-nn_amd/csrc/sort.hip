@@ -7,10 +7,11 @@
 // sorts each of the 1024 buckets by the low 10 bits in one block (one launch
 // instead of a second three-kernel pass). Three kernels per radix pass:
 //   hist   -- each block counts the digits of its 2048-key chunk (LDS atomics)
-//             into hist[digit][block]; the first pass computes the Morton
-//             codes from the positions itself;
-//   scan   -- one block per digit: exclusive prefix of the digit's counts over
-//             the blocks, and the digit total;
+//             into its row hist[block][digit] (one coalesced row store); the
+//             first pass computes the Morton codes from the positions itself;
+//   scan   -- 16 digits per block, 16 threads per digit, each over a
+//             contiguous run of blocks: exclusive prefix of every digit's
+//             counts over the blocks (pre[block][digit]), and the totals;
 //   scatter-- each block ranks its chunk stably: every wave ranks a
 //             contiguous quarter of it against its own LDS counters (wave
 //             ballots for the rank among equal digits, rounds in input
@@ -124,34 +125,63 @@ __global__ void __launch_bounds__(kSortThreads)
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
     const int d = t + kSortThreads * j;
-    hist[static_cast<size_t>(d) * blocks + blockIdx.x] = cnt[d];
+    hist[static_cast<size_t>(blockIdx.x) * kBins + d] = cnt[d];
   }
 }
 
-// Row d of hist (the G per-block counts of digit d, contiguous): exclusive
-// prefix over blocks into pre[d][*], the digit's total into totals[d].
-// One block per digit; thread t owns blocks [t*k, (t+1)*k).
+// Column d of hist (the G per-block counts of digit d, row stride bins):
+// exclusive prefix over the blocks into pre[*][d], the digit's total into
+// totals[d]. Block x takes digits 16 x .. 16 x + 15; thread t takes digit
+// 16 x + t % 16 and the blocks of segment t / 16, a contiguous sixteenth of
+// them: it sums its segment (16 loads in flight at a time, from clamped
+// addresses), the sixteen segment sums of its digit are scanned through
+// LDS, then it writes its segment's prefixes (a segment of at most 16
+// blocks, e.g. 2D at 2^18 points, from the registers of the first pass).
+constexpr int kScanDigits = 16, kScanSegs = kSortThreads / kScanDigits, kScanChunk = 16;
 __global__ void __launch_bounds__(kSortThreads)
-    radix_scan_kernel(const uint32_t *hist, int blocks, uint32_t *pre, uint32_t *totals) {
-  __shared__ uint32_t wsum[kSortWaves];
-  const int d = blockIdx.x;
+    radix_scan_kernel(const uint32_t *__restrict__ hist, int blocks, int bins,
+                      uint32_t *__restrict__ pre, uint32_t *__restrict__ totals) {
+  __shared__ uint32_t seg[kScanSegs][kScanDigits];
   const int t = threadIdx.x;
-  const int k = (blocks + kSortThreads - 1) / kSortThreads;
-  const uint32_t *row = hist + static_cast<size_t>(d) * blocks;
-  uint32_t *out = pre + static_cast<size_t>(d) * blocks;
-  const int lo = t * k;
-  uint32_t s = 0;
-  for (int i = 0; i < k; ++i)
-    if (lo + i < blocks) s += row[lo + i];
-  uint32_t total = 0;
-  uint32_t run = block_excl_scan(s, wsum, &total);
-  for (int i = 0; i < k; ++i)
-    if (lo + i < blocks) {
-      const uint32_t c = row[lo + i];
-      out[lo + i] = run;
-      run += c;
+  const int dl = t % kScanDigits, sg = t / kScanDigits;
+  const int d = blockIdx.x * kScanDigits + dl;
+  const int k = (blocks + kScanSegs - 1) / kScanSegs;
+  const int lo = sg * k, hi = std::min(blocks, lo + k);
+  uint32_t v[kScanChunk];
+  auto load_chunk = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < kScanChunk; ++j) {
+      const int b = c0 + j;
+      const uint32_t c = hist[static_cast<size_t>(std::min(b, hi - 1)) * bins + d];
+      v[j] = b < hi ? c : 0u;
     }
-  if (t == 0) totals[d] = total;
+  };
+  uint32_t s = 0;
+  for (int c0 = lo; c0 < hi; c0 += kScanChunk) {
+    load_chunk(c0);
+#pragma unroll
+    for (int j = 0; j < kScanChunk; ++j) s += v[j];
+  }
+  seg[sg][dl] = s;
+  __syncthreads();
+  uint32_t run = 0, total = 0;
+#pragma unroll
+  for (int j = 0; j < kScanSegs; ++j) {
+    const uint32_t c = seg[j][dl];
+    run += j < sg ? c : 0u;
+    total += c;
+  }
+  const bool one_chunk = hi - lo <= kScanChunk;  // v still holds the segment
+  for (int c0 = lo; c0 < hi; c0 += kScanChunk) {
+    if (!one_chunk) load_chunk(c0);
+#pragma unroll
+    for (int j = 0; j < kScanChunk; ++j) {
+      const int b = c0 + j;
+      if (b < hi) pre[static_cast<size_t>(b) * bins + d] = run;
+      run += v[j];
+    }
+  }
+  if (sg == 0) totals[d] = total;
 }
 
 // LDS of one chunk's stable ranking (radix_scatter_kernel, bucket_sort_kernel).
@@ -316,7 +346,7 @@ __global__ void __launch_bounds__(kSortThreads)
   for (int j = 0; j < BPT; ++j) {
     const int dd = t * BPT + j;
     L.lstart[dd] = lb;
-    L.glob[dd] = gb + pre[static_cast<size_t>(dd) * blocks + blockIdx.x] - lb;  // modulo 2^32
+    L.glob[dd] = gb + pre[static_cast<size_t>(blockIdx.x) * (1 << RB) + dd] - lb;  // modulo 2^32
     lb += cnt[j];
     gb += tot[j];
   }
@@ -437,8 +467,8 @@ hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const flo
       hipLaunchKernelGGL((radix_hist_kernel<RB, false, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
                          stream, kin, nullptr, dims, n, shift, blocks, hist);
     }
-    hipLaunchKernelGGL(radix_scan_kernel, dim3(1 << RB), dim3(kSortThreads), 0, stream, hist,
-                       blocks, pre, totals);
+    hipLaunchKernelGGL(radix_scan_kernel, dim3((1 << RB) / kScanDigits), dim3(kSortThreads), 0,
+                       stream, hist, blocks, 1 << RB, pre, totals);
     if (pass == 0) {
       hipLaunchKernelGGL((radix_scatter_kernel<RB, true, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
                          stream, nullptr, nullptr, pos, dims, n, shift, blocks, hist, pre, totals,
@@ -464,7 +494,7 @@ hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const flo
 }  // namespace
 
 hipError_t morton_sort_temp_bytes(int n, size_t *bytes) {
-  // hist[kBins][G] + pre[kBins][G] + totals[kBins] at the widest digit
+  // hist[G][kBins] + pre[G][kBins] + totals[kBins] at the widest digit
   const size_t bins = size_t(1) << 10;
   const int blocks = std::max(sort_blocks(n, kKeysPerThread), sort_blocks(n, kKeysPerThread2D));
   *bytes = (2 * bins * std::max(1, blocks) + bins) * sizeof(uint32_t);
@@ -495,8 +525,8 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
   constexpr int K2 = kKeysPerThread2D;
   hipLaunchKernelGGL((radix_hist_kernel<10, true, K2>), dim3(blocks), dim3(kSortThreads), 0,
                      stream, nullptr, pos, dims, n, 10, blocks, hist);
-  hipLaunchKernelGGL(radix_scan_kernel, dim3(1 << 10), dim3(kSortThreads), 0, stream, hist,
-                     blocks, pre, totals);
+  hipLaunchKernelGGL(radix_scan_kernel, dim3((1 << 10) / kScanDigits), dim3(kSortThreads), 0,
+                     stream, hist, blocks, 1 << 10, pre, totals);
   hipLaunchKernelGGL((radix_scatter_kernel<10, true, K2>), dim3(blocks), dim3(kSortThreads), 0,
                      stream, nullptr, nullptr, pos, dims, n, 10, blocks, hist, pre, totals, keys1,
                      vals1);
