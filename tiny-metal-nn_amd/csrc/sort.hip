@@ -294,7 +294,7 @@ __device__ __forceinline__ void write_chunk(const ChunkLds<RB, KPT> &L, int nblk
 template <int RB, bool FIRST, int KPT>
 __global__ void __launch_bounds__(kSortThreads)
     radix_scatter_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const float *pos,
-                         int dims, int n, int shift, int blocks, const uint32_t * /*hist*/,
+                         int dims, int n, int shift, int blocks, uint32_t *starts,
                          const uint32_t *pre, const uint32_t *totals, uint32_t *keys_out,
                          uint32_t *vals_out) {
   constexpr int BPT = (1 << RB) / kSortThreads;
@@ -347,6 +347,8 @@ __global__ void __launch_bounds__(kSortThreads)
     const int dd = t * BPT + j;
     L.lstart[dd] = lb;
     L.glob[dd] = gb + pre[static_cast<size_t>(blockIdx.x) * (1 << RB) + dd] - lb;  // modulo 2^32
+    // the digits' output starts, for a following bucket pass (nullable)
+    if (starts != nullptr && blockIdx.x == 0) starts[dd] = gb;
     lb += cnt[j];
     gb += tot[j];
   }
@@ -364,19 +366,15 @@ __global__ void __launch_bounds__(kSortThreads)
 // written at the running offsets of its digits (stable across chunks).
 template <int RB, int KPT>
 __global__ void __launch_bounds__(kSortThreads)
-    bucket_sort_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const uint32_t *totals,
-                       uint32_t *keys_out, uint32_t *vals_out) {
+    bucket_sort_kernel(const uint32_t *keys_in, const uint32_t *vals_in, const uint32_t *starts,
+                       const uint32_t *totals, uint32_t *keys_out, uint32_t *vals_out) {
   constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
   constexpr int kChunk = chunk_keys(KPT);
   __shared__ ChunkLds<RB, KPT> L;
   __shared__ uint32_t offs[kBins];  // running output offset of each digit in the bucket
   const int t = threadIdx.x;
   const int b = blockIdx.x;
-  // bucket start: the totals of the buckets before it
-  uint32_t s = 0;
-  for (int i = t; i < b; i += kSortThreads) s += totals[i];
-  uint32_t start = 0;
-  block_excl_scan(s, L.wsum, &start);
+  const uint32_t start = starts[b];  // written by the MSD pass's scatter
   const int size = static_cast<int>(totals[b]);
   if (size == 0) return;  // uniform
   const bool one_chunk = size <= kChunk;
@@ -471,11 +469,11 @@ hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const flo
                        stream, hist, blocks, 1 << RB, pre, totals);
     if (pass == 0) {
       hipLaunchKernelGGL((radix_scatter_kernel<RB, true, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
-                         stream, nullptr, nullptr, pos, dims, n, shift, blocks, hist, pre, totals,
+                         stream, nullptr, nullptr, pos, dims, n, shift, blocks, nullptr, pre, totals,
                          kout, vout);
     } else {
       hipLaunchKernelGGL((radix_scatter_kernel<RB, false, kKeysPerThread>), dim3(blocks), dim3(kSortThreads), 0,
-                         stream, kin, vin, nullptr, dims, n, shift, blocks, hist, pre, totals,
+                         stream, kin, vin, nullptr, dims, n, shift, blocks, nullptr, pre, totals,
                          kout, vout);
     }
     hipError_t e = hipGetLastError();
@@ -494,10 +492,11 @@ hipError_t run_passes(uint32_t *hist, uint32_t *pre, uint32_t *totals, const flo
 }  // namespace
 
 hipError_t morton_sort_temp_bytes(int n, size_t *bytes) {
-  // hist[G][kBins] + pre[G][kBins] + totals[kBins] at the widest digit
+  // hist[G][kBins] + pre[G][kBins] + totals[kBins] + starts[kBins] at the
+  // widest digit
   const size_t bins = size_t(1) << 10;
   const int blocks = std::max(sort_blocks(n, kKeysPerThread), sort_blocks(n, kKeysPerThread2D));
-  *bytes = (2 * bins * std::max(1, blocks) + bins) * sizeof(uint32_t);
+  *bytes = (2 * bins * std::max(1, blocks) + 2 * bins) * sizeof(uint32_t);
   return hipSuccess;
 }
 
@@ -517,6 +516,7 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
   uint32_t *hist = static_cast<uint32_t *>(tmp);
   uint32_t *pre = hist + bins * blocks;
   uint32_t *totals = pre + bins * blocks;
+  uint32_t *starts = totals + bins;
   if (digit_bits(end_bit) == 8)
     return run_passes<8>(hist, pre, totals, pos, dims, keys0, keys1, vals0, vals1, n, end_bit,
                          stream, keys_sorted, vals_sorted);
@@ -528,10 +528,10 @@ hipError_t morton_sort_batch(void *tmp, size_t tmp_bytes, const float *pos, int 
   hipLaunchKernelGGL(radix_scan_kernel, dim3((1 << 10) / kScanDigits), dim3(kSortThreads), 0,
                      stream, hist, blocks, 1 << 10, pre, totals);
   hipLaunchKernelGGL((radix_scatter_kernel<10, true, K2>), dim3(blocks), dim3(kSortThreads), 0,
-                     stream, nullptr, nullptr, pos, dims, n, 10, blocks, hist, pre, totals, keys1,
+                     stream, nullptr, nullptr, pos, dims, n, 10, blocks, starts, pre, totals, keys1,
                      vals1);
   hipLaunchKernelGGL((bucket_sort_kernel<10, K2>), dim3(1 << 10), dim3(kSortThreads), 0, stream,
-                     keys1, vals1, totals, keys0, vals0);
+                     keys1, vals1, starts, totals, keys0, vals0);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   *keys_sorted = keys0;
