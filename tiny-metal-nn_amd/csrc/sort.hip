@@ -104,9 +104,6 @@ __global__ void __launch_bounds__(kSortThreads)
   constexpr int kBins = 1 << RB, BPT = kBins / kSortThreads;
   __shared__ uint32_t cnt[kBins];
   const int t = threadIdx.x;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) cnt[t + kSortThreads * j] = 0u;
-  __syncthreads();
   const int base = blockIdx.x * chunk_keys(KPT);
   size_t gi[KPT];
   bool ok[KPT];
@@ -116,8 +113,12 @@ __global__ void __launch_bounds__(kSortThreads)
     ok[r] = i < n;
     gi[r] = static_cast<size_t>(ok[r] ? i : 0);
   }
+  // the keys are loaded (and coded) while the counters are cleared
   uint32_t key[KPT];
   load_keys<FIRST, KPT>(keys, pos, dims, gi, key);
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) cnt[t + kSortThreads * j] = 0u;
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < KPT; ++r)
     if (ok[r]) atomicAdd(&cnt[(key[r] >> shift) & (kBins - 1)], 1u);
@@ -302,10 +303,17 @@ __global__ void __launch_bounds__(kSortThreads)
   const int t = threadIdx.x;
   const int base = blockIdx.x * chunk_keys(KPT);
   const int nblk = std::min(chunk_keys(KPT), n - base);
+  // all loads are issued before the ranking: the owned digits' totals and
+  // this block's prefixes first (they do not depend on the keys)
+  uint32_t tot[BPT], pv[BPT];
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    tot[j] = totals[t * BPT + j];
+    pv[j] = pre[static_cast<size_t>(blockIdx.x) * (1 << RB) + t * BPT + j];
+  }
   clear_counts(L);
   __syncthreads();
 
-  // all loads are issued before the ranking
   uint32_t key[KPT], val[KPT], piw[KPT];
   size_t gi[KPT];
 #pragma unroll
@@ -331,11 +339,10 @@ __global__ void __launch_bounds__(kSortThreads)
   // the chunk's count of each owned digit, the run's start in the chunk and
   // its global slot (exclusive scan of the digit totals plus this block's
   // prefix in the digit)
-  uint32_t cnt[BPT], tot[BPT], sc = 0, st = 0;
+  uint32_t cnt[BPT], sc = 0, st = 0;
   wave_offsets(L, cnt);
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
-    tot[j] = totals[t * BPT + j];
     sc += cnt[j];
     st += tot[j];
   }
@@ -346,7 +353,7 @@ __global__ void __launch_bounds__(kSortThreads)
   for (int j = 0; j < BPT; ++j) {
     const int dd = t * BPT + j;
     L.lstart[dd] = lb;
-    L.glob[dd] = gb + pre[static_cast<size_t>(blockIdx.x) * (1 << RB) + dd] - lb;  // modulo 2^32
+    L.glob[dd] = gb + pv[j] - lb;  // modulo 2^32
     // the digits' output starts, for a following bucket pass (nullable)
     if (starts != nullptr && blockIdx.x == 0) starts[dd] = gb;
     lb += cnt[j];
