@@ -51,6 +51,7 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import statistics
 import os
 import sys
 import time
@@ -273,19 +274,22 @@ def kernel_rooflines(phase_us: dict, models: dict, names: dict, n: int, fused_sc
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
-def infer_roofline(prof: dict, gather_ref_us: float | None = None) -> dict | None:
+def infer_roofline(groups: list, gather_ref_us: float | None = None) -> dict | None:
     """C1 forward kernel (field_forward_kernel, fp32 MFMA, inline encode):
     algorithmic FLOPs 2 * (32*64 + 64*64 + 64*3) = 12,672 per point against
     the fp32 dense MFMA peak, and algorithmic bytes per point (position 8 B,
     4 corners x 16 levels x 2 features x 4 B of gathers, 12 B of outputs =
     532 B) against the HBM peak, per launch of 2^16 points over the sampled
-    calls' average kernel duration. `achievable`: the gather-only reference
-    kernel over the same unsorted 2^16 points (every corner of every level,
-    one thread per point), measured in the same run -- the time the kernel's
-    gathers alone take."""
-    if not prof.get("infer_calls"):
+    calls' kernel duration: the median over groups of calls of each group's
+    average (`groups`: the sampled-call profiles). `achievable`: the
+    gather-only reference kernel over the same unsorted 2^16 points (every
+    corner of every level, one thread per point), measured in the same run --
+    the time the kernel's gathers alone take."""
+    per = [g["gpu_infer_us"] / g["infer_calls"] for g in groups if g.get("infer_calls")]
+    if not per:
         return None
-    us = prof["gpu_infer_us"] / prof["infer_calls"]
+    us = statistics.median(per)
+    calls = sum(int(g["infer_calls"]) for g in groups if g.get("infer_calls"))
     flops = 2 * (32 * 64 + 64 * 64 + 64 * 3) * B_INFER
     bytes_ = (8 + 4 * 16 * 2 * 4 + 12) * B_INFER
     tf = flops / (us * 1e-6) / 1e12
@@ -295,7 +299,9 @@ def infer_roofline(prof: dict, gather_ref_us: float | None = None) -> dict | Non
             "traffic": None, "kernel": "field_forward_kernel<64, 32, false, 18>",
             "kernel_avg_us": round(us, 2), "work_per_launch": flops,
             "gather_GBps": round(gbs, 1), "gather_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
-            "sampled_calls": int(prof["infer_calls"]),
+            "sampled_calls": calls,
+            "statistic": f"median over {len(per)} groups of {calls // len(per)} calls of the group's "
+                         "average kernel duration (event pair around each kernel)",
             "achievable": None if gather_ref_us is None else {
                 "reference": "gather-only kernel over the same unsorted points",
                 "us": round(gather_ref_us, 2),
@@ -779,15 +785,17 @@ def main() -> int:
     tr.synchronize()
     torch.cuda.synchronize()
     infer_sps = B_INFER * iters / (time.perf_counter() - t2)
-    # five more calls with an event pair around the kernel
-    tr.set_training_step_profiling(True, 1)
+    # five groups of five more calls with an event pair around the kernel
+    igroups = []
     for _ in range(5):
-        tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
-    iprof = tr.training_step_profile()
-    tr.set_training_step_profiling(False)
+        tr.set_training_step_profiling(True, 1)
+        for _ in range(5):
+            tr.inference_device(xi.data_ptr(), yi.data_ptr(), B_INFER)
+        igroups.append(tr.training_step_profile())
+        tr.set_training_step_profiling(False)
     infer_gather = tr.debug_hash_rates(xi.data_ptr(), B_INFER, sorted=False, reps=20)["gather_us"]
     tr.close()
-    infer_roof = infer_roofline(iprof, infer_gather)
+    infer_roof = infer_roofline(igroups, infer_gather)
 
     fused = bool(ins.get("train_fused_scatter"))
     ph = median_phases(samples)
