@@ -6,8 +6,9 @@
 // 20-bit codes: one MSD pass on the top 10 bits, then bucket_sort_kernel
 // sorts each of the 1024 buckets by the low 10 bits in one block (one launch
 // instead of a second three-kernel pass). Three kernels per radix pass:
-//   hist   -- each block counts the digits of its 2048-key chunk (LDS atomics)
-//             into its row hist[block][digit] (one coalesced row store); the
+//   hist   -- each block counts the digits of its chunk (256 x KPT keys: 2048
+//             for 3D/4D, 1536 for 2D) with LDS atomics into its row
+//             hist[block][digit] (one coalesced row store); the
 //             first pass computes the Morton codes from the positions itself;
 //   scan   -- 16 digits per block, 16 threads per digit, each over a
 //             contiguous run of blocks: exclusive prefix of every digit's
@@ -17,7 +18,8 @@
 //             ballots for the rank among equal digits, rounds in input
 //             order), then a per-digit prefix over the waves; it sorts the
 //             chunk locally in LDS and writes it out digit run by digit run,
-//             so consecutive lanes store consecutive addresses.
+//             so consecutive lanes store consecutive addresses; the 2D MSD
+//             pass also writes each digit's output start for the buckets.
 // Ties keep input order (stable), so the sorted order is deterministic.
 #include "sort.hpp"
 
