@@ -1054,13 +1054,25 @@ __device__ __forceinline__ void dw_regs_to_lds(const DwRegs<HT, KT0, NHLT> &R, c
   }
 }
 
+// The hash-grid backward of one 32-point tile from its dx registers
+// (tile_scatter.hpp, which defines it): groups [GB, GE) of (K tile, level
+// pair), so a caller may spread a tile's backward over several places.
+template <int D, int F, int KT0, int GB = 0, int GE = 2 * KT0>
+__device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&dx)[KT0][kNT],
+                                             const float (&pos)[kNT][D], const bool (&valid)[kNT],
+                                             const float *res, int q);
+
 // The fused kernel body. Template parameters: padded hidden width HP and
 // input width INP (MFMA tiles), fp16 (split-fp16 forward, fp16 backward) or
 // fp32 MFMA, training or forward only, DF = D * 8 + F (0: runtime geometry),
 // NHLT = hidden-layer count (0: runtime count, dW accumulated in LDS;
 // > 0: dW accumulated in registers across tiles), XMEM: input features read
-// from a.xfeat (written by encode_features_kernel) instead of encoded here.
-template <int HP, int INP, bool F16, bool TRAIN, int DF, int NHLT, bool XMEM = false>
+// from a.xfeat (written by encode_features_kernel) instead of encoded here,
+// SD, SF > 0: the training modes run each tile's hash-grid backward
+// (tile_scatter, a D = SD, F = SF grid, positions from a.spos) instead of
+// storing dx.
+template <int HP, int INP, bool F16, bool TRAIN, int DF, int NHLT, bool XMEM = false, int SD = 0,
+          int SF = 0>
 __device__ __forceinline__ void field_body(const FieldArgs &a) {
   constexpr int HT = HP / 16;
   constexpr int KT0 = INP / 16;
@@ -1181,6 +1193,17 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
         encode_tile<KT0, DF>(a, res, q, P, X);
       // prefetch: the next tile's positions
       load_pos(next, Pn);
+    }
+    // this tile's sorted positions, for the fused hash-grid backward
+    constexpr int kSP = SD > 0 ? SD : 1;
+    float Ps[kNT][kSP];
+    if constexpr (SD > 0) {
+      const bool scat = a.mode != kModeInputGrad;  // uniform
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+        for (int k = 0; k < SD; ++k)
+          Ps[nt][k] = (scat && valid[nt]) ? a.spos[static_cast<size_t>(pt[nt]) * SD + k] : 0.0f;
     }
     // this tile's targets / d_out
     float Tv[kNT][4];
@@ -1417,6 +1440,12 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
       }
       f32x4 dx[KT0][kNT];
       layer_mma<F16, HT, KT0>(smem + s.bwd_off(0), dl, dx, lane);
+      if constexpr (SD > 0) {
+        if (a.mode != kModeInputGrad) {  // uniform
+          tile_scatter<SD, SF, KT0>(a, dx, Ps, valid, res, q);
+          continue;
+        }
+      }
       // dx (D layout: feature 16*kt + 4*q + r of point 16*nt + p) -> [n][IN]
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) {
@@ -1464,10 +1493,10 @@ __device__ __forceinline__ void field_body(const FieldArgs &a) {
 // Training launches are LDS-bound to one 4-wave block per CU (one wave per
 // SIMD), so they may use the whole register file. Their input features come
 // from encode_features_kernel (XMEM).
-template <int HP, int INP, bool F16, int NHLT>
+template <int HP, int INP, bool F16, int NHLT, int SD = 0, int SF = 0>
 __global__ void __launch_bounds__(kBlockThreads)
     __attribute__((amdgpu_waves_per_eu(1, 1))) field_train_kernel(FieldArgs a) {
-  field_body<HP, INP, F16, true, 0, NHLT, true>(a);
+  field_body<HP, INP, F16, true, 0, NHLT, true, SD, SF>(a);
 }
 
 // Forward only (inference, the fp16 forward of the split training API),

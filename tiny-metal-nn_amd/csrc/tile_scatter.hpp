@@ -40,7 +40,7 @@ __host__ __device__ constexpr bool tile_scatter_shape(int D, int F) {
 // GB, GE: the (K tile, pair) groups [GB, GE) of dx this call covers (group
 // 2 kt + h: levels 8 kt + 2 q + h), so a caller can spread one tile's
 // backward over several places.
-template <int D, int F, int KT0, int GB = 0, int GE = 2 * KT0>
+template <int D, int F, int KT0, int GB, int GE>  // defaults: field_kernel.hpp
 __device__ __forceinline__ void tile_scatter(const FieldArgs &a, const f32x4 (&dx)[KT0][kNT],
                                              const float (&pos)[kNT][D], const bool (&valid)[kNT],
                                              const float *res, int q) {

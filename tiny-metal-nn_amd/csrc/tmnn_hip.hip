@@ -172,6 +172,18 @@ KernelChoice select_kernel(int HP, int INP, bool f16, bool train, int D, int F, 
   if (fused && train && f16 && HP == 64 && INP == 64 && NHL == 3)
     return {mlp_train_kernel<64, 64, 3>, true, false, true, true};
   if (fused && train) {
+    // fp32 training of the 64-wide shapes on cache-sized tables: the field
+    // kernel runs each tile's hash-grid backward itself (tile_scatter.hpp)
+    if (!f16 && HP == 64 && INP == 32 && small_table && tile_scatter_shape(D, F)) {
+      if (NHL == 2)
+        return {D == 2 ? field_train_kernel<64, 32, false, 2, 2, 2>
+                       : field_train_kernel<64, 32, false, 2, 3, 2>,
+                true, false, true, false, false, true};
+      if (NHL == 1)
+        return {D == 2 ? field_train_kernel<64, 32, false, 1, 2, 2>
+                       : field_train_kernel<64, 32, false, 1, 3, 2>,
+                true, false, true, false, false, true};
+    }
 // fp32 training of the BASELINE shapes (fp16 took the kernels above)
 #define TMNN_TRAIN_SPEC(hp, inp, nhl)                                              \
   if (!f16 && HP == hp && INP == inp && NHL == nhl)                                \
