@@ -229,6 +229,7 @@ def kernel_rooflines(phase_us: dict, models: dict, names: dict, n: int, fused_sc
             if fp32:  # the fp32 training kernels: no LDS model, fp32 MFMA peak
                 r.update({"bound": "mfma", "achieved": mfma["achieved"], "peak": mfma_peak,
                           "unit": "TFLOP/s", "frac": mfma["frac"]})
+                r["roofline_us"] = round(t_mfma, 2)
             else:
                 lb = lds_bytes_per_launch(names[key], n, *mlp_shape)
                 t_lds = lb / (lds_peak_gbs * 1e9) * 1e6
@@ -425,7 +426,8 @@ def _config(d, levels, feats, log2t, base, scale, hidden, nhl, loss, n, precisio
 
 def mlp_kernel_name(which: str, fused: bool, precision: str) -> str:
     if precision == "fp32":
-        return {"c2": "field_train_kernel<64, 32, false, 2>"}.get(which, "field_train_kernel")
+        return {"c2": "field_train_kernel<64, 32, false, 2, 2, 2>" if fused else
+                      "field_train_kernel<64, 32, false, 2, 0, 0>"}.get(which, "field_train_kernel")
     return {"c2": "mlp_train_kernel<64, 32, 2, 8, 2, 2>" if fused else
                   "mlp_train_kernel<64, 32, 2, 8, 0, 0>",
             "c3": "mlp_train_kernel<64, 32, 1, 8, 3, 2>" if fused else
