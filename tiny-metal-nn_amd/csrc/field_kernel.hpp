@@ -731,6 +731,26 @@ __global__ void pack_image_kernel(PackArgs a) {
   }
 }
 
+// Block-wide copy of `bytes` (a multiple of 16) from global memory into LDS.
+// Whole 1 KB chunks go by direct global-to-LDS loads (global_load_lds_dwordx4:
+// lane i's 16 bytes land at the wave-uniform LDS base + 16 i), which need no
+// registers and keep every chunk of the copy in flight at once; the rest goes
+// through registers. Returns once this thread's part has landed; the caller's
+// barrier publishes the copy to the block.
+__device__ __forceinline__ void copy_to_lds(unsigned char *dst, const unsigned char *src,
+                                            int bytes) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int chunks = bytes >> 10;
+  for (int c = wave; c < chunks; c += nw)
+    __builtin_amdgcn_global_load_lds(src + (c << 10) + lane * 16,
+                                     (__attribute__((address_space(3))) void *)(dst + (c << 10)),
+                                     16, 0, 0);
+  const uint4 *s = reinterpret_cast<const uint4 *>(src);
+  uint4 *d = reinterpret_cast<uint4 *>(dst);
+  for (int e = (chunks << 6) + threadIdx.x; e < bytes / 16; e += blockDim.x) d[e] = s[e];
+  __builtin_amdgcn_s_waitcnt(0);  // the direct loads (vmcnt) and the stores have completed
+}
+
 // Block-wide copy of the packed image into LDS (+ zeroing of an LDS or
 // global dW accumulator for the generic kernels).
 template <bool TRAIN, bool REGDW>
@@ -738,11 +758,7 @@ __device__ __forceinline__ void stage_weights(const FieldArgs &a, const FieldLay
                                               unsigned char *smem) {
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
-  const int n16 = s.dw_off / 16;
-  const uint4 *src = reinterpret_cast<const uint4 *>(a.image);
-  uint4 *dst = reinterpret_cast<uint4 *>(smem);
-#pragma unroll 4
-  for (int e = tid; e < n16; e += nthr) dst[e] = src[e];
+  copy_to_lds(smem, a.image, s.dw_off);
   if constexpr (TRAIN && !REGDW) {
     if (s.dw_global) {
       float *dwg = a.grad_partials + static_cast<size_t>(blockIdx.x) * a.mlp_count;
