@@ -65,3 +65,34 @@ def test_random_shape_inference_and_step_loss(oracle, idx):
         lo = oracle.training_step(omodel(oracle, tr), oracle.adam(1e-2, 1e-2), 0, params, m1, m2,
                                   pos, tgt)
         assert lg == pytest.approx(lo, rel=1e-5 if prec == "fp32" else 3e-3), (lg, lo)
+
+
+STEP_SHAPES = _shapes(7027, 8)
+
+
+@pytest.mark.parametrize("idx", range(len(STEP_SHAPES)))
+def test_random_shape_three_steps_track_oracle(oracle, idx):
+    """Three fused training steps (Adam in between) on random shapes: each
+    step's loss against the oracle's step on the same batch and state, within
+    1e-4 (fp32) or 1e-2 (fp16) relative."""
+    d, L, F, log2T, base, scale, H, NHL, M, prec, loss, n = STEP_SHAPES[idx]
+    n = max(n, 33)
+    print(f"steps {idx}: d{d} L{L} F{F} T2^{log2T} H{H}x{NHL} M{M} {prec} {loss} n{n}", flush=True)
+    sys.stdout.flush()
+    enc = dict(n_levels=L, n_features_per_level=F, log2_hashmap_size=log2T,
+               base_resolution=base, per_level_scale=scale)
+    net = dict(n_neurons=H, n_hidden_layers=NHL)
+    prng = np.random.default_rng(100 + idx)
+    with make_trainer(d, M, enc, net, loss=loss, precision=prec, batch=max(n, 1024),
+                      hash_range=0.5) as tr:
+        hw, mw = tr.get_weights()
+        m = omodel(oracle, tr)
+        a = oracle.adam(1e-2, 1e-2)
+        params = np.concatenate([hw, mw])
+        m1, m2 = np.zeros_like(params), np.zeros_like(params)
+        for step in range(3):
+            pos = prng.random((n, d), dtype=np.float32)
+            tgt = prng.random((n, M), dtype=np.float32)
+            lg = tr.training_step(pos, tgt)
+            lo = oracle.training_step(m, a, step, params, m1, m2, pos, tgt)
+            assert lg == pytest.approx(lo, rel=1e-4 if prec == "fp32" else 1e-2), (step, lg, lo)
